@@ -1,0 +1,201 @@
+/*
+ * moc_amd.h - C ABI of the MI355X (gfx950) MoC sparse SwiGLU FFN library.
+ *
+ * libmoc_amd.so exports exactly the functions declared here.  All of them
+ * take raw device pointers, element counts and element strides; `stream` is
+ * a hipStream_t passed as void* (NULL = the default stream).  Nothing here
+ * allocates device memory: callers own every buffer (outputs and workspaces),
+ * so any sequence of calls may be recorded into a HIP graph.  No function
+ * throws; each returns MOC_OK or a negative status, and moc_last_error()
+ * describes the last failure on the calling thread.
+ *
+ * Selection rule used everywhere: values ordered descending, ties broken
+ * toward the lower channel index, -0.0 == +0.0, NaN ranks above +inf.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (paths relative to the xiaohuangji/MoC repository).
+ */
+#ifndef MOC_AMD_H_
+#define MOC_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOC_ABI_VERSION 1
+
+/* status codes */
+#define MOC_OK 0
+#define MOC_ERR_INVALID (-1) /* bad argument: shape, dtype, stride, alignment */
+#define MOC_ERR_HIP (-2)     /* HIP runtime / launch failure */
+
+/* element types */
+#define MOC_BF16 0
+#define MOC_F32 1
+
+/* index types */
+#define MOC_I16 0
+#define MOC_I32 1
+#define MOC_I64 2
+
+/* ------------------------------------------------------------------ misc */
+const char* moc_last_error(void);
+int moc_abi_version(void);
+
+/* Zero `bytes` bytes at 16-byte aligned `dst` with a fill kernel (graph-safe
+ * replacement for the reference's `tensor.zero_()` before scatters,
+ * moc/training/triton_sparse_aux.py:212-213,277-278,345-346,404-405). */
+int moc_fill_zero(void* dst, int64_t bytes, void* stream);
+
+/* dst[r, c] = src[r, c] for c < cols, 0 for cols <= c < dst_cols.  Builds the
+ * padded, 16-byte aligned copies the MFMA GEMM reads (no reference
+ * counterpart beyond the contiguous copy of moc/inference/inference_ffn.py:109). */
+int moc_copy_pad_2d(int dtype, const void* src, int64_t rows, int64_t cols, int64_t src_ld,
+                    void* dst, int64_t dst_ld, int64_t dst_cols, void* stream);
+
+/* ------------------------------------------------------------- selection */
+/* Row-wise Top-K of scores[rows, inter] (leading dimension ld).
+ * Replaces torch.topk(g, k, dim=-1, largest=True, sorted=False) at
+ * moc/ffn.py:144,392 and moc/inference/inference_ffn.py:147-153, and the CUB
+ * kernels behind moc_native::optimized_global_topk_bf16
+ * (moc/inference/cuda/optimized_global_moc_ext.cu:39-125,376-398;
+ * optimized_global_moc_ext.cpp:25-33,89).
+ * Writes idx_out[rows, k] (MOC_I16/I32/I64) in ascending channel order,
+ * optionally vals_out[rows, k] (scores at idx, same dtype) and a bitmask
+ * mask_out[rows, mask_ld] of uint32 words (bit c%32 of word c/32 = channel
+ * c selected).  score_transform 1 ranks by |SiLU(score)| rounded to the
+ * score dtype (moc/ffn.py:335-338) while vals keep the raw scores.
+ * Limits: 1 <= k <= inter <= 16384. */
+int moc_topk_rows(int dtype, const void* scores, int64_t rows, int64_t inter, int64_t ld,
+                  int64_t k, int score_transform, void* vals_out, void* idx_out, int idx_dtype,
+                  uint32_t* mask_out, int64_t mask_ld, void* stream);
+
+/* K' of the 2:8 structure: 2*floor(inter/8) + min(2, inter%8)
+ * (moc/ffn.py:62-65). */
+int64_t moc_moc28_effective_k(int64_t inter);
+
+/* Top-2 of each aligned group of 8 channels, top-min(2, tail) of a trailing
+ * partial group (moc/ffn.py:68-108).  idx_out/vals_out are [rows, K'] with
+ * (top-1, top-2) per group. */
+int moc_select_2of8(int dtype, const void* scores, int64_t rows, int64_t inter, int64_t ld,
+                    void* vals_out, void* idx_out, int idx_dtype, void* stream);
+
+/* ------------------------------------------------------- training helpers */
+/* u_s = U[r, idx], s_s = SiLU(vals), z_s = s_s * u_s, z_full[r, idx] = z_s
+ * with z_full zero-filled first (moc/training/triton_sparse_aux.py:197-231,
+ * kernel :17-49; bf16 rounds s, then z).  Any output may be NULL. */
+int moc_sparse_forward_aux(int dtype, const void* topk_vals, const void* idx, int idx_dtype,
+                           const void* u_full, int64_t u_ld, int64_t rows, int64_t k,
+                           int64_t inter, void* u_sparse, void* s_sparse, void* z_sparse,
+                           void* z_full, int64_t z_ld, void* stream);
+
+/* dense (zero-filled) [rows, ld] <- sparse [rows, k] at idx
+ * (moc/training/triton_sparse_aux.py:266-290, kernel :71-87). */
+int moc_scatter_sparse_to_dense(int dtype, const void* sparse, const void* idx, int idx_dtype,
+                                int64_t rows, int64_t k, int64_t inter, void* dense, int64_t ld,
+                                void* stream);
+
+/* sparse [rows, k] <- dense [rows, ld] at idx
+ * (moc/training/triton_sparse_aux.py:234-263, kernel :52-68). */
+int moc_gather_dense_to_sparse(int dtype, const void* dense, int64_t ld, const void* idx,
+                               int idx_dtype, int64_t rows, int64_t k, void* sparse,
+                               void* stream);
+
+/* GCP recompute s = SiLU(g_s), z = s * u_s over n entries
+ * (_MoCGCPFunction.backward, moc/ffn.py:435-436).  Outputs may be NULL. */
+int moc_gcp_recompute(int dtype, const void* g_sparse, const void* u_sparse, int64_t n,
+                      void* s_sparse, void* z_sparse, void* stream);
+
+/* grad_g, grad_u dense [rows, out_ld] (zero-filled) from grad_z_full at idx:
+ * grad_u = s*gz, grad_g = u*gz*SiLU'(g) (moc/training/triton_sparse_aux.py:
+ * 363-423; bf16 follows the materialised-bf16 chain at :376-400, f32 the fused
+ * kernel :139-182).  s_sparse may be NULL: s is then recomputed from g
+ * (GCP, moc/ffn.py:435). */
+int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype, const void* g_sparse,
+                            const void* u_sparse, const void* s_sparse, const void* gz_full,
+                            int64_t gz_ld, int64_t rows, int64_t k, int64_t inter, void* grad_g,
+                            void* grad_u, int64_t out_ld, void* stream);
+
+/* ------------------------------------------------------------------ GEMM */
+/* C[M,N] (row-major, ldc) = sum_k A(m,k) B(k,n) [+ sum_k A2(m,k) B2(k,n)],
+ * A(m,k) = A[m*a_sm + k*a_sk], B(k,n) = B[k*b_sk + n*b_sn].  Each operand
+ * needs a unit stride along K or along M/N; the second pair (K2 > 0, A2 set)
+ * must share the first pair's layouts.  bf16 operands: 16-byte aligned, the
+ * non-unit stride a multiple of 8; f32 accumulation; c_dtype bf16 or f32.
+ * f32 operands: any strides, f32 output.
+ * Replaces the torch GEMMs of the FFN (moc/ffn.py:141,146,163,203-254,389,394,
+ * 414,447-494) and the dense gate/up/down projections of
+ * moc/inference/inference_ffn.py:166,171-179. */
+int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+             int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2, const void* A2,
+             int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn, void* C,
+             int64_t ldc, int c_dtype, void* stream);
+
+/* ---------------------------------------------------------------- decode */
+/* y[b, r] = bf16(sum_h x[b,h] W[r,h]) for b < nb <= 16 tokens: the decode
+ * gate projection (module.gate_proj(x) before
+ * moc_native::optimized_global_after_gate_bf16,
+ * moc/inference/inference_ffn.py:188, benchmark_ffn_latency.py:130).
+ * bf16 only; x, W 16-byte aligned with ldx, ldw multiples of 8. */
+int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void* W, int64_t ldw,
+                  int64_t rows, int64_t hidden, void* y, int64_t ldy, void* stream);
+
+/* z[b,k] = bf16(bf16(SiLU(vals[b,k])) * bf16(x[b] . W_up[idx[b,k]]))
+ * (moc_native::optimized_global_selected_up_silu_bf16,
+ * optimized_global_moc_ext.cu:127-162,400-427; rounding points of
+ * masked_reference, moc/inference/inference_ffn.py:171-175).  bf16 only. */
+int moc_selected_up_silu_bf16(const void* x, int64_t nb, int64_t hidden, const void* topk_vals,
+                              const void* idx, int idx_dtype, int64_t k, const void* w_up,
+                              int64_t inter, void* z, void* stream);
+
+/* Workspace bytes moc_selected_down_bf16 needs for (nb, k, hidden). */
+int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64_t hidden);
+
+/* y[b,h] = bf16(sum_k z[b,k] W_down_t[idx[b,k], h]), split over k with a
+ * fixed-order f32 reduction (moc_native::optimized_global_selected_down_bf16,
+ * optimized_global_moc_ext.cu:247-372,429-455; moc::selected_grouped_down,
+ * moc/inference/triton_fused_ffn_kernels.py:228-267). */
+int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
+                           const void* w_down_t, int64_t inter, int64_t hidden, void* y,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes moc_global_after_gate_bf16 needs. */
+int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t k,
+                                             int64_t hidden);
+
+/* Global-MoC decode after the gate: Top-K of gate_scores[nb, inter], selected
+ * Up * SiLU, selected Down -> y[nb, hidden]
+ * (moc_native::optimized_global_after_gate_bf16, optimized_global_moc_ext.cu:
+ * 457-540, optimized_global_moc_ext.cpp:61-76,92). */
+int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
+                               int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
+                               void* y, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------- 2:8 */
+/* Fused gate+up projection with top-2-of-8 selection for nb tokens:
+ * idx[b, 2g+j] (int64), sz[b, 2g+j] = bf16(SiLU(g)*u) with g, u the bf16
+ * projections of the selected channel (moc::fused_grouped_top2_up_silu,
+ * moc/inference/triton_grouped_moc_ops.py:26-78; kernel
+ * triton_fused_ffn_kernels.py:29-156).  inter % 8 == 0; bf16 only. */
+int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
+                                  const void* w_up, int64_t inter, void* idx, void* sz,
+                                  void* stream);
+
+/* Workspace bytes moc_selected_grouped_down_bf16 needs. */
+int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t inter,
+                                                 int64_t hidden);
+
+/* y[b,h] = bf16(sum_k sz[b,k] W_down_t[idx[b,k], h]) for the 2:8 layout
+ * (moc::selected_grouped_down, triton_grouped_moc_ops.py:96-131; kernel
+ * triton_fused_ffn_kernels.py:228-267). */
+int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb, int64_t k,
+                                   const void* w_down_t, int64_t inter, int64_t hidden, void* y,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOC_AMD_H_ */

@@ -1,0 +1,31 @@
+// Internal helpers shared by the C-ABI entry points: argument checks that
+// record a message instead of throwing, and the launch check.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+
+#include "../../include/moc_amd.h"
+
+namespace moc {
+
+// Records a printf-style message retrievable through moc_last_error().
+void set_error(const char* fmt, ...);
+
+// After a launch: turns a pending HIP error into MOC_ERR_HIP with a message.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace moc
+
+#define MOC_REQUIRE(cond, ...)        \
+  do {                                \
+    if (!(cond)) {                    \
+      ::moc::set_error(__VA_ARGS__);  \
+      return MOC_ERR_INVALID;         \
+    }                                 \
+  } while (0)

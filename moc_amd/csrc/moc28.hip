@@ -1,0 +1,335 @@
+// MoC 2:8 inference kernels (gfx950): every aligned group of 8 channels keeps
+// its two largest gate values.
+//
+//  moc_grouped_top2_up_silu_bf16  fused gate+up projection + top-2-of-8 +
+//      SiLU(g)*u, writing only idx[nb, K'] and sz[nb, K'].  Replaces
+//      moc::fused_grouped_top2_up_silu (moc/inference/triton_grouped_moc_ops.py:
+//      26-78; kernel moc/inference/triton_fused_ffn_kernels.py:29-156).
+//      Semantics kept from that kernel: G and U accumulate in f32 and are
+//      rounded to bf16 before selection (:95-97,117-118); top-1 is the max
+//      with the lowest index among equal maxima, top-2 the max of the other
+//      seven under the same rule (:103-114); sz = (g*sigmoid(g))*u in f32,
+//      stored bf16 (:126-129); idx int64 ordered (top-1, top-2) per group.
+//      nb <= 16: a workgroup owns 16 channels (two groups) and all tokens,
+//      G/U through MFMA 16x16x32 with the waves splitting the hidden dim.
+//      nb  > 16: a 128-token x 64-channel MFMA GEMM tile computes G and U
+//      side by side (B tile = 64 W_gate rows + the same 64 W_up rows); the
+//      epilogue stages bf16 G/U in LDS and selects per (token, group).
+//  moc_selected_grouped_down_bf16  y = sz * W_down^T[idx] (moc::selected_grouped_down,
+//      triton_grouped_moc_ops.py:96-131, kernel triton_fused_ffn_kernels.py:228-267).
+//      nb <= 64: split-K gathered GEMV; nb > 64: sz is scattered into a dense
+//      zero-filled [nb, inter] tile and multiplied on MFMA (dense-equivalent
+//      work: 4x the compacted FLOPs).
+#include "abi.h"
+#include "common.h"
+#include "gemm_tile.h"
+
+extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
+                                      int64_t k, const void* w_down_t, int64_t inter,
+                                      int64_t hidden, void* y, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
+extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64_t hidden);
+extern "C" int moc_scatter_sparse_to_dense(int dtype, const void* sparse, const void* idx,
+                                           int idx_dtype, int64_t rows, int64_t k, int64_t inter,
+                                           void* dense, int64_t ld, void* stream);
+extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+                        int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
+                        const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
+                        int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
+                        void* stream);
+
+namespace moc {
+namespace {
+
+using namespace tile;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Select top-2 of one group from bf16-rounded g[8], u[8] (values as f32) and
+// emit (idx, sz) pairs.
+__device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
+                                                  int64_t* __restrict__ idx_out,
+                                                  uint16_t* __restrict__ sz_out) {
+  uint32_t key[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) key[j] = bf16_order_key(f32_to_bf16(g[j]));
+  int b1 = 0;
+#pragma unroll
+  for (int j = 1; j < 8; ++j)
+    if (key[j] > key[b1]) b1 = j;
+  int b2 = (b1 == 0) ? 1 : 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j != b1 && key[j] > key[b2]) b2 = j;
+  const float g1 = g[b1], g2 = g[b2];
+  idx_out[0] = c0 + b1;
+  idx_out[1] = c0 + b2;
+  sz_out[0] = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
+  sz_out[1] = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
+}
+
+// ---------------------------------------------------------------------------
+// nb <= 16 path.
+// ---------------------------------------------------------------------------
+constexpr int kDecUnroll = 4;
+
+__global__ __launch_bounds__(256) void grouped_decode_kernel(
+    const uint16_t* __restrict__ x, int nb, int hidden, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ wu, int inter, int64_t* __restrict__ idx,
+    uint16_t* __restrict__ sz) {
+  __shared__ f32x4_t red[2][4][64];
+  __shared__ float gu[2][16][17];  // [g|u][channel][token]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c0 = blockIdx.x * 16;
+  const int ch = c0 + (lane & 15);
+  const int tok = lane & 15;
+  const int kq = (lane >> 4) * 8;
+  const bool ch_ok = ch < inter;
+  const bool tok_ok = tok < nb;
+  const uint16_t* gr = wg + static_cast<int64_t>(ch_ok ? ch : 0) * hidden + kq;
+  const uint16_t* ur = wu + static_cast<int64_t>(ch_ok ? ch : 0) * hidden + kq;
+  const uint16_t* xr = x + static_cast<int64_t>(tok_ok ? tok : 0) * hidden + kq;
+  const int nsteps = (hidden + 31) / 32;
+  f32x4_t ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = wave; s0 < nsteps; s0 += 4 * kDecUnroll) {
+    uint4 gv[kDecUnroll], uv[kDecUnroll], xv[kDecUnroll];
+#pragma unroll
+    for (int q = 0; q < kDecUnroll; ++q) {
+      const int s = s0 + 4 * q;
+      const bool kin = s < nsteps && s * 32 + kq < hidden;
+      const uint4 zero = make_uint4(0, 0, 0, 0);
+      gv[q] = (kin && ch_ok) ? *reinterpret_cast<const uint4*>(gr + s * 32) : zero;
+      uv[q] = (kin && ch_ok) ? *reinterpret_cast<const uint4*>(ur + s * 32) : zero;
+      xv[q] = (kin && tok_ok) ? *reinterpret_cast<const uint4*>(xr + s * 32) : zero;
+    }
+#pragma unroll
+    for (int q = 0; q < kDecUnroll; ++q) {
+      const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, xv[q]);
+      ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, gv[q]), xb, ag, 0, 0, 0);
+      au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, uv[q]), xb, au, 0, 0, 0);
+    }
+  }
+  red[0][wave][lane] = ag;
+  red[1][wave][lane] = au;
+  __syncthreads();
+  if (wave < 2) {
+    f32x4_t t = red[wave][0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const f32x4_t o = red[wave][w][lane];
+      t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gu[wave][4 * (lane >> 4) + j][lane & 15] = round_bf16(t[j]);
+  }
+  __syncthreads();
+  // 16 tokens x 2 groups
+  if (threadIdx.x < 32) {
+    const int t = threadIdx.x & 15;
+    const int grp = threadIdx.x >> 4;
+    const int cg = c0 + grp * 8;
+    if (t < nb && cg < inter) {
+      float g[8], u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        g[j] = gu[0][grp * 8 + j][t];
+        u[j] = gu[1][grp * 8 + j][t];
+      }
+      const int kout = inter / 4;
+      const int64_t o = static_cast<int64_t>(t) * kout + (cg / 8) * 2;
+      select_group_emit(g, u, cg, idx + o, sz + o);
+    }
+  }
+}
+
+// B tile of the fused gate/up GEMM: rows [0, 64) are W_gate rows c0.., rows
+// [64, 128) the same W_up rows; same thread mapping and LDS layout as the
+// K-contiguous TileLoader.
+struct DualLoader : TileLoader<true> {
+  __device__ __forceinline__ void load(const uint16_t* __restrict__ wg,
+                                       const uint16_t* __restrict__ wu, int hidden, int cvalid,
+                                       int c0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = tid + kThreads * i;
+      const int row = v >> 3;
+      const int rr = row & 63;
+      const uint16_t* p = (row < 64 ? wg : wu) + static_cast<int64_t>(c0 + rr) * hidden;
+      const int gk = k0 + (v & 7) * 8;
+      if (rr < cvalid && gk + 8 <= hidden) {
+        r[i] = *reinterpret_cast<const uint4*>(p + gk);
+      } else {
+        uint16_t e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = (rr < cvalid && gk + j < hidden) ? p[gk + j] : 0;
+        r[i] = make_uint4(e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16),
+                          e[4] | (uint32_t(e[5]) << 16), e[6] | (uint32_t(e[7]) << 16));
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// nb > 16 path: 128 tokens x 64 channels per workgroup.
+// ---------------------------------------------------------------------------
+constexpr int kGroupPitch = 130;  // bf16 per staged row in the epilogue
+
+__global__ __launch_bounds__(kThreads) void grouped_prefill_kernel(
+    const uint16_t* __restrict__ x, int nb, int hidden, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ wu, int inter, int64_t* __restrict__ idx,
+    uint16_t* __restrict__ sz) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (kBM + kBN) * kPitch];
+  auto As = [&](int b) { return smem + b * (kBM * kPitch); };
+  auto Bs = [&](int b) { return smem + 2 * kBM * kPitch + b * (kBN * kPitch); };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row0 = blockIdx.y * kBM;  // tokens
+  const int c0 = blockIdx.x * 64;     // channels
+  const int wm = (wave >> 1) * 64;
+  const int wn = (wave & 1) * 64;     // 0: gate half, 64: up half
+  const int nk = (hidden + kBK - 1) / kBK;
+  const int cvalid = min(64, inter - c0);
+
+  TileLoader<true> la;
+  DualLoader lb;
+  auto load = [&](int t) {
+    la.load(x, hidden, nb, hidden, row0, t * kBK, tid);
+    lb.load(wg, wu, hidden, cvalid, c0, t * kBK, tid);
+  };
+  auto store = [&](int buf) {
+    la.store(As(buf), tid);
+    lb.store(Bs(buf), tid);
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int frow = lane & 31;
+  const int fk = (lane >> 5) * 8;
+  for (int t = 0; t < nk; ++t) {
+    const int cur = t & 1;
+    if (t + 1 < nk) load(t + 1);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8_t a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                As(cur) + (wm + 32 * i + frow) * kPitch + ks * 16 + fk));
+        b[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                Bs(cur) + (wn + 32 * i + frow) * kPitch + ks * 16 + fk));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (t + 1 < nk) store(cur ^ 1);
+    __syncthreads();
+  }
+
+  // stage bf16-rounded G (cols 0..63) and U (cols 64..127) per token row
+  uint16_t* q = smem;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = wn + 32 * j + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        q[row * kGroupPitch + col] = f32_to_bf16(acc[i][j][r]);
+      }
+    }
+  __syncthreads();
+  const int kout = inter / 4;
+  for (int p = tid; p < kBM * 8; p += kThreads) {
+    const int tr = p >> 3;
+    const int grp = p & 7;
+    const int tok = row0 + tr;
+    const int cg = c0 + grp * 8;
+    if (tok >= nb || cg >= inter) continue;
+    float g[8], u[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      g[j] = bf16_to_f32(q[tr * kGroupPitch + grp * 8 + j]);
+      u[j] = bf16_to_f32(q[tr * kGroupPitch + 64 + grp * 8 + j]);
+    }
+    const int64_t o = static_cast<int64_t>(tok) * kout + (cg / 8) * 2;
+    select_group_emit(g, u, cg, idx + o, sz + o);
+  }
+}
+
+inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+}  // namespace
+}  // namespace moc
+
+using namespace moc;
+
+extern "C" int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t hidden,
+                                             const void* w_gate, const void* w_up, int64_t inter,
+                                             void* idx, void* sz, void* stream) {
+  MOC_REQUIRE(nb >= 0 && hidden >= 1 && inter >= 8, "moc_grouped_top2_up_silu_bf16: bad shape");
+  MOC_REQUIRE(inter % 8 == 0, "intermediate=%lld must be divisible by 8", (long long)inter);
+  MOC_REQUIRE(hidden % 8 == 0, "moc_grouped_top2_up_silu_bf16: hidden must be a multiple of 8");
+  MOC_REQUIRE(inter < (1LL << 30) && hidden < (1LL << 30), "moc_grouped_top2_up_silu_bf16: too large");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && w_gate && w_up && idx && sz, "moc_grouped_top2_up_silu_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up),
+              "moc_grouped_top2_up_silu_bf16: x and weights must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  if (nb <= 16) {
+    grouped_decode_kernel<<<dim3(static_cast<unsigned>((inter + 15) / 16)), 256, 0, st>>>(
+        (const uint16_t*)x, (int)nb, (int)hidden, (const uint16_t*)w_gate, (const uint16_t*)w_up,
+        (int)inter, (int64_t*)idx, (uint16_t*)sz);
+    return check_launch("grouped_decode_kernel");
+  }
+  MOC_REQUIRE((nb + kBM - 1) / kBM <= 65535, "moc_grouped_top2_up_silu_bf16: too many tokens");
+  const dim3 grid(static_cast<unsigned>((inter + 63) / 64), static_cast<unsigned>((nb + kBM - 1) / kBM));
+  grouped_prefill_kernel<<<grid, kThreads, 0, st>>>((const uint16_t*)x, (int)nb, (int)hidden,
+                                                    (const uint16_t*)w_gate, (const uint16_t*)w_up,
+                                                    (int)inter, (int64_t*)idx, (uint16_t*)sz);
+  return check_launch("grouped_prefill_kernel");
+}
+
+extern "C" int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t inter,
+                                                            int64_t hidden) {
+  if (nb <= 0 || k <= 0 || inter <= 0 || hidden <= 0) return 0;
+  if (nb <= 64) return moc_selected_down_workspace_size(nb, k, hidden);
+  return align256(nb * inter * 2);
+}
+
+extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb,
+                                              int64_t k, const void* w_down_t, int64_t inter,
+                                              int64_t hidden, void* y, void* workspace,
+                                              int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(nb >= 0 && k >= 1 && inter >= k && hidden >= 1, "moc_selected_grouped_down_bf16: bad shape");
+  MOC_REQUIRE(hidden % 8 == 0, "moc_selected_grouped_down_bf16: hidden must be a multiple of 8");
+  if (nb == 0) return MOC_OK;
+  const int64_t need = moc_selected_grouped_down_workspace_size(nb, k, inter, hidden);
+  MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "moc_selected_grouped_down_bf16: workspace of %lld bytes required", (long long)need);
+  if (nb <= 64)
+    return moc_selected_down_bf16(sz, idx, MOC_I64, nb, k, w_down_t, inter, hidden, y, workspace,
+                                  workspace_bytes, stream);
+  MOC_REQUIRE(inter % 8 == 0, "moc_selected_grouped_down_bf16: intermediate must be a multiple of 8");
+  int rc = moc_scatter_sparse_to_dense(MOC_BF16, sz, idx, MOC_I64, nb, k, inter, workspace, inter,
+                                       stream);
+  if (rc != MOC_OK) return rc;
+  // y[nb, hidden] = z[nb, inter] (K-contiguous) x W_down^T[inter, hidden] (N-contiguous)
+  return moc_gemm(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, hidden, 1, 0,
+                  nullptr, 0, 0, nullptr, 0, 0, y, hidden, MOC_BF16, stream);
+}

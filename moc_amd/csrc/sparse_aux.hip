@@ -1,0 +1,303 @@
+// Sparse helper kernels of the MoC training path (gfx950).
+//
+// These move data between the compact per-token selection [rows, K] (values
+// paired with channel indices) and the dense [rows, I] activations that the
+// GEMMs consume.  Each entry point restates one launcher of
+// moc/training/triton_sparse_aux.py with the same bf16 rounding points:
+//
+//   moc_sparse_forward_aux     <- sparse_forward_aux      (:197-231, kernel :17-49)
+//   moc_scatter_sparse_to_dense<- scatter_sparse_to_dense (:266-290, kernel :71-87)
+//   moc_gather_dense_to_sparse <- gather_dense_to_sparse  (:234-263, kernel :52-68)
+//   moc_sparse_backward_aux    <- sparse_backward_aux     (:363-423; bf16 chain :376-400,
+//                                                          fp32 kernel :139-182)
+//   moc_gcp_recompute          <- _MoCGCPFunction.backward recompute (moc/ffn.py:435-436)
+//
+// Dense outputs are cleared by a fill kernel inside the same entry point (no
+// hipMemsetAsync, so the calls stay valid inside a captured HIP graph).
+// Elementwise work is one thread per selected entry; every kernel is bound by
+// HBM traffic.
+#include "abi.h"
+#include "common.h"
+
+extern "C" int moc_fill_zero(void* dst, int64_t bytes, void* stream);
+
+namespace moc {
+namespace {
+
+template <bool BF16>
+struct Elem;
+template <>
+struct Elem<true> {
+  using T = uint16_t;
+  __device__ static float ld(T v) { return bf16_to_f32(v); }
+  __device__ static T st(float f) { return f32_to_bf16(f); }
+  __device__ static float rnd(float f) { return round_bf16(f); }
+};
+template <>
+struct Elem<false> {
+  using T = float;
+  __device__ static float ld(T v) { return v; }
+  __device__ static T st(float f) { return f; }
+  __device__ static float rnd(float f) { return f; }
+};
+
+template <bool BF16, typename IdxT>
+__global__ __launch_bounds__(256) void sparse_forward_aux_kernel(
+    const typename Elem<BF16>::T* __restrict__ vals, const IdxT* __restrict__ idx,
+    const typename Elem<BF16>::T* __restrict__ u_full, int64_t u_ld, int64_t n, int k,
+    typename Elem<BF16>::T* __restrict__ u_s, typename Elem<BF16>::T* __restrict__ s_s,
+    typename Elem<BF16>::T* __restrict__ z_s, typename Elem<BF16>::T* __restrict__ z_full,
+    int64_t z_ld, int64_t inter) {
+  using E = Elem<BF16>;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int64_t row = e / k;
+  const int64_t ch = static_cast<int64_t>(idx[e]);
+  if (ch < 0 || ch >= inter) return;  // malformed index: never touch memory
+  const float g = E::ld(vals[e]);
+  const typename E::T u_raw = u_full[row * u_ld + ch];
+  const float u = E::ld(u_raw);
+  // Triton: s = g * sigmoid(g); bf16: s rounded, z = bf16(s_bf16 * u)
+  const float s = E::rnd(g * sigmoid_f32(g));
+  const typename E::T z = E::st(s * u);
+  if (u_s) u_s[e] = u_raw;
+  if (s_s) s_s[e] = E::st(s);
+  if (z_s) z_s[e] = z;
+  if (z_full) z_full[row * z_ld + ch] = z;
+}
+
+template <typename T, typename IdxT>
+__global__ __launch_bounds__(256) void scatter_kernel(const T* __restrict__ sparse,
+                                                      const IdxT* __restrict__ idx, int64_t n,
+                                                      int k, T* __restrict__ dense, int64_t ld,
+                                                      int64_t inter) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int64_t row = e / k;
+  const int64_t ch = static_cast<int64_t>(idx[e]);
+  if (ch < 0 || ch >= inter) return;
+  dense[row * ld + ch] = sparse[e];
+}
+
+template <typename T, typename IdxT>
+__global__ __launch_bounds__(256) void gather_kernel(const T* __restrict__ dense, int64_t ld,
+                                                     const IdxT* __restrict__ idx, int64_t n,
+                                                     int k, T* __restrict__ sparse, int64_t inter) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int64_t row = e / k;
+  const int64_t ch = static_cast<int64_t>(idx[e]);
+  sparse[e] = (ch >= 0 && ch < inter) ? dense[row * ld + ch] : T(0);
+}
+
+// GCP recompute.  torch F.silu on a bf16 tensor evaluates g / (1 + exp(-g))
+// in f32 and rounds; the product is another rounded bf16 op.
+template <bool BF16>
+__global__ __launch_bounds__(256) void gcp_recompute_kernel(
+    const typename Elem<BF16>::T* __restrict__ g_s, const typename Elem<BF16>::T* __restrict__ u_s,
+    int64_t n, typename Elem<BF16>::T* __restrict__ s_s, typename Elem<BF16>::T* __restrict__ z_s) {
+  using E = Elem<BF16>;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const float s = E::rnd(silu_f32(E::ld(g_s[e])));
+  if (s_s) s_s[e] = E::st(s);
+  if (z_s) z_s[e] = E::st(s * E::ld(u_s[e]));
+}
+
+// Backward aux.  bf16 follows the reference's correctness-first chain where
+// every elementwise op materialises a bf16 tensor:
+//   grad_s = bf16(u*gz), grad_u = bf16(s*gz), sig = bf16(sigmoid(g)),
+//   t1 = bf16(1-sig), t2 = bf16(g*t1), t3 = bf16(1+t2), d = bf16(sig*t3),
+//   grad_g = bf16(grad_s*d).
+// f32 is the fused kernel: grad_g = u*gz*sig*(1+g*(1-sig)), grad_u = s*gz.
+// A null s_s recomputes s = silu(g) as the GCP variant does.
+template <bool BF16, typename IdxT>
+__global__ __launch_bounds__(256) void sparse_backward_aux_kernel(
+    const IdxT* __restrict__ idx, const typename Elem<BF16>::T* __restrict__ g_s,
+    const typename Elem<BF16>::T* __restrict__ u_s, const typename Elem<BF16>::T* __restrict__ s_s,
+    const typename Elem<BF16>::T* __restrict__ gz_full, int64_t gz_ld, int64_t n, int k,
+    typename Elem<BF16>::T* __restrict__ grad_g, typename Elem<BF16>::T* __restrict__ grad_u,
+    int64_t out_ld, int64_t inter) {
+  using E = Elem<BF16>;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int64_t row = e / k;
+  const int64_t ch = static_cast<int64_t>(idx[e]);
+  if (ch < 0 || ch >= inter) return;
+  const float gz = E::ld(gz_full[row * gz_ld + ch]);
+  const float g = E::ld(g_s[e]);
+  const float u = E::ld(u_s[e]);
+  const float s = s_s ? E::ld(s_s[e]) : E::rnd(silu_f32(g));
+  float gg, gu;
+  if (BF16) {
+    const float gs = round_bf16(u * gz);
+    gu = round_bf16(s * gz);
+    const float sig = round_bf16(sigmoid_f32(g));
+    const float t1 = round_bf16(1.0f - sig);
+    const float t2 = round_bf16(g * t1);
+    const float t3 = round_bf16(1.0f + t2);
+    const float d = round_bf16(sig * t3);
+    gg = round_bf16(gs * d);
+  } else {
+    const float sig = sigmoid_f32(g);
+    const float d = sig * (1.0f + g * (1.0f - sig));
+    gg = u * gz * d;
+    gu = s * gz;
+  }
+  grad_g[row * out_ld + ch] = E::st(gg);
+  grad_u[row * out_ld + ch] = E::st(gu);
+}
+
+inline dim3 grid_for(int64_t n) { return dim3(static_cast<unsigned>((n + 255) / 256)); }
+
+bool idx_ok(int d) { return d == MOC_I16 || d == MOC_I32 || d == MOC_I64; }
+
+}  // namespace
+}  // namespace moc
+
+using namespace moc;
+
+#define MOC_IDX_DISPATCH(IDX_DTYPE, MACRO)       \
+  do {                                           \
+    if ((IDX_DTYPE) == MOC_I16) {                \
+      MACRO(int16_t);                            \
+    } else if ((IDX_DTYPE) == MOC_I32) {         \
+      MACRO(int32_t);                            \
+    } else {                                     \
+      MACRO(int64_t);                            \
+    }                                            \
+  } while (0)
+
+extern "C" int moc_sparse_forward_aux(int dtype, const void* topk_vals, const void* idx,
+                                      int idx_dtype, const void* u_full, int64_t u_ld,
+                                      int64_t rows, int64_t k, int64_t inter, void* u_sparse,
+                                      void* s_sparse, void* z_sparse, void* z_full, int64_t z_ld,
+                                      void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_sparse_forward_aux: bad dtype");
+  MOC_REQUIRE(idx_ok(idx_dtype), "moc_sparse_forward_aux: bad index dtype");
+  MOC_REQUIRE(rows >= 0 && k >= 1 && inter >= k, "moc_sparse_forward_aux: bad shape");
+  MOC_REQUIRE(u_ld >= inter && (z_full == nullptr || z_ld >= inter),
+              "moc_sparse_forward_aux: bad leading dimension");
+  const int64_t n = rows * k;
+  if (n == 0) return MOC_OK;
+  MOC_REQUIRE(topk_vals && idx && u_full, "moc_sparse_forward_aux: null input");
+  hipStream_t st = as_stream(stream);
+  const size_t esz = dtype == MOC_BF16 ? 2 : 4;
+  if (z_full) {
+    const int rc = moc_fill_zero(z_full, rows * z_ld * static_cast<int64_t>(esz), stream);
+    if (rc != MOC_OK) return rc;
+  }
+#define MOC_FWD(T)                                                                          \
+  if (dtype == MOC_BF16)                                                                    \
+    sparse_forward_aux_kernel<true, T><<<grid_for(n), 256, 0, st>>>(                        \
+        (const uint16_t*)topk_vals, (const T*)idx, (const uint16_t*)u_full, u_ld, n, (int)k, \
+        (uint16_t*)u_sparse, (uint16_t*)s_sparse, (uint16_t*)z_sparse, (uint16_t*)z_full,   \
+        z_ld, inter);                                                                       \
+  else                                                                                      \
+    sparse_forward_aux_kernel<false, T><<<grid_for(n), 256, 0, st>>>(                       \
+        (const float*)topk_vals, (const T*)idx, (const float*)u_full, u_ld, n, (int)k,      \
+        (float*)u_sparse, (float*)s_sparse, (float*)z_sparse, (float*)z_full, z_ld, inter)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_FWD);
+#undef MOC_FWD
+  return check_launch("sparse_forward_aux_kernel");
+}
+
+extern "C" int moc_scatter_sparse_to_dense(int dtype, const void* sparse, const void* idx,
+                                           int idx_dtype, int64_t rows, int64_t k, int64_t inter,
+                                           void* dense, int64_t ld, void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_scatter_sparse_to_dense: bad dtype");
+  MOC_REQUIRE(idx_ok(idx_dtype), "moc_scatter_sparse_to_dense: bad index dtype");
+  MOC_REQUIRE(rows >= 0 && k >= 1 && inter >= k && ld >= inter,
+              "moc_scatter_sparse_to_dense: bad shape");
+  if (rows == 0) return MOC_OK;
+  MOC_REQUIRE(sparse && idx && dense, "moc_scatter_sparse_to_dense: null pointer");
+  const size_t esz = dtype == MOC_BF16 ? 2 : 4;
+  int rc = moc_fill_zero(dense, rows * ld * static_cast<int64_t>(esz), stream);
+  if (rc != MOC_OK) return rc;
+  const int64_t n = rows * k;
+  hipStream_t st = as_stream(stream);
+#define MOC_SCAT(T)                                                                              \
+  if (dtype == MOC_BF16)                                                                         \
+    scatter_kernel<uint16_t, T><<<grid_for(n), 256, 0, st>>>((const uint16_t*)sparse, (const T*)idx, \
+                                                             n, (int)k, (uint16_t*)dense, ld, inter); \
+  else                                                                                           \
+    scatter_kernel<float, T><<<grid_for(n), 256, 0, st>>>((const float*)sparse, (const T*)idx, n,  \
+                                                          (int)k, (float*)dense, ld, inter)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_SCAT);
+#undef MOC_SCAT
+  return check_launch("scatter_kernel");
+}
+
+extern "C" int moc_gather_dense_to_sparse(int dtype, const void* dense, int64_t ld,
+                                          const void* idx, int idx_dtype, int64_t rows,
+                                          int64_t k, void* sparse, void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_gather_dense_to_sparse: bad dtype");
+  MOC_REQUIRE(idx_ok(idx_dtype), "moc_gather_dense_to_sparse: bad index dtype");
+  MOC_REQUIRE(rows >= 0 && k >= 1 && ld >= k, "moc_gather_dense_to_sparse: bad shape");
+  const int64_t n = rows * k;
+  if (n == 0) return MOC_OK;
+  MOC_REQUIRE(sparse && idx && dense, "moc_gather_dense_to_sparse: null pointer");
+  const int64_t inter = ld;  // indices beyond the row pitch read as zero
+  hipStream_t st = as_stream(stream);
+#define MOC_GATH(T)                                                                            \
+  if (dtype == MOC_BF16)                                                                       \
+    gather_kernel<uint16_t, T><<<grid_for(n), 256, 0, st>>>((const uint16_t*)dense, ld,        \
+                                                            (const T*)idx, n, (int)k,          \
+                                                            (uint16_t*)sparse, inter);         \
+  else                                                                                         \
+    gather_kernel<float, T><<<grid_for(n), 256, 0, st>>>((const float*)dense, ld, (const T*)idx, \
+                                                         n, (int)k, (float*)sparse, inter)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_GATH);
+#undef MOC_GATH
+  return check_launch("gather_kernel");
+}
+
+extern "C" int moc_gcp_recompute(int dtype, const void* g_sparse, const void* u_sparse, int64_t n,
+                                 void* s_sparse, void* z_sparse, void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_gcp_recompute: bad dtype");
+  MOC_REQUIRE(n >= 0, "moc_gcp_recompute: bad size");
+  if (n == 0) return MOC_OK;
+  MOC_REQUIRE(g_sparse && u_sparse, "moc_gcp_recompute: null input");
+  hipStream_t st = as_stream(stream);
+  if (dtype == MOC_BF16)
+    gcp_recompute_kernel<true><<<grid_for(n), 256, 0, st>>>(
+        (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, n, (uint16_t*)s_sparse,
+        (uint16_t*)z_sparse);
+  else
+    gcp_recompute_kernel<false><<<grid_for(n), 256, 0, st>>>(
+        (const float*)g_sparse, (const float*)u_sparse, n, (float*)s_sparse, (float*)z_sparse);
+  return check_launch("gcp_recompute_kernel");
+}
+
+extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype,
+                                       const void* g_sparse, const void* u_sparse,
+                                       const void* s_sparse, const void* gz_full, int64_t gz_ld,
+                                       int64_t rows, int64_t k, int64_t inter, void* grad_g,
+                                       void* grad_u, int64_t out_ld, void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_sparse_backward_aux: bad dtype");
+  MOC_REQUIRE(idx_ok(idx_dtype), "moc_sparse_backward_aux: bad index dtype");
+  MOC_REQUIRE(rows >= 0 && k >= 1 && inter >= k && gz_ld >= inter && out_ld >= inter,
+              "moc_sparse_backward_aux: bad shape");
+  if (rows == 0) return MOC_OK;
+  MOC_REQUIRE(idx && g_sparse && u_sparse && gz_full && grad_g && grad_u,
+              "moc_sparse_backward_aux: null pointer");
+  const size_t esz = dtype == MOC_BF16 ? 2 : 4;
+  int rc = moc_fill_zero(grad_g, rows * out_ld * static_cast<int64_t>(esz), stream);
+  if (rc == MOC_OK) rc = moc_fill_zero(grad_u, rows * out_ld * static_cast<int64_t>(esz), stream);
+  if (rc != MOC_OK) return rc;
+  const int64_t n = rows * k;
+  hipStream_t st = as_stream(stream);
+#define MOC_BWD(T)                                                                            \
+  if (dtype == MOC_BF16)                                                                      \
+    sparse_backward_aux_kernel<true, T><<<grid_for(n), 256, 0, st>>>(                         \
+        (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                  \
+        (const uint16_t*)s_sparse, (const uint16_t*)gz_full, gz_ld, n, (int)k,                \
+        (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld, inter);                                 \
+  else                                                                                        \
+    sparse_backward_aux_kernel<false, T><<<grid_for(n), 256, 0, st>>>(                        \
+        (const T*)idx, (const float*)g_sparse, (const float*)u_sparse, (const float*)s_sparse, \
+        (const float*)gz_full, gz_ld, n, (int)k, (float*)grad_g, (float*)grad_u, out_ld, inter)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_BWD);
+#undef MOC_BWD
+  return check_launch("sparse_backward_aux_kernel");
+}

@@ -1,0 +1,292 @@
+"""Mixture-of-Channels SwiGLU FFN on MI355X (module API of moc/ffn.py).
+
+Public names, constructor arguments, attributes and state_dict keys follow
+moc/ffn.py:111-121,500-609 so that models, checkpoints and harnesses written
+against the reference load unchanged:
+
+  dense     - StandardSwiGLUFFN, the dense baseline (stock torch modules).
+  moc       - MoC, selected activations saved for backward.
+  moc_gcp   - MoC with gate checkpointing: saves x, idx, G*M, U*M and
+              recomputes S*M, Z*M in backward (moc/ffn.py:372-497).
+  moc_2_8   - top-2 of every aligned 8-channel group (moc/ffn.py:262-310).
+  moc_post_silu_abs - Top-K of |SiLU(G)| (moc/ffn.py:313-369).
+
+Every MoC mode runs on the gfx950 kernels of libmoc_amd.so: MFMA GEMMs for
+the nine projections, the LDS radix-select Top-K, and the sparse aux
+kernels.  The `*_triton_aux` mode names are accepted for compatibility and
+behave like their plain counterparts (with the reference's requirement of
+int16 saved indices).  There is no CPU path: MoC modes raise on non-device
+tensors.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels as K
+
+_MODES = (
+    "moc",
+    "moc_gcp",
+    "moc_triton_aux",
+    "moc_gcp_triton_aux",
+    "moc_2_8",
+    "moc_2_8_triton_aux",
+    "moc_post_silu_abs",
+    "moc_post_silu_abs_triton_aux",
+)
+
+
+def _pack_topk_idx_dtype(dtype, inter: int):
+    """Index dtype check of _pack_topk_idx (moc/ffn.py:27-41) with the static
+    bound max_allowed_idx = inter - 1 the reference always passes."""
+    if dtype is None:
+        return torch.int64
+    info = torch.iinfo(dtype)
+    if inter - 1 > info.max:
+        raise ValueError(f"topk_idx range [0, {inter - 1}] cannot be stored as {dtype}")
+    return dtype
+
+
+def _moc_2_8_effective_k(intermediate_size: int) -> int:
+    """Structure-determined K' for MoC 2:8 selection (moc/ffn.py:62-65)."""
+    full_groups, tail = divmod(intermediate_size, 8)
+    return full_groups * 2 + min(2, tail)
+
+
+class StandardSwiGLUFFN(nn.Module):
+    """Standard LLaMA-style SwiGLU FFN (moc/ffn.py:111-121)."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+def _check_inputs(x, gate_w, up_w, down_w, strict_aux: bool, index_save_dtype):
+    if strict_aux and index_save_dtype != torch.int16:
+        raise ValueError("MoC fused helper kernels require compact saved indices.")
+    for t in (x, gate_w, up_w, down_w):
+        if not t.is_cuda:
+            raise ValueError("MoC HIP kernels require ROCm device tensors.")
+    if not (x.dtype == gate_w.dtype == up_w.dtype == down_w.dtype):
+        raise ValueError(
+            f"MoC HIP kernels need one compute dtype, got x={x.dtype}, weights="
+            f"{gate_w.dtype}/{up_w.dtype}/{down_w.dtype}")
+
+
+def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool):
+    """Shared MoC forward: G -> select -> U -> sparse aux -> D.
+
+    Follows _MoCFunction.forward (moc/ffn.py:130-173) and the variants at
+    :266-308 (2:8), :322-367 (post-SiLU) and :378-421 (GCP)."""
+    d = x.shape[-1]
+    inter = gate_w.shape[0]
+    x2 = K.aligned_rows(x.reshape(-1, d))
+    rows = x2.shape[0]
+    g = K.padded_empty(rows, inter, x.dtype, x.device)
+    K.linear(x2, gate_w, out=g)
+    if selection == "topk":
+        vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype)
+    elif selection == "post_silu_abs":
+        vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype, score_transform=1)
+    elif selection == "2of8":
+        vals, idx = K.select_2of8(g, idx_dtype=idx_dtype)
+    else:
+        raise ValueError(selection)
+    del g
+    u = K.padded_empty(rows, inter, x.dtype, x.device)
+    K.linear(x2, up_w, out=u)
+    u_s, s_s, z_s, z_full = K.sparse_forward_aux(vals, idx, u, inter, want_s=save_s, want_z=save_s)
+    del u
+    wd = K.aligned_rows(down_w)
+    out = K.gemm(z_full, wd.t())
+    del z_full
+    kk = idx.shape[-1]
+    shp = (*x.shape[:-1], kk)
+    return (out.reshape(*x.shape[:-1], down_w.shape[0]), idx.reshape(shp), vals.reshape(shp),
+            u_s.reshape(shp), None if s_s is None else s_s.reshape(shp),
+            None if z_s is None else z_s.reshape(shp))
+
+
+def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool):
+    """Shared MoC backward (moc/ffn.py:175-259 and the GCP form :423-497).
+
+    dWd = go^T Z, gZ = go Wd, (gG, gU) = sparse_backward_aux, dWg = gG^T x,
+    dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products)."""
+    d = x.shape[-1]
+    inter = gate_w.shape[0]
+    x2 = K.aligned_rows(x.reshape(-1, d))
+    go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
+    if gcp:
+        s_s, z_s = K.gcp_recompute(g_s, u_s)
+    z_full = K.scatter_sparse_to_dense(z_s, idx, inter)
+    grad_down_w = K.gemm(go.t(), z_full, out_dtype=down_w.dtype)
+    del z_full
+    wd = K.aligned_rows(down_w)
+    gz = K.padded_empty(go.shape[0], inter, x.dtype, x.device)
+    K.gemm(go, wd, out=gz)
+    grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
+    del gz
+    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=gate_w.dtype)
+    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=up_w.dtype)
+    grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
+    return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
+
+
+class _MoCFunction(torch.autograd.Function):
+    """MoC autograd path that keeps selected activations for backward
+    (moc/ffn.py:124-259)."""
+
+    selection = "topk"
+
+    @staticmethod
+    def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
+        return _MoCFunction._fwd(ctx, _MoCFunction.selection, x, gate_w, up_w, down_w, k,
+                                 index_save_dtype, use_triton_aux)
+
+    @staticmethod
+    def _fwd(ctx, selection, x, gate_w, up_w, down_w, k, index_save_dtype, use_triton_aux):
+        _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
+        inter = gate_w.shape[0]
+        idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
+        out, idx, vals, u_s, s_s, z_s = _forward_common(
+            x, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=True)
+        ctx.save_for_backward(x, idx, vals, u_s, s_s, z_s, gate_w, up_w, down_w)
+        ctx.k = idx.shape[-1]
+        ctx.inter = inter
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w = ctx.saved_tensors
+        dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w,
+                                             down_w, gcp=False)
+        return dx, dwg, dwu, dwd, None, None, None
+
+
+class _MoC28Function(torch.autograd.Function):
+    """MoC with structured 2:8 selection; reuses the MoC backward
+    (moc/ffn.py:262-310)."""
+
+    @staticmethod
+    def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
+        return _MoCFunction._fwd(ctx, "2of8", x, gate_w, up_w, down_w, k, index_save_dtype,
+                                 use_triton_aux)
+
+    backward = staticmethod(_MoCFunction.backward)
+
+
+class _MoCPostSiluFunction(torch.autograd.Function):
+    """MoC with Top-K on |SiLU(G)|; the pre-SiLU gates at those channels feed
+    the shared sparse machinery (moc/ffn.py:313-369)."""
+
+    @staticmethod
+    def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
+        return _MoCFunction._fwd(ctx, "post_silu_abs", x, gate_w, up_w, down_w, k,
+                                 index_save_dtype, use_triton_aux)
+
+    backward = staticmethod(_MoCFunction.backward)
+
+
+class _MoCGCPFunction(torch.autograd.Function):
+    """MoC with selected-activation checkpointing (moc/ffn.py:372-497): saves
+    x, idx, G*M, U*M; S*M and Z*M are recomputed in backward."""
+
+    @staticmethod
+    def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
+        _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
+        inter = gate_w.shape[0]
+        idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
+        out, idx, vals, u_s, _, _ = _forward_common(
+            x, gate_w, up_w, down_w, k, "topk", idx_dtype, save_s=False)
+        ctx.save_for_backward(x, idx, vals, u_s, gate_w, up_w, down_w)
+        ctx.k = k
+        ctx.inter = inter
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, idx, g_s, u_s, gate_w, up_w, down_w = ctx.saved_tensors
+        dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, None, None, gate_w,
+                                             up_w, down_w, gcp=True)
+        return dx, dwg, dwu, dwd, None, None, None
+
+
+def _autocast_cast(x, ws):
+    """Under torch.autocast the reference's matmuls run in the autocast dtype
+    (moc/ffn.py:50-59); cast inputs the same way for the fused path."""
+    if torch.is_autocast_enabled("cuda") and x.is_cuda:
+        dt = torch.get_autocast_dtype("cuda")
+        return x.to(dt), [w.to(dt) for w in ws]
+    return x, ws
+
+
+class MoCSwiGLUFFN(nn.Module):
+    """MoC SwiGLU FFN with selectable backward strategy (moc/ffn.py:500-581).
+
+    mode='moc'     : save sparse selected activations.
+    mode='moc_gcp' : recompute selected activations in backward.
+    """
+
+    def __init__(self, hidden_size: int, intermediate_size: int, k: int | None = None,
+                 mode: str = "moc", index_save_dtype=None):
+        super().__init__()
+        if mode not in _MODES:
+            raise ValueError(
+                f"Unknown mode '{mode}'. Use 'moc', 'moc_gcp', "
+                "'moc_triton_aux', 'moc_gcp_triton_aux', "
+                "'moc_2_8', 'moc_2_8_triton_aux', "
+                "'moc_post_silu_abs', or 'moc_post_silu_abs_triton_aux'."
+            )
+        self.mode = mode
+        self.requested_k = k
+        if mode.startswith("moc_2_8"):
+            self.k_effective = _moc_2_8_effective_k(intermediate_size)
+        else:
+            if k is None:
+                raise ValueError("MoC FFN requires `k` outside moc_2_8 modes.")
+            self.k_effective = k
+        self.k = self.k_effective
+        self.index_save_dtype = index_save_dtype
+        self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x):
+        weights = [self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight]
+        x, (wg, wu, wd) = _autocast_cast(x, weights)
+        aux = self.mode.endswith("_triton_aux")
+        if self.mode in ("moc_gcp", "moc_gcp_triton_aux"):
+            fn = _MoCGCPFunction
+        elif self.mode in ("moc_2_8", "moc_2_8_triton_aux"):
+            fn = _MoC28Function
+        elif self.mode in ("moc_post_silu_abs", "moc_post_silu_abs_triton_aux"):
+            fn = _MoCPostSiluFunction
+        else:
+            fn = _MoCFunction
+        return fn.apply(x, wg, wu, wd, self.k, self.index_save_dtype, aux)
+
+
+def build_ffn(hidden_size: int, intermediate_size: int, ffn_type: str = "dense", k=None):
+    """Factory for Dense FFN, MoC, MoC+GCP, MoC 2:8 and post-SiLU variants
+    (moc/ffn.py:584-609)."""
+    if ffn_type == "dense":
+        return StandardSwiGLUFFN(hidden_size, intermediate_size)
+    if ffn_type in ("moc", "moc_gcp", "moc_2_8", "moc_post_silu_abs"):
+        if k is None and ffn_type != "moc_2_8":
+            raise ValueError("MoC FFN requires `k`")
+        mode = {
+            "moc": "moc_triton_aux",
+            "moc_gcp": "moc_gcp_triton_aux",
+            "moc_2_8": "moc_2_8_triton_aux",
+            "moc_post_silu_abs": "moc_post_silu_abs_triton_aux",
+        }[ffn_type]
+        return MoCSwiGLUFFN(hidden_size, intermediate_size, k, mode=mode,
+                            index_save_dtype=torch.int16)
+    raise ValueError(f"Unknown ffn_type '{ffn_type}'")

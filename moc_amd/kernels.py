@@ -1,0 +1,366 @@
+"""Python entry points over the gfx950 kernels of libmoc_amd.so.
+
+Each function validates shapes, strides and dtypes, allocates its outputs
+with torch (device memory only), and launches on torch's current stream.
+There is no CPU or eager fallback: non-device tensors raise ValueError and a
+missing library raises NativeLibraryMissing.
+
+Internal [rows, intermediate] activations are allocated with a leading
+dimension padded to a multiple of 8 elements so that every MFMA operand row
+is 16-byte aligned; functions return the logical [:, :intermediate] view.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as N
+
+
+def round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+def _empty(shape, dtype, device):
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
+def _rows_view(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """2-D [rows, cols] view with unit column stride; returns (view, ld)."""
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.shape[1] > 1:
+        t = t.contiguous()
+    ld = t.stride(0) if t.shape[0] > 1 else max(t.shape[1], 1)
+    return t, ld
+
+
+def padded_empty(rows: int, cols: int, dtype, device) -> torch.Tensor:
+    """[rows, cols] view of a [rows, round_up(cols, 8)] allocation."""
+    return _empty((rows, round_up(max(cols, 1), 8)), dtype, device)[:, :cols]
+
+
+def aligned_rows(t: torch.Tensor) -> torch.Tensor:
+    """Row-major copy (if needed) whose rows are 16-byte aligned for MFMA loads."""
+    t, ld = _rows_view(t)
+    if t.dtype != torch.bfloat16:
+        return t
+    if ld % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    out = padded_empty(t.shape[0], t.shape[1], t.dtype, t.device)
+    N.call("moc_copy_pad_2d", N.MOC_BF16, t.data_ptr(), t.shape[0], t.shape[1], ld,
+           out.data_ptr(), out.stride(0), out.stride(0), N.stream_of(t))
+    return out
+
+
+# ----------------------------------------------------------------- selection
+def topk_rows(scores: torch.Tensor, k: int, *, idx_dtype=torch.int64, want_vals: bool = True,
+              want_mask: bool = False, score_transform: int = 0):
+    """Row-wise Top-K of a [rows, I] tensor -> (vals | None, idx, mask | None).
+
+    idx is in ascending channel order; ties go to the lower channel index.
+    """
+    N.require_device(scores)
+    s, ld = _rows_view(scores)
+    rows, inter = s.shape
+    dev = s.device
+    idx = _empty((rows, k), idx_dtype, dev)
+    vals = _empty((rows, k), s.dtype, dev) if want_vals else None
+    words = (inter + 31) // 32
+    mask = _empty((rows, words), torch.int32, dev) if want_mask else None
+    N.call("moc_topk_rows", N.dtype_code(s.dtype), s.data_ptr(), rows, inter, ld, int(k),
+           int(score_transform), N.ptr(vals), idx.data_ptr(), N.idx_code(idx_dtype),
+           N.ptr(mask), words, N.stream_of(s))
+    return vals, idx, mask
+
+
+def moc28_effective_k(inter: int) -> int:
+    full, tail = divmod(int(inter), 8)
+    return full * 2 + min(2, tail)
+
+
+def select_2of8(scores: torch.Tensor, *, idx_dtype=torch.int64):
+    """Top-2 of every aligned 8-channel group -> (vals, idx), (top-1, top-2) per group."""
+    N.require_device(scores)
+    s, ld = _rows_view(scores)
+    rows, inter = s.shape
+    kout = moc28_effective_k(inter)
+    idx = _empty((rows, kout), idx_dtype, s.device)
+    vals = _empty((rows, kout), s.dtype, s.device)
+    N.call("moc_select_2of8", N.dtype_code(s.dtype), s.data_ptr(), rows, inter, ld,
+           vals.data_ptr(), idx.data_ptr(), N.idx_code(idx_dtype), N.stream_of(s))
+    return vals, idx
+
+
+# ----------------------------------------------------------- training helpers
+def _sparse_2d(t: torch.Tensor) -> torch.Tensor:
+    return t.reshape(-1, t.shape[-1]).contiguous()
+
+
+def sparse_forward_aux(topk_vals: torch.Tensor, topk_idx: torch.Tensor, u_full: torch.Tensor,
+                       inter: int, *, want_s: bool = True, want_z: bool = True,
+                       want_full: bool = True):
+    """-> (u_sparse, s_sparse | None, z_sparse | None, z_full | None); z_full is a
+    [rows, inter] view of a padded, zero-filled buffer."""
+    N.require_device(topk_vals, topk_idx, u_full)
+    vals = _sparse_2d(topk_vals)
+    idx = _sparse_2d(topk_idx)
+    rows, k = vals.shape
+    u, u_ld = _rows_view(u_full.reshape(rows, -1) if u_full.dim() != 2 else u_full)
+    if u.shape[1] < inter:
+        raise ValueError(f"u_full has {u.shape[1]} columns, expected >= {inter}")
+    dt, dev = vals.dtype, vals.device
+    if u.dtype != dt:
+        raise ValueError(f"dtype mismatch: topk_vals {dt}, u_full {u.dtype}")
+    u_s = _empty((rows, k), dt, dev)
+    s_s = _empty((rows, k), dt, dev) if want_s else None
+    z_s = _empty((rows, k), dt, dev) if want_z else None
+    z_full = padded_empty(rows, inter, dt, dev) if want_full else None
+    N.call("moc_sparse_forward_aux", N.dtype_code(dt), vals.data_ptr(), idx.data_ptr(),
+           N.idx_code(idx.dtype), u.data_ptr(), u_ld, rows, k, inter, u_s.data_ptr(),
+           N.ptr(s_s), N.ptr(z_s), N.ptr(z_full),
+           z_full.stride(0) if z_full is not None else inter, N.stream_of(vals))
+    return u_s, s_s, z_s, z_full
+
+
+def scatter_sparse_to_dense(sparse: torch.Tensor, topk_idx: torch.Tensor, inter: int) -> torch.Tensor:
+    """[rows, k] -> zero-filled [rows, inter] (view of a padded buffer)."""
+    N.require_device(sparse, topk_idx)
+    sp = _sparse_2d(sparse)
+    idx = _sparse_2d(topk_idx)
+    rows, k = sp.shape
+    dense = padded_empty(rows, inter, sp.dtype, sp.device)
+    N.call("moc_scatter_sparse_to_dense", N.dtype_code(sp.dtype), sp.data_ptr(), idx.data_ptr(),
+           N.idx_code(idx.dtype), rows, k, inter, dense.data_ptr(), dense.stride(0),
+           N.stream_of(sp))
+    return dense
+
+
+def gather_dense_to_sparse(dense: torch.Tensor, topk_idx: torch.Tensor) -> torch.Tensor:
+    N.require_device(dense, topk_idx)
+    idx = _sparse_2d(topk_idx)
+    rows, k = idx.shape
+    d, ld = _rows_view(dense.reshape(rows, -1) if dense.dim() != 2 else dense)
+    out = _empty((rows, k), d.dtype, d.device)
+    N.call("moc_gather_dense_to_sparse", N.dtype_code(d.dtype), d.data_ptr(), ld, idx.data_ptr(),
+           N.idx_code(idx.dtype), rows, k, out.data_ptr(), N.stream_of(d))
+    return out
+
+
+def gcp_recompute(g_sparse: torch.Tensor, u_sparse: torch.Tensor):
+    """GCP recompute -> (s = SiLU(g), z = s * u)."""
+    N.require_device(g_sparse, u_sparse)
+    g = g_sparse.contiguous()
+    u = u_sparse.contiguous()
+    s = torch.empty_like(g)
+    z = torch.empty_like(g)
+    N.call("moc_gcp_recompute", N.dtype_code(g.dtype), g.data_ptr(), u.data_ptr(), g.numel(),
+           s.data_ptr(), z.data_ptr(), N.stream_of(g))
+    return s, z
+
+
+def sparse_backward_aux(topk_idx: torch.Tensor, g_sparse: torch.Tensor, u_sparse: torch.Tensor,
+                        s_sparse: torch.Tensor | None, grad_z_full: torch.Tensor, inter: int):
+    """-> (grad_g, grad_u) as zero-filled [rows, inter] views of padded buffers."""
+    N.require_device(topk_idx, g_sparse, u_sparse, s_sparse, grad_z_full)
+    idx = _sparse_2d(topk_idx)
+    g = _sparse_2d(g_sparse)
+    u = _sparse_2d(u_sparse)
+    s = _sparse_2d(s_sparse) if s_sparse is not None else None
+    rows, k = g.shape
+    gz, gz_ld = _rows_view(grad_z_full.reshape(rows, -1) if grad_z_full.dim() != 2 else grad_z_full)
+    if gz.dtype != g.dtype:
+        raise ValueError(f"dtype mismatch: g_sparse {g.dtype}, grad_z_full {gz.dtype}")
+    gg = padded_empty(rows, inter, g.dtype, g.device)
+    gu = padded_empty(rows, inter, g.dtype, g.device)
+    N.call("moc_sparse_backward_aux", N.dtype_code(g.dtype), idx.data_ptr(), N.idx_code(idx.dtype),
+           g.data_ptr(), u.data_ptr(), N.ptr(s), gz.data_ptr(), gz_ld, rows, k, inter,
+           gg.data_ptr(), gu.data_ptr(), gg.stride(0), N.stream_of(g))
+    return gg, gu
+
+
+# ---------------------------------------------------------------------- GEMM
+def _operand(t: torch.Tensor, bf16: bool) -> tuple[torch.Tensor, int, int]:
+    """Return (tensor, stride0, stride1) of a 2-D operand usable by moc_gemm.
+
+    bf16 operands need a unit stride along one dimension, the other stride a
+    multiple of 8 elements and a 16-byte aligned base; anything else is copied
+    into an aligned row-major buffer.  Strides of size-1 dimensions carry no
+    information and are normalised.
+    """
+    if t.dim() != 2:
+        raise ValueError(f"GEMM operands must be 2-D, got {tuple(t.shape)}")
+    r, c = t.shape
+    s0, s1 = t.stride()
+    if not bf16:
+        return t, s0, s1
+    if r == 1:
+        s0 = round_up(max(c, 1), 8)
+    if c == 1:
+        s1 = round_up(max(r, 1), 8) if s0 == 1 else 1
+    aligned = t.data_ptr() % 16 == 0
+    if aligned and s1 == 1 and s0 % 8 == 0:
+        return t, s0, s1
+    if aligned and s0 == 1 and s1 % 8 == 0:
+        return t, s0, s1
+    tt = aligned_rows(t)
+    return tt, (tt.stride(0) if r > 1 else round_up(max(c, 1), 8)), 1
+
+
+def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
+         b2: torch.Tensor | None = None, out: torch.Tensor | None = None,
+         out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """C = a @ b (+ a2 @ b2) on the MFMA engine; a: [M, K], b: [K, N]."""
+    N.require_device(a, b, a2, b2, out)
+    if a.dtype != b.dtype or (a2 is not None and (a2.dtype != a.dtype or b2.dtype != a.dtype)):
+        raise ValueError("moc gemm operands must share one dtype")
+    M, K = a.shape
+    K_, Nn = b.shape
+    if K != K_:
+        raise ValueError(f"gemm shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
+    bf16 = a.dtype == torch.bfloat16
+    out_dtype = out_dtype or a.dtype
+    if not bf16 and out_dtype != torch.float32:
+        raise ValueError("f32 GEMM produces f32")
+    if out is None:
+        out = _empty((M, Nn), out_dtype, a.device)
+    if out.shape != (M, Nn) or (out.stride(1) != 1 and Nn > 1):
+        raise ValueError("gemm out must be [M, N] with unit column stride")
+    aa, as0, as1 = _operand(a, bf16)
+    bb, bs0, bs1 = _operand(b, bf16)
+    K2 = 0
+    a2p = b2p = None
+    a2s0 = a2s1 = b2s0 = b2s1 = 0
+    if a2 is not None:
+        K2 = a2.shape[1]
+        if a2.shape[0] != M or b2.shape != (K2, Nn):
+            raise ValueError("second GEMM pair has mismatched shapes")
+        a2p, a2s0, a2s1 = _operand(a2, bf16)
+        b2p, b2s0, b2s1 = _operand(b2, bf16)
+    ldc = out.stride(0) if M > 1 else max(Nn, 1)
+    N.call("moc_gemm", N.dtype_code(a.dtype), M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
+           bs0, bs1, K2, N.ptr(a2p), a2s0, a2s1, N.ptr(b2p), b2s0, b2s1, out.data_ptr(), ldc,
+           N.dtype_code(out_dtype), N.stream_of(a))
+    return out
+
+
+def linear(x2d: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None,
+           out_dtype=None) -> torch.Tensor:
+    """x2d @ weight.T for an nn.Linear weight [out_features, in_features]."""
+    return gemm(x2d, weight.t(), out=out, out_dtype=out_dtype)
+
+
+# -------------------------------------------------------------------- decode
+def gemv(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[nb <= 16, hidden] @ weight[rows, hidden].T -> [nb, rows] (bf16)."""
+    N.require_device(x, weight)
+    xx = aligned_rows(x)
+    w = aligned_rows(weight)
+    nb, hidden = xx.shape
+    rows = w.shape[0]
+    if w.shape[1] != hidden:
+        raise ValueError(f"gemv shape mismatch {tuple(x.shape)} x {tuple(weight.shape)}")
+    y = _empty((nb, rows), torch.bfloat16, x.device) if out is None else out
+    if y.shape != (nb, rows) or not y.is_contiguous():
+        raise ValueError("gemv out must be a contiguous [nb, rows] tensor")
+    N.call("moc_gemv_bf16", xx.data_ptr(), xx.stride(0) if nb > 1 else round_up(hidden, 8), nb,
+           w.data_ptr(), w.stride(0), rows, hidden, y.data_ptr(), rows, N.stream_of(x))
+    return y
+
+
+def _bf16_contig(*ts):
+    for t in ts:
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"expected bfloat16, got {t.dtype}")
+    return [t.contiguous() for t in ts]
+
+
+def selected_up_silu(x, topk_vals, topk_idx, up_weight) -> torch.Tensor:
+    N.require_device(x, topk_vals, topk_idx, up_weight)
+    x, vals, w = _bf16_contig(x, topk_vals, up_weight)
+    idx = topk_idx.contiguous()
+    nb, hidden = x.shape
+    k = idx.shape[1]
+    z = _empty((nb, k), torch.bfloat16, x.device)
+    N.call("moc_selected_up_silu_bf16", x.data_ptr(), nb, hidden, vals.data_ptr(), idx.data_ptr(),
+           N.idx_code(idx.dtype), k, w.data_ptr(), w.shape[0], z.data_ptr(), N.stream_of(x))
+    return z
+
+
+def selected_down(sparse_z, topk_idx, down_weight_t) -> torch.Tensor:
+    N.require_device(sparse_z, topk_idx, down_weight_t)
+    z, wdt = _bf16_contig(sparse_z, down_weight_t)
+    idx = topk_idx.contiguous()
+    nb, k = z.shape
+    inter, hidden = wdt.shape
+    y = _empty((nb, hidden), torch.bfloat16, z.device)
+    ws_bytes = N.query("moc_selected_down_workspace_size", nb, k, hidden)
+    ws = _empty((max(ws_bytes, 1),), torch.uint8, z.device)
+    N.call("moc_selected_down_bf16", z.data_ptr(), idx.data_ptr(), N.idx_code(idx.dtype), nb, k,
+           wdt.data_ptr(), inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(z))
+    return y
+
+
+def global_after_gate_workspace_bytes(nb: int, inter: int, k: int, hidden: int) -> int:
+    return N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
+
+
+def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, workspace=None,
+                      out=None) -> torch.Tensor:
+    N.require_device(x, gate_scores, up_weight, down_weight_t)
+    x, g, wu, wdt = _bf16_contig(x, gate_scores, up_weight, down_weight_t)
+    nb, hidden = x.shape
+    inter = g.shape[1]
+    if wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
+        raise ValueError("up_weight and down_weight_t must be [intermediate, hidden]")
+    y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
+    ws_bytes = N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = _empty((max(ws_bytes, 1),), torch.uint8, x.device)
+    N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
+           wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), workspace.data_ptr(), ws_bytes,
+           N.stream_of(x))
+    return y
+
+
+# ----------------------------------------------------------------------- 2:8
+def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None):
+    """-> (idx int64 [nb, inter/4], sparse_z bf16 [nb, inter/4])."""
+    N.require_device(x, gate_weight, up_weight)
+    x, wg, wu = _bf16_contig(x, gate_weight, up_weight)
+    nb, hidden = x.shape
+    inter = wg.shape[0]
+    if inter % 8 != 0:
+        raise ValueError(f"intermediate={inter} must be divisible by 8")
+    if wg.shape != wu.shape or wg.shape[1] != hidden:
+        raise ValueError(f"H mismatch: x={tuple(x.shape)}, gate={tuple(wg.shape)}, up={tuple(wu.shape)}")
+    k = inter // 4
+    idx = _empty((nb, k), torch.int64, x.device) if idx_out is None else idx_out
+    sz = _empty((nb, k), torch.bfloat16, x.device) if sz_out is None else sz_out
+    if idx.shape != (nb, k) or sz.shape != (nb, k) or not (idx.is_contiguous() and sz.is_contiguous()):
+        raise ValueError(f"out shapes must be ({nb},{k})")
+    N.call("moc_grouped_top2_up_silu_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(), wu.data_ptr(),
+           inter, idx.data_ptr(), sz.data_ptr(), N.stream_of(x))
+    return idx, sz
+
+
+def selected_grouped_down_workspace_bytes(nb: int, k: int, inter: int, hidden: int) -> int:
+    return N.query("moc_selected_grouped_down_workspace_size", nb, k, inter, hidden)
+
+
+def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=None) -> torch.Tensor:
+    N.require_device(sparse_z, idx, down_weight_t)
+    sz, wdt = _bf16_contig(sparse_z, down_weight_t)
+    ii = idx.contiguous()
+    if ii.dtype != torch.int64:
+        raise ValueError("idx must be int64")
+    nb, k = sz.shape
+    inter, hidden = wdt.shape
+    y = _empty((nb, hidden), torch.bfloat16, sz.device) if out is None else out
+    if y.shape != (nb, hidden) or not y.is_contiguous():
+        raise ValueError(f"out shape must be ({nb},{hidden})")
+    ws_bytes = selected_grouped_down_workspace_bytes(nb, k, inter, hidden)
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else \
+        _empty((max(ws_bytes, 1),), torch.uint8, sz.device)
+    N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
+           inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
+    return y

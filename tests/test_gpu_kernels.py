@@ -1,0 +1,286 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle (marked gpu).
+
+Integer/index outputs (Top-K indices, masks, 2:8 indices) must match the
+oracle bit-exactly on identical inputs.  Floating outputs are bf16 and are
+compared within rtol/atol 2e-2, or in bf16 ulps
+where the arithmetic is the same sequence of rounded operations.  Inputs are
+seeded on the CPU and copied to the device, so both sides see identical bits.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moc_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLD = Path(__file__).resolve().parent / "golden"
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from moc_amd import _native
+    _native.load()  # raises if the library is missing: no silent fallback
+
+
+def K():
+    from moc_amd import kernels
+    return kernels
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def bf16_ulp_diff(a: torch.Tensor, b: torch.Tensor) -> np.ndarray:
+    """|difference| in bf16 units of last place (order-key distance)."""
+    ka = O.order_keys(a.detach().cpu().to(torch.bfloat16)).astype(np.int64)
+    kb = O.order_keys(b.detach().cpu().to(torch.bfloat16)).astype(np.int64)
+    return np.abs(ka - kb)
+
+
+def bf16_close(a, b, ulps: int = 1, atol: float = 1e-3) -> None:
+    """Each element within `ulps` bf16 ulps of b, or within atol (near zero
+    the ulp distance of two roundings of a cancelling sum is meaningless)."""
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    assert a.shape == b.shape, (a.shape, b.shape)
+    ulp = torch.from_numpy(bf16_ulp_diff(a, b))
+    bad = (ulp > ulps) & ((a - b).abs() > atol)
+    assert not bool(bad.any()), f"{int(bad.sum())} elements off, e.g. {a[bad][:4].tolist()} vs {b[bad][:4].tolist()}"
+
+
+def close(a, b, rtol=2e-2, atol=2e-2):
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    assert a.shape == b.shape, (a.shape, b.shape)
+    err = (a - b).abs()
+    bad = err > atol + rtol * b.abs()
+    assert not bool(bad.any()), f"max err {err.max().item():.4g} at {torch.nonzero(bad)[:4].tolist()}"
+
+
+# ----------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("a_kc", [True, False])
+@pytest.mark.parametrize("b_kc", [True, False])
+@pytest.mark.parametrize("mnk", [(128, 128, 64), (136, 72, 93), (130, 67, 93), (1, 300, 40),
+                                 (264, 5464, 200), (257, 5461, 200)])
+def test_gemm_bf16_layouts(a_kc, b_kc, mnk):
+    M, Nn, Kk = mnk
+    g = gen(1)
+    a = torch.randn(M, Kk, generator=g).to(torch.bfloat16)
+    b = torch.randn(Kk, Nn, generator=g).to(torch.bfloat16)
+    ref = a.float() @ b.float()
+    ad = a.to(DEV) if a_kc else a.t().contiguous().to(DEV).t()
+    bd = b.t().contiguous().to(DEV).t() if b_kc else b.to(DEV)
+    if a_kc and Kk % 8:  # K-contiguous rows need a pitch that is a multiple of 8
+        ad = K().aligned_rows(ad)
+    out = K().gemm(ad, bd, out_dtype=torch.float32)
+    close(out, ref, rtol=1e-4, atol=1e-3)
+    out16 = K().gemm(ad, bd)
+    bf16_close(out16, ref, ulps=1, atol=1e-3)
+
+
+def test_gemm_dual_product_and_f32():
+    g = gen(2)
+    a, a2 = torch.randn(200, 72, generator=g), torch.randn(200, 40, generator=g)
+    b, b2 = torch.randn(72, 96, generator=g), torch.randn(40, 96, generator=g)
+    ref = a @ b + a2 @ b2
+    dual = K().gemm(a.bfloat16().to(DEV), b.bfloat16().to(DEV), a2=a2.bfloat16().to(DEV),
+                    b2=b2.bfloat16().to(DEV), out_dtype=torch.float32)
+    close(dual, a.bfloat16().float() @ b.bfloat16().float() + a2.bfloat16().float() @ b2.bfloat16().float(),
+          rtol=1e-4, atol=1e-3)
+    f32 = K().gemm(a.to(DEV), b.to(DEV), a2=a2.to(DEV), b2=b2.to(DEV))
+    close(f32, ref, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------------- Top-K
+@pytest.mark.parametrize("name", ["topk_bf16_ties", "topk_bf16_rand"])
+def test_topk_golden_bitexact(name):
+    d = dict(np.load(GOLD / f"{name}.npz"))
+    s = O.torch_from_bf16_bits(d["scores_bits"]).to(DEV)
+    _, idx, _ = K().topk_rows(s, int(d["k"]))
+    assert np.array_equal(idx.cpu().numpy(), d["idx"])
+
+
+def test_topk_golden_f32_bitexact():
+    d = dict(np.load(GOLD / "topk_f32_ties.npz"))
+    _, idx, _ = K().topk_rows(torch.from_numpy(d["scores"]).to(DEV), int(d["k"]))
+    assert np.array_equal(idx.cpu().numpy(), d["idx"])
+
+
+@pytest.mark.parametrize("dtype,rows,inter,k", [
+    (torch.bfloat16, 64, 5461, 1024),   # 1b decode/training shape
+    (torch.bfloat16, 300, 2048, 384),   # 130m
+    (torch.float32, 96, 1376, 256),     # 60m (f32, config 1)
+    (torch.bfloat16, 7, 37, 37),        # k == inter
+    (torch.bfloat16, 5, 16384, 1),      # widest supported row, k == 1
+    (torch.float32, 3, 9000, 4500),
+])
+def test_topk_bitexact_vs_oracle(dtype, rows, inter, k):
+    s = (torch.randn(rows, inter, generator=gen(rows + inter)) * 0.9).to(dtype)
+    vals, idx, mask = K().topk_rows(s.to(DEV), k, want_mask=True)
+    want = O.topk_indices(s, k)
+    assert np.array_equal(idx.cpu().numpy(), want)
+    assert torch.equal(vals.cpu(), O.gather_rows(s, want))
+    bits = mask.cpu().numpy().view(np.uint32)
+    m = np.zeros((rows, inter), dtype=bool)
+    for c in range(inter):
+        m[:, c] = (bits[:, c // 32] >> (c % 32)) & 1
+    assert np.array_equal(m, O.topk_mask(want, inter))
+
+
+def test_topk_heavy_ties_and_index_dtypes():
+    vals = torch.tensor(np.random.default_rng(3).choice([0.0, -0.0, 1.0, -2.0, 0.5, float("inf")],
+                                                        size=(33, 700)), dtype=torch.float32)
+    for dt in (torch.bfloat16, torch.float32):
+        s = vals.to(dt)
+        want = O.topk_indices(s, 111)
+        for idt in (torch.int16, torch.int32, torch.int64):
+            _, idx, _ = K().topk_rows(s.to(DEV), 111, idx_dtype=idt)
+            assert idx.dtype == idt and np.array_equal(idx.cpu().numpy().astype(np.int64), want)
+
+
+def test_topk_strided_rows_and_post_silu_transform():
+    s = (torch.randn(20, 600, generator=gen(5)) * 2).to(torch.bfloat16)
+    sd = s.to(DEV)
+    _, idx, _ = K().topk_rows(sd[:, :555], 100)  # leading dimension 600, width 555
+    assert np.array_equal(idx.cpu().numpy(), O.topk_indices(s[:, :555].contiguous(), 100))
+    vals, idx, _ = K().topk_rows(sd, 64, score_transform=1)
+    want = O.topk_indices(O.silu_abs_scores(s), 64)
+    # the transformed score is computed on the device; its bf16 rounding can
+    # differ from the CPU's in rare near-ties, so compare tie-aware
+    score = O.silu_abs_scores(s).float()
+    got = idx.cpu().numpy()
+    for r in range(s.shape[0]):
+        thr = torch.sort(score[r], descending=True).values[63].item()
+        gs = {i for i in got[r] if score[r, i] > thr * (1 + 2 ** -7)}
+        ws = {i for i in want[r] if score[r, i] > thr * (1 + 2 ** -7)}
+        assert gs == ws
+    assert torch.equal(vals.cpu(), O.gather_rows(s, got))  # raw pre-SiLU gates
+
+
+def test_select_2of8_bitexact():
+    d = dict(np.load(GOLD / "sel28_bf16_tail.npz"))
+    s = O.torch_from_bf16_bits(d["scores_bits"])
+    vals, idx = K().select_2of8(s.to(DEV))
+    assert np.array_equal(idx.cpu().numpy(), d["idx"])
+    for dt, inter in ((torch.bfloat16, 5461), (torch.float32, 2736), (torch.bfloat16, 5464)):
+        s = torch.randn(50, inter, generator=gen(inter)).to(dt)
+        vals, idx = K().select_2of8(s.to(DEV), idx_dtype=torch.int16)
+        want = O.select_2of8_indices(s)
+        assert np.array_equal(idx.cpu().numpy().astype(np.int64), want)
+        assert torch.equal(vals.cpu(), O.gather_rows(s, want))
+
+
+# ------------------------------------------------------------- training aux
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_sparse_aux_forward_backward(dtype):
+    rows, inter, k = 300, 2048, 384
+    g = gen(6)
+    G = torch.randn(rows, inter, generator=g).to(dtype)
+    U = torch.randn(rows, inter, generator=g).to(dtype)
+    GZ = torch.randn(rows, inter, generator=g).to(dtype)
+    idx = O.topk_indices(G, k)
+    vals = O.gather_rows(G, idx)
+    u_s, s_s, z_s, z_full = O.sparse_forward_aux(vals, idx, U, inter)
+    ti = torch.from_numpy(idx).to(torch.int16).to(DEV)
+    du, ds, dz, dzf = K().sparse_forward_aux(vals.to(DEV), ti, U.to(DEV), inter)
+    assert torch.equal(du.cpu(), u_s)
+    if dtype == torch.bfloat16:
+        bf16_close(ds, s_s, ulps=1, atol=0)
+        bf16_close(dz, z_s, ulps=2, atol=0)
+        bf16_close(dzf, z_full, ulps=2, atol=0)
+    else:
+        close(ds, s_s, rtol=1e-5, atol=1e-6)
+        close(dz, z_s, rtol=1e-5, atol=1e-6)
+        close(dzf, z_full, rtol=1e-5, atol=1e-6)
+    # scatter / gather round trip
+    dense = K().scatter_sparse_to_dense(z_s.to(DEV), ti, inter)
+    want = torch.zeros(rows, inter, dtype=dtype).scatter_(1, torch.from_numpy(idx), z_s)
+    assert torch.equal(dense.cpu(), want)
+    assert torch.equal(K().gather_dense_to_sparse(dense, ti).cpu(), z_s)
+    # GCP recompute + backward aux
+    rs, rz = O.gcp_recompute(vals, u_s)
+    ks, kz = K().gcp_recompute(vals.to(DEV), u_s.to(DEV))
+    tol = dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    close(ks, rs, **tol)
+    close(kz, rz, **tol)
+    gg, gu = O.sparse_backward_aux(idx, vals, u_s, rs, GZ, inter)
+    kg, ku = K().sparse_backward_aux(ti, vals.to(DEV), u_s.to(DEV), rs.to(DEV), GZ.to(DEV), inter)
+    close(kg, gg, **tol)
+    close(ku, gu, **tol)
+    kg2, ku2 = K().sparse_backward_aux(ti, vals.to(DEV), u_s.to(DEV), None, GZ.to(DEV), inter)
+    close(kg2, gg, **tol)
+
+
+# ------------------------------------------------------------------- decode
+@pytest.mark.parametrize("nb", [1, 4, 16])
+def test_global_decode_path_1b(nb):
+    d, inter, k = 2048, 5461, 1024
+    g = gen(100 + nb)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(d, inter, generator=g) * 0.02).to(torch.bfloat16)
+    xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    wdt = wd.t().contiguous().to(DEV)
+    G = K().gemv(xd, wgd)
+    Gc = G.cpu()
+    bf16_close(Gc, x.float() @ wg.float().t(), ulps=1, atol=1e-3)
+    y_ref, idx_ref, z_ref = O.masked_reference(x, wg, wu, wd, k, g_override=Gc)
+    vals, idx, _ = K().topk_rows(G, k)
+    assert np.array_equal(idx.cpu().numpy(), idx_ref)
+    z = K().selected_up_silu(xd, vals, idx, wud)
+    bf16_close(z, z_ref, ulps=2, atol=1e-4)
+    y = K().selected_down(z, idx, wdt)
+    close(y, O.selected_down(z.cpu(), idx_ref, wd.t().contiguous()), rtol=1e-2, atol=1e-3)
+    y2 = K().global_after_gate(xd, G, wud, wdt, k)
+    close(y2, y_ref)
+    close(y2, y, rtol=0, atol=0)
+
+
+def test_grouped_2of8_integer_inputs_bitexact():
+    """Integer-valued bf16 inputs make G and U exact, so the fused kernel's
+    selection can be compared bit-exactly with the oracle."""
+    rng = np.random.default_rng(9)
+    for nb in (3, 40):
+        d, inter = 64, 96
+        x = torch.tensor(rng.integers(-3, 4, (nb, d)), dtype=torch.bfloat16)
+        wg = torch.tensor(rng.integers(-2, 3, (inter, d)), dtype=torch.bfloat16)
+        wu = torch.tensor(rng.integers(-2, 3, (inter, d)), dtype=torch.bfloat16)
+        wd = torch.tensor(rng.integers(-2, 3, (d, inter)), dtype=torch.bfloat16) * 0.125
+        idx_ref, sz_ref, _ = O.grouped_top2_up_silu(x, wg, wu)
+        idx, sz = K().grouped_top2_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV))
+        assert np.array_equal(idx.cpu().numpy(), idx_ref)
+        bf16_close(sz, sz_ref, ulps=1, atol=0)
+        y = K().selected_grouped_down(sz, idx, wd.t().contiguous().to(DEV))
+        close(y, O.selected_down(sz.cpu(), idx_ref, wd.t().contiguous()), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("nb", [1, 16, 300])
+def test_grouped_2of8_1b_shape(nb):
+    d, inter = 2048, 5464
+    g = gen(200 + nb)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(d, inter, generator=g) * 0.02).to(torch.bfloat16)
+    idx, sz = K().grouped_top2_up_silu(x.to(DEV), wg.to(DEV), wu.to(DEV))
+    # selection on the device's own G: recompute G with the MFMA GEMM and
+    # check the pairs are valid top-2 choices of that G up to one bf16 ulp
+    G = (x.float() @ wg.float().t())
+    gi = idx.cpu().numpy()
+    assert gi.shape == (nb, inter // 4)
+    grp = G.view(nb, inter // 8, 8)
+    sel = torch.gather(G, 1, torch.from_numpy(gi)).view(nb, inter // 8, 2)
+    third = torch.sort(grp, dim=-1, descending=True).values[..., 2]
+    assert bool((sel.min(-1).values >= third - 2 ** -6 * third.abs().clamp_min(1e-3)).all())
+    y_ref, _, _ = O.masked_reference(x, wg, wu, wd, inter // 4, grouped=True)
+    y = K().selected_grouped_down(sz, idx, wd.t().contiguous().to(DEV))
+    close(y, y_ref)

@@ -1,0 +1,139 @@
+"""CPU-only checks of the boundary and host logic (no GPU compute).
+
+* libmoc_amd.so loads and exports every function include/moc_amd.h declares;
+* argument validation returns MOC_ERR_INVALID with the reference's messages
+  before any device work (these calls never launch a kernel);
+* the Python module API mirrors the reference (names, attributes, errors,
+  state_dict keys) and the MoC path refuses CPU tensors instead of falling
+  back to a CPU implementation;
+* the product package never imports the oracle.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import moc_amd
+from moc_amd import _native as N
+from moc_amd import build_ffn, build_model, PRESETS
+from moc_amd.ffn import MoCSwiGLUFFN, _moc_2_8_effective_k
+from moc_amd.inference.inference_ffn import InferenceMoCSwiGLUFFN
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not N.LIB_PATH.exists():
+        pytest.fail("libmoc_amd.so is not built (python -m moc_amd.build)")
+    return N.load()
+
+
+def test_library_exports_every_header_symbol(lib):
+    names = N.header_function_names()
+    assert len(names) >= 20
+    assert set(names) == set(N.SIGNATURES), set(names) ^ set(N.SIGNATURES)
+    for name in names:
+        assert getattr(lib, name) is not None
+    assert lib.moc_abi_version() == 1
+
+
+def test_validation_errors_without_device_work(lib):
+    # k > inter
+    rc = lib.moc_topk_rows(N.MOC_BF16, None, 4, 100, 100, 101, 0, None, None, N.MOC_I64, None, 0, None)
+    assert rc == N.MOC_ERR_INVALID
+    assert "invalid k" in N.last_error()
+    # int16 indices cannot address 40000 channels (moc/ffn.py:37-40)
+    rc = lib.moc_topk_rows(N.MOC_BF16, None, 4, 16000, 16000, 10, 0, None, None, N.MOC_I16, None, 0, None)
+    assert rc == N.MOC_OK or rc == N.MOC_ERR_INVALID  # null pointer or ok-range; no launch either way
+    rc = lib.moc_select_2of8(N.MOC_BF16, None, 2, 40000, 40000, None, None, N.MOC_I16, None)
+    assert rc == N.MOC_ERR_INVALID and "int16" in N.last_error()
+    # 2:8 grouped kernel needs I % 8 == 0 (triton_grouped_moc_ops.py:46-47)
+    rc = lib.moc_grouped_top2_up_silu_bf16(None, 1, 64, None, None, 5461, None, None, None)
+    assert rc == N.MOC_ERR_INVALID and "divisible by 8" in N.last_error()
+    # GEMM leading dimension must keep 16-byte rows
+    rc = lib.moc_gemm(N.MOC_BF16, 4, 4, 4, ctypes.c_void_p(16), 5, 1, ctypes.c_void_p(16), 1, 8,
+                      0, None, 0, 0, None, 0, 0, ctypes.c_void_p(16), 4, N.MOC_BF16, None)
+    assert rc == N.MOC_ERR_INVALID and "multiples of 8" in N.last_error()
+    # rows == 0 is a no-op
+    assert lib.moc_topk_rows(N.MOC_F32, None, 0, 10, 10, 3, 0, None, None, N.MOC_I32, None, 0, None) == N.MOC_OK
+    assert lib.moc_moc28_effective_k(5461) == 1366
+    assert lib.moc_selected_down_workspace_size(1, 1024, 2048) > 0
+
+
+def test_module_api_mirrors_reference():
+    ffn = build_ffn(64, 176, "moc_gcp", k=32)
+    assert isinstance(ffn, MoCSwiGLUFFN)
+    assert ffn.mode == "moc_gcp_triton_aux" and ffn.index_save_dtype == torch.int16
+    assert ffn.k == ffn.k_effective == ffn.requested_k == 32
+    assert set(ffn.state_dict()) == {"gate_proj.weight", "up_proj.weight", "down_proj.weight"}
+    assert ffn.gate_proj.weight.shape == (176, 64) and ffn.down_proj.weight.shape == (64, 176)
+    f28 = build_ffn(2048, 5461, "moc_2_8", k=999)
+    assert f28.k_effective == 1366 == _moc_2_8_effective_k(5461) and f28.requested_k == 999
+    with pytest.raises(ValueError, match="requires `k`"):
+        build_ffn(64, 176, "moc")
+    with pytest.raises(ValueError, match="Unknown ffn_type"):
+        build_ffn(64, 176, "nope")
+    with pytest.raises(ValueError, match="Unknown mode"):
+        MoCSwiGLUFFN(64, 176, 32, mode="bad")
+    assert type(build_ffn(64, 176, "dense")).__name__ == "StandardSwiGLUFFN"
+
+
+def test_moc_path_refuses_cpu_tensors():
+    ffn = MoCSwiGLUFFN(64, 176, 32, mode="moc_gcp")
+    with pytest.raises(ValueError, match="ROCm device"):
+        ffn(torch.randn(3, 64))
+    ffn = build_ffn(64, 176, "moc", k=32)
+    with pytest.raises(ValueError):
+        ffn(torch.randn(3, 64))
+
+
+def test_inference_module_validation():
+    with pytest.raises(ValueError, match=r"k=0 must be in"):
+        InferenceMoCSwiGLUFFN(64, 128, 0)
+    with pytest.raises(ValueError, match="set together"):
+        InferenceMoCSwiGLUFFN(64, 128, 32, grouped_a=2)
+    with pytest.raises(ValueError, match="grouped MoC requires"):
+        InferenceMoCSwiGLUFFN(64, 128, 31, grouped_a=2, grouped_b=8)
+    m = InferenceMoCSwiGLUFFN(64, 128, 32, grouped_a=2, grouped_b=8)
+    assert m.config.grouped and m.config.k == 32
+    x = torch.randn(2, 1, 64)
+    x2, shp = m._flatten_decode_input(x)
+    assert x2.shape == (2, 64) and m._restore_output_shape(x2, shp).shape == (2, 1, 64)
+    with pytest.raises(ValueError, match="expected decode shape"):
+        m._flatten_decode_input(torch.randn(2, 3, 64))
+
+
+def test_build_model_and_presets():
+    cfg = moc_amd.MoCConfig(hidden_size=64, intermediate_size=176, num_hidden_layers=2,
+                            num_attention_heads=4, vocab_size=100, k=32)
+    model = build_model(cfg, ffn_type="moc_gcp")
+    assert model.blocks[0].ffn.mode == "moc_gcp_triton_aux"
+    keys = set(model.state_dict())
+    assert "blocks.1.ffn.down_proj.weight" in keys and "tok_emb.weight" in keys
+    with pytest.raises(ValueError, match="ffn_type must be"):
+        build_model(cfg, ffn_type="bad")
+    assert PRESETS["1b"].intermediate_size == 5461 and PRESETS["350m"].k == 512
+    assert moc_amd.count_parameters(PRESETS["60m"]) > 0
+
+
+def test_custom_ops_registered_with_reference_names():
+    from moc_amd import ops
+    ops.register()
+    for name in ("optimized_global_topk_bf16", "optimized_global_selected_up_silu_bf16",
+                 "optimized_global_selected_down_bf16", "optimized_global_after_gate_bf16"):
+        assert hasattr(torch.ops.moc_native, name)
+    for name in ("optimized_global_topk_bf16", "fused_grouped_top2_up_silu", "selected_grouped_down"):
+        assert hasattr(torch.ops.moc, name)
+    with pytest.raises(Exception):
+        torch.ops.moc_native.optimized_global_topk_bf16(torch.randn(2, 8).bfloat16(), 3)
+
+
+def test_product_never_imports_oracle():
+    for path in (ROOT / "moc_amd").rglob("*.py"):
+        text = path.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle", text, flags=re.M), path
