@@ -222,14 +222,16 @@ def select(g: torch.Tensor, k: int, mode: str) -> np.ndarray:
 
 
 def ffn_forward(x, gate_w, up_w, down_w, k: int, mode: str = "moc_gcp", g_override=None,
-                idx_override=None):
+                idx_override=None, u_override=None):
     """Forward of _MoCFunction / _MoCGCPFunction / _MoC28Function /
     _MoCPostSiluFunction (moc/ffn.py:130-173, 266-308, 322-367, 378-421).
 
     g_override lets a parity test hand in the device's own G so that the
     selection is compared on identical inputs; idx_override replaces the
     selection itself (for scores the device derives from G, such as
-    |SiLU(G)|).  Returns a dict of the saved/intermediate tensors plus D."""
+    |SiLU(G)|); u_override hands in the device's bf16 U, whose last-bit
+    rounding depends on the GEMM's accumulation order.  Returns a dict of
+    the saved/intermediate tensors plus D."""
     dt = x.dtype
     d = x.shape[-1]
     inter = gate_w.shape[0]
@@ -237,16 +239,21 @@ def ffn_forward(x, gate_w, up_w, down_w, k: int, mode: str = "moc_gcp", g_overri
     g = mm(x2, gate_w.t(), dt) if g_override is None else g_override.reshape(-1, inter).to(dt)
     idx = select(g, k, mode) if idx_override is None else np.asarray(idx_override, dtype=np.int64)
     vals = gather_rows(g, idx)
-    u = mm(x2, up_w.t(), dt)
+    u = mm(x2, up_w.t(), dt) if u_override is None else u_override.reshape(-1, inter).to(dt)
     u_s, s_s, z_s, z_full = sparse_forward_aux(vals, idx, u, inter)
     out = mm(z_full, down_w.t(), dt)
     return {"g": g, "idx": idx, "vals": vals, "u_s": u_s, "s_s": s_s, "z_s": z_s,
             "z_full": z_full, "out": out.reshape(*x.shape[:-1], down_w.shape[0])}
 
 
-def ffn_backward(x, gate_w, up_w, down_w, fwd: dict, grad_out, gcp: bool = True):
+def ffn_backward(x, gate_w, up_w, down_w, fwd: dict, grad_out, gcp: bool = True,
+                 gz_override=None):
     """_MoCGCPFunction.backward (moc/ffn.py:423-497) or, with gcp=False,
-    _MoCFunction.backward (moc/ffn.py:175-259).  Returns (dx, dWg, dWu, dWd)."""
+    _MoCFunction.backward (moc/ffn.py:175-259).  Returns (dx, dWg, dWu, dWd).
+
+    gz_override hands in the device's bf16 grad_z_full = grad_out @ W_down
+    (moc/ffn.py:450), so that a one-ulp rounding difference of that GEMM is
+    not amplified by the weight-gradient reductions that follow it."""
     dt = x.dtype
     d = x.shape[-1]
     inter = gate_w.shape[0]
@@ -260,7 +267,7 @@ def ffn_backward(x, gate_w, up_w, down_w, fwd: dict, grad_out, gcp: bool = True)
         s_s, z_s = fwd["s_s"], fwd["z_s"]
     z_full = torch.zeros(x2.shape[0], inter, dtype=dt).scatter_(1, torch.from_numpy(idx), z_s)
     grad_down_w = mm(go.t(), z_full, down_w.dtype)
-    gz = mm(go, down_w, dt)
+    gz = mm(go, down_w, dt) if gz_override is None else gz_override.reshape(-1, inter).to(dt)
     grad_g, grad_u = sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
     grad_gate_w = mm(grad_g.t(), x2, gate_w.dtype)
     grad_up_w = mm(grad_u.t(), x2, up_w.dtype)
