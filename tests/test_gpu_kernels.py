@@ -69,7 +69,8 @@ def close(a, b, rtol=2e-2, atol=2e-2):
 @pytest.mark.parametrize("a_kc", [True, False])
 @pytest.mark.parametrize("b_kc", [True, False])
 @pytest.mark.parametrize("mnk", [(128, 128, 64), (136, 72, 93), (130, 67, 93), (1, 300, 40),
-                                 (264, 5464, 200), (257, 5461, 200)])
+                                 (264, 5464, 200), (257, 5461, 200), (520, 600, 5461),
+                                 (300, 264, 1000)])
 def test_gemm_bf16_layouts(a_kc, b_kc, mnk):
     M, Nn, Kk = mnk
     g = gen(1)
