@@ -1,30 +1,43 @@
 // Global-MoC decode kernels (gfx950): a handful of tokens (nb <= 16) through
-// one MoC FFN layer.  Every kernel here is bound by HBM bandwidth: the gate
-// projection streams all of W_gate, the selected Up/Down kernels stream only
-// the K selected rows of W_up and W_down^T.
+// one MoC FFN layer.  Every kernel here is bound by HBM bandwidth or by
+// memory latency: the gate projection streams all of W_gate, the selected
+// Up/Down kernels stream only the selected rows of W_up and W_down^T.
 //
-//  moc_gemv_bf16              gate projection G = x W_gate^T on MFMA 16x16x32
-//                             (tokens are the N dimension, zero-padded to 16)
+//  moc_gemv_bf16              gate projection G = x W_gate^T.  A workgroup
+//                             owns <= 32 consecutive rows, pulls all of them
+//                             into LDS with direct-to-LDS loads in one go
+//                             (every byte of its share in flight at once),
+//                             then runs MFMA 16x16x32 (tokens padded to 16)
+//  moc_global_after_gate_bf16 (1) select + Up: every workgroup of a token
+//                             recomputes the token's Top-K from G (radix
+//                             select in LDS, lower index on ties) and
+//                             computes z = bf16(bf16(SiLU(g)) bf16(x.W_up[c]))
+//                             for its own slice of the selected ranks;
+//                             (2) selected Down
+//  moc_selected_down_bf16     y[b] = sum_j z[b,j] W_down^T[idx[b,j]]: a
+//                             workgroup per (64-column block, 128 selected
+//                             rows), 128-byte row segments, partial sums
+//                             reduced in a fixed order by the last workgroup
+//                             of each column block to arrive
 //  moc_selected_up_silu_bf16  one wave per (token, selected channel)
-//  moc_selected_down_bf16     split-K over selected rows + fixed-order reduce
-//  moc_global_after_gate_bf16 Top-K -> selected Up -> selected Down
 //
 // Reference: moc/inference/cuda/optimized_global_moc_ext.cu:127-540 and the
 // masked_reference oracle moc/inference/inference_ffn.py:169-180, whose
 // rounding points (U, SiLU(G) and Z materialised in bf16) these kernels keep.
 #include "abi.h"
 #include "common.h"
+#include "select.h"
 
-extern "C" int moc_topk_rows(int dtype, const void* scores, int64_t rows, int64_t inter,
-                             int64_t ld, int64_t k, int score_transform, void* vals_out,
-                             void* idx_out, int idx_dtype, uint32_t* mask_out, int64_t mask_ld,
-                             void* stream);
+extern "C" int moc_fill_zero(void* dst, int64_t bytes, void* stream);
 
 namespace moc {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr uint32_t kOob = 0x80000000u;  // buffer offset that reads as zero
 
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
   const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
@@ -42,10 +55,124 @@ __device__ __forceinline__ int64_t load_idx(const void* p, int64_t e) {
   return static_cast<int64_t>(static_cast<const IdxT*>(p)[e]);
 }
 
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>((uintptr_t)((__attribute__((address_space(3))) const char*)p));
+}
+
+// One direct-to-LDS 16-byte load per lane (lane l -> LDS byte m0 + 16 l);
+// the counter is waited for with an explicit vmcnt(0).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t m0, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(m0), "v"(voff), "s"(rsrc)
+      : "memory");
+}
+
 // ---------------------------------------------------------------------------
-// Gate GEMV: workgroup = 16 rows of W, four waves split the hidden dimension
-// in interleaved 32-wide k steps, an LDS reduction joins the waves.
+// Gate GEMV, streaming form.  Workgroup w owns rows [w*rows/nwg, ...) (<= 32).
+// Row r of the workgroup sits at LDS byte r * 2*hidden; its 16-byte chunk c
+// is stored in slot c ^ (r & 15), so the 16 lanes of an MFMA fragment read
+// (16 rows, one chunk) hit 16 distinct bank groups.
 // ---------------------------------------------------------------------------
+constexpr int kGvMaxRows = 32;
+constexpr int kGvLdsBytes = 128 * 1024;
+constexpr int kGvMaxHidden = 2048;
+constexpr int kGvMaxSteps = kGvMaxHidden / 32 / 4;  // k steps per wave
+
+__global__ __launch_bounds__(256) void gemv_stream_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int nb, const uint16_t* __restrict__ W,
+    int64_t ldw, int rows, int hidden, int nwg, uint16_t* __restrict__ y, int64_t ldy,
+    int wbytes) {
+  __shared__ __attribute__((aligned(1024))) char lw[kGvLdsBytes];
+  __shared__ f32x4_t red[2][4][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r_lo = static_cast<int>(static_cast<int64_t>(blockIdx.x) * rows / nwg);
+  const int r_hi = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * rows / nwg);
+  const int nr = r_hi - r_lo;
+  const int cpr = hidden / 8;  // 16-byte chunks per row (a multiple of 16)
+
+  // 1. every chunk of the workgroup's rows in flight at once
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W), (short)0, wbytes, 0x00020000);
+  const uint32_t lbase = lds_addr(lw);
+  const int ninstr = (nr * cpr + 63) / 64;
+  // linear chunk q = 64 i + lane of the workgroup's rows -> (row r, slot s);
+  // i advances by 4 per trip, so (r, s) advance by 256 chunks incrementally
+  int r = (wave * 64 + lane) / cpr;
+  int s = wave * 64 + lane - r * cpr;
+  const uint32_t rowb = static_cast<uint32_t>(ldw * 2);
+  uint32_t rowoff = static_cast<uint32_t>((static_cast<int64_t>(r_lo + r) * ldw) * 2);
+  for (int i = wave; i < ninstr; i += 4) {
+    const int c = s ^ (r & 15);
+    const uint32_t off = (r < nr) ? rowoff + static_cast<uint32_t>(c * 16) : kOob;
+    dma16(rs, __builtin_amdgcn_readfirstlane(lbase + i * 1024), off);
+    s += 256;
+    while (s >= cpr) {
+      s -= cpr;
+      ++r;
+      rowoff += rowb;
+    }
+  }
+  // the wave's x fragments (L2-resident) load while the rows stream in
+  const int tok = lane & 15, kq = lane >> 4;
+  const bool tok_ok = tok < nb;
+  const uint16_t* xr = x + static_cast<int64_t>(tok_ok ? tok : 0) * ldx;
+  const int steps = hidden / 32;
+  const int s_lo = wave * steps / 4, s_hi = (wave + 1) * steps / 4;
+  uint4 xf[kGvMaxSteps];
+#pragma unroll
+  for (int u = 0; u < kGvMaxSteps; ++u) {
+    const int c = (s_lo + u) * 4 + kq;
+    xf[u] = (tok_ok && s_lo + u < s_hi) ? *reinterpret_cast<const uint4*>(xr + c * 8)
+                                        : make_uint4(0, 0, 0, 0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // 2. MFMA 16x16x32: A = W rows (lane: row l%16, k 8(l/16)..), B = x
+  //    (lane: token l%16); the four waves split the k steps
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  const int r0 = lane & 15;
+#pragma unroll
+  for (int u = 0; u < kGvMaxSteps; ++u) {
+    if (s_lo + u >= s_hi) break;
+    const int c = (s_lo + u) * 4 + kq;
+    const bf16x8_t xb = __builtin_bit_cast(bf16x8_t, xf[u]);
+    const uint4 w0 = *reinterpret_cast<const uint4*>(lw + r0 * (2 * hidden) + ((c ^ r0) * 16));
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w0), xb, acc0, 0, 0, 0);
+    if (nr > 16) {
+      const int r1 = 16 + r0;
+      const uint4 w1 = *reinterpret_cast<const uint4*>(lw + r1 * (2 * hidden) + ((c ^ (r1 & 15)) * 16));
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w1), xb, acc1, 0, 0, 0);
+    }
+  }
+  red[0][wave][lane] = acc0;
+  red[1][wave][lane] = acc1;
+  __syncthreads();
+  // 3. sum the four waves' partials in a fixed order; 16x16 accumulator
+  //    layout: lane l element j -> row 4(l/16) + j, column (token) l%16
+  if (wave < 2 && (wave == 0 || nr > 16)) {
+    f32x4_t t = red[wave][0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const f32x4_t o = red[wave][w][lane];
+      t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
+    }
+    if (tok_ok) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 16 * wave + 4 * (lane >> 4) + j;
+        if (r < nr) y[static_cast<int64_t>(tok) * ldy + r_lo + r] = f32_to_bf16(t[j]);
+      }
+    }
+  }
+}
+
+// Fallback gate GEMV for shapes the streaming kernel does not take
+// (hidden not a multiple of 128 or larger than the LDS row budget).
 constexpr int kGemvUnroll = 8;
 
 __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict__ x, int64_t ldx,
@@ -90,7 +217,6 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
       const f32x4_t o = red[w][lane];
       t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
     }
-    // 16x16 accumulator layout: lane l element j -> row 4*(l/16)+j, column l%16
     const int n = lane & 15;
     if (n < nb) {
 #pragma unroll
@@ -103,7 +229,175 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Selected Up * SiLU: one wave per (token, selected channel).
+// Select + Up.  Workgroup (b, p) of P per token: (1) token b's gate row as
+// order keys in registers (512 threads), (2) the k-th largest key and the
+// ranks of the selected channels in ascending channel order, ties toward
+// the lower index (select.h; the same rule and result as moc_topk_rows),
+// (3) for the ranks [p k / P, (p+1) k / P):
+// u = x_b . W_up[c] (one wave per channel, f32), z = bf16(bf16(SiLU(g)) *
+// bf16(u)); writes idx[b, rank] and z[b, rank].  Workgroup 0 also clears the
+// down kernel's arrival counters.
+// ---------------------------------------------------------------------------
+constexpr int kSelWaves = 8;
+constexpr int kSelThreads = 64 * kSelWaves;
+
+// Thread t holds the gate keys of channels [t L, t L + L) (select.h).
+template <int L>
+__global__ __launch_bounds__(kSelThreads) void select_up_kernel(
+    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
+    int k, int P, const uint16_t* __restrict__ w_up, int32_t* __restrict__ idx_out,
+    uint16_t* __restrict__ z_out, int* __restrict__ cnt, int ncnt) {
+  extern __shared__ __attribute__((aligned(16))) char dyn[];
+  int* list_ch = reinterpret_cast<int*>(dyn);                        // [ceil(k/P)]
+  uint16_t* list_g = reinterpret_cast<uint16_t*>(list_ch + (k + P - 1) / P);
+  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves>()];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x / P, p = blockIdx.x - b * P;
+  if (blockIdx.x == 0)
+    for (int i = tid; i < ncnt; i += kSelThreads) cnt[i] = 0;
+
+  // 1. token b's gate keys
+  const uint16_t* grow = gate + static_cast<int64_t>(b) * inter;
+  const int c0 = tid * L;
+  uint32_t w[sel_words<true, L>()];
+  load_row_raw<true, L>(grow, inter, c0, (reinterpret_cast<uintptr_t>(grow) & 15) == 0, w);
+  raw_to_keys<true, L>(inter, c0, 0, [](uint32_t r) { return r; }, w);
+
+  // 2. threshold, then this workgroup's ranks [p k / P, (p+1) k / P) of the
+  //    selected channels (channel order, ties toward the lower index)
+  uint32_t thr, krem, take[(L + 31) / 32], first;
+  select_threshold<kSelWaves, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k), sel_lds, thr,
+                                                        krem);
+  select_ranks<kSelWaves, L, true>(w, thr, krem, sel_lds, take, first);
+  const int lo = static_cast<int>(static_cast<int64_t>(p) * k / P);
+  const int hi = static_cast<int>(static_cast<int64_t>(p + 1) * k / P);
+  select_emit<L>(take, c0, first, [&](int c, uint32_t pos) {
+    if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) {
+      list_ch[pos - lo] = c;
+      list_g[pos - lo] = grow[c];
+    }
+  });
+  __syncthreads();
+
+  // 3. selected Up * SiLU: one wave per channel, up to four channels in
+  //    flight per wave
+  const int cpr = hidden / 8;
+  const uint16_t* xb = x + static_cast<int64_t>(b) * hidden;
+  const int nsel = hi - lo;
+  for (int e0 = wave * 4; e0 < nsel; e0 += 4 * kSelWaves) {
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c = lane; c < cpr; c += 64) {
+      const uint4 xv = *reinterpret_cast<const uint4*>(xb + c * 8);
+      uint4 wv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u;
+        wv[u] = (e < nsel)
+                    ? *reinterpret_cast<const uint4*>(w_up + static_cast<int64_t>(list_ch[e]) * hidden + c * 8)
+                    : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = dot8(wv[u], xv, acc[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int e = e0 + u;
+      const float tot = wave_sum(acc[u]);
+      if (lane == 0 && e < nsel) {
+        const int ch = list_ch[e];
+        const float uu = round_bf16(tot);
+        const float sg = round_bf16(silu_f32(bf16_to_f32(list_g[e])));
+        const int64_t o = static_cast<int64_t>(b) * k + lo + e;
+        idx_out[o] = ch;
+        z_out[o] = f32_to_bf16(sg * uu);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Selected Down.  Workgroup (cb, gg): columns [64 cb, 64 cb + 64) of y and
+// group gg = b G + g of 128 selected rows of token b (G = ceil(k / 128)).
+// Thread t: row slot t/8 (+32 per pass), 8 columns (16 bytes) at 8 (t%8).
+// Column sums of the group go to part[gg][64 cb ..]; the last of the G
+// workgroups of (b, cb) to arrive adds the G partials in group order.
+// ---------------------------------------------------------------------------
+constexpr int kDownRows = 128;
+
+template <typename IdxT>
+__global__ __launch_bounds__(256) void selected_down_kernel(
+    const uint16_t* __restrict__ z, const void* __restrict__ idx, int k, int hidden,
+    const uint16_t* __restrict__ wdt, int inter, int G, float* __restrict__ part,
+    int* __restrict__ cnt, uint16_t* __restrict__ y) {
+  __shared__ float red[32][65];
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const int cb = blockIdx.x, gg = blockIdx.y;
+  const int b = gg / G, g = gg - b * G;
+  const int rs = tid >> 3, q = tid & 7;
+  const int col = cb * 64 + q * 8;
+  const int64_t zb = static_cast<int64_t>(b) * k;
+
+  int64_t ch[4];
+  float zz[4];
+#pragma unroll
+  for (int ps = 0; ps < 4; ++ps) {
+    const int j = g * kDownRows + ps * 32 + rs;
+    const bool ok = j < k;
+    ch[ps] = ok ? load_idx<IdxT>(idx, zb + j) : -1;
+    zz[ps] = ok ? bf16_to_f32(z[zb + j]) : 0.f;
+  }
+  uint4 wv[4];
+#pragma unroll
+  for (int ps = 0; ps < 4; ++ps)
+    wv[ps] = (ch[ps] >= 0 && ch[ps] < inter)
+                 ? *reinterpret_cast<const uint4*>(wdt + ch[ps] * hidden + col)
+                 : make_uint4(0, 0, 0, 0);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ps = 0; ps < 4; ++ps) {
+    const uint32_t a[4] = {wv[ps].x, wv[ps].y, wv[ps].z, wv[ps].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = fmaf(zz[ps], __uint_as_float(a[i] << 16), acc[2 * i]);
+      acc[2 * i + 1] = fmaf(zz[ps], __uint_as_float(a[i] & 0xFFFF0000u), acc[2 * i + 1]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[rs][q * 8 + i] = acc[i];
+  __syncthreads();
+  // Partials are written through to the device-coherent level (agent-scope
+  // atomic stores) and waited for before the arrival count is bumped; the
+  // last workgroup reads them back with agent-scope loads.  No full L2
+  // write-back or invalidate (what a __threadfence() costs) is needed.
+  float* prow = part + static_cast<int64_t>(gg) * hidden + cb * 64;
+  if (tid < 64) {
+    float s = 0.f;
+    for (int r = 0; r < 32; ++r) s += red[r][tid];
+    __hip_atomic_store(prow + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&cnt[b * (hidden / 64) + cb], 1);
+    last = (prev == G - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  if (tid < 64) {
+    const float* p0 = part + static_cast<int64_t>(b) * G * hidden + cb * 64 + tid;
+    float s = 0.f;
+    for (int gi = 0; gi < G; ++gi)
+      s += __hip_atomic_load(p0 + static_cast<int64_t>(gi) * hidden, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    y[static_cast<int64_t>(b) * hidden + cb * 64 + tid] = f32_to_bf16(s);
+  }
+  if (tid == 0) cnt[b * (hidden / 64) + cb] = 0;  // ready for the next call
+}
+
+// ---------------------------------------------------------------------------
+// Selected Up * SiLU from given (vals, idx): one wave per (token, channel).
 // ---------------------------------------------------------------------------
 template <typename IdxT>
 __global__ __launch_bounds__(256) void selected_up_silu_kernel(
@@ -144,129 +438,61 @@ __global__ __launch_bounds__(256) void selected_up_silu_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Selected Down, split over the k selected rows.  Workgroup (split, h-chunk,
-// token): 4 waves stride over the split's rows, each lane owns 8 columns.
-// Partials [splits, nb, hidden] f32 are summed in split order by a second
-// kernel, so the result does not depend on scheduling.
-// ---------------------------------------------------------------------------
-struct DownPlan {
-  int splits;
-  int rows_per_split;
-  int hchunks;
-};
-
-__host__ __device__ inline DownPlan down_plan(int64_t nb, int64_t k, int64_t hidden) {
-  DownPlan p;
-  p.hchunks = static_cast<int>((hidden + 511) / 512);
-  const int64_t target = 512;  // workgroups to fill 256 CUs twice
-  int64_t s = (target + p.hchunks * nb - 1) / (p.hchunks * nb);
-  const int64_t smax = (k + 3) / 4;  // at least 4 rows (one per wave) per split
-  if (s > smax) s = smax;
-  if (s < 1) s = 1;
-  p.rows_per_split = static_cast<int>((k + s - 1) / s);
-  p.splits = static_cast<int>((k + p.rows_per_split - 1) / p.rows_per_split);
-  return p;
-}
-
-template <typename IdxT>
-__global__ __launch_bounds__(256) void selected_down_partial_kernel(
-    const uint16_t* __restrict__ z, const void* __restrict__ idx, int k, int hidden,
-    const uint16_t* __restrict__ wdt, int inter, int rows_per_split, int nb,
-    float* __restrict__ part) {
-  __shared__ float red[4][512];
-  const int split = blockIdx.x;
-  const int hc = blockIdx.y;
-  const int b = blockIdx.z;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = hc * 512 + lane * 8;
-  const bool col_ok = col < hidden;
-  const int kbeg = split * rows_per_split;
-  const int kend = min(k, kbeg + rows_per_split);
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const int64_t zb = static_cast<int64_t>(b) * k;
-  int kk = kbeg + wave;
-  for (; kk + 4 < kend; kk += 8) {
-    const int64_t r0 = load_idx<IdxT>(idx, zb + kk);
-    const int64_t r1 = load_idx<IdxT>(idx, zb + kk + 4);
-    const float z0 = bf16_to_f32(z[zb + kk]);
-    const float z1 = bf16_to_f32(z[zb + kk + 4]);
-    uint4 w0 = make_uint4(0, 0, 0, 0), w1 = make_uint4(0, 0, 0, 0);
-    if (col_ok && r0 >= 0 && r0 < inter) w0 = *reinterpret_cast<const uint4*>(wdt + r0 * hidden + col);
-    if (col_ok && r1 >= 0 && r1 < inter) w1 = *reinterpret_cast<const uint4*>(wdt + r1 * hidden + col);
-    const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w};
-    const uint32_t a1[4] = {w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(z0, __uint_as_float(a0[i] << 16), acc[2 * i]);
-      acc[2 * i + 1] = fmaf(z0, __uint_as_float(a0[i] & 0xFFFF0000u), acc[2 * i + 1]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(z1, __uint_as_float(a1[i] << 16), acc[2 * i]);
-      acc[2 * i + 1] = fmaf(z1, __uint_as_float(a1[i] & 0xFFFF0000u), acc[2 * i + 1]);
-    }
-  }
-  for (; kk < kend; kk += 4) {
-    const int64_t r0 = load_idx<IdxT>(idx, zb + kk);
-    const float z0 = bf16_to_f32(z[zb + kk]);
-    uint4 w0 = make_uint4(0, 0, 0, 0);
-    if (col_ok && r0 >= 0 && r0 < inter) w0 = *reinterpret_cast<const uint4*>(wdt + r0 * hidden + col);
-    const uint32_t a0[4] = {w0.x, w0.y, w0.z, w0.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(z0, __uint_as_float(a0[i] << 16), acc[2 * i]);
-      acc[2 * i + 1] = fmaf(z0, __uint_as_float(a0[i] & 0xFFFF0000u), acc[2 * i + 1]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) red[wave][lane * 8 + i] = acc[i];
-  __syncthreads();
-  if (wave == 0 && col_ok) {
-    float* dst = part + (static_cast<int64_t>(split) * nb + b) * hidden + col;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      dst[i] = ((red[0][lane * 8 + i] + red[1][lane * 8 + i]) + red[2][lane * 8 + i]) +
-               red[3][lane * 8 + i];
-  }
-}
-
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ part,
-                                                           int splits, int64_t n,
-                                                           uint16_t* __restrict__ y) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= n) return;
-  float s = 0.f;
-  for (int i = 0; i < splits; ++i) s += part[static_cast<int64_t>(i) * n + e];
-  y[e] = f32_to_bf16(s);
-}
-
 bool idx_ok(int d) { return d == MOC_I16 || d == MOC_I32 || d == MOC_I64; }
+
+inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+// Down workspace: partials [nb * G][hidden] f32, then counters [nb][hidden/64].
+struct DownWs {
+  int G;
+  int64_t part_bytes, cnt_bytes;
+};
+inline DownWs down_ws(int64_t nb, int64_t k, int64_t hidden) {
+  DownWs w;
+  w.G = static_cast<int>((k + kDownRows - 1) / kDownRows);
+  w.part_bytes = align256(nb * w.G * hidden * 4);
+  w.cnt_bytes = align256(nb * (hidden / 64) * 4);
+  return w;
+}
 
 int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
                          const void* wdt, int64_t inter, int64_t hidden, void* y, void* ws,
                          hipStream_t st) {
-  const DownPlan p = down_plan(nb, k, hidden);
+  const DownWs w = down_ws(nb, k, hidden);
   float* part = static_cast<float*>(ws);
-  const dim3 grid(p.splits, p.hchunks, static_cast<unsigned>(nb)), block(256);
+  int* cnt = reinterpret_cast<int*>(static_cast<char*>(ws) + w.part_bytes);
+  const dim3 grid(static_cast<unsigned>(hidden / 64), static_cast<unsigned>(nb * w.G)), block(256);
 #define MOC_DOWN(T)                                                                         \
-  selected_down_partial_kernel<T><<<grid, block, 0, st>>>(                                  \
-      (const uint16_t*)z, idx, (int)k, (int)hidden, (const uint16_t*)wdt, (int)inter,       \
-      p.rows_per_split, (int)nb, part)
+  selected_down_kernel<T><<<grid, block, 0, st>>>((const uint16_t*)z, idx, (int)k, (int)hidden, \
+                                                  (const uint16_t*)wdt, (int)inter, w.G, part, \
+                                                  cnt, (uint16_t*)y)
   if (idx_dtype == MOC_I16) MOC_DOWN(int16_t);
   else if (idx_dtype == MOC_I32) MOC_DOWN(int32_t);
   else MOC_DOWN(int64_t);
 #undef MOC_DOWN
-  int rc = check_launch("selected_down_partial_kernel");
-  if (rc != MOC_OK) return rc;
-  const int64_t n = nb * hidden;
-  split_reduce_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), 256, 0, st>>>(
-      part, p.splits, n, static_cast<uint16_t*>(y));
-  return check_launch("split_reduce_kernel");
+  return check_launch("selected_down_kernel");
 }
 
-inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
+template <int L>
+void launch_select_up_l(const void* x, int hidden, const void* gate, int inter, int k, int nb,
+                        int P, const void* w_up, int32_t* idx, uint16_t* z, int* cnt, int ncnt,
+                        hipStream_t st) {
+  const int per = (k + P - 1) / P;
+  const size_t lds = static_cast<size_t>(per) * 6;
+  select_up_kernel<L><<<dim3(static_cast<unsigned>(nb * P)), kSelThreads, lds, st>>>(
+      (const uint16_t*)x, hidden, (const uint16_t*)gate, inter, k, P, (const uint16_t*)w_up, idx,
+      z, cnt, ncnt);
+}
+
+void launch_select_up(const void* x, int hidden, const void* gate, int inter, int k, int nb, int P,
+                      const void* w_up, int32_t* idx, uint16_t* z, int* cnt, int ncnt,
+                      hipStream_t st) {
+  const int per = (inter + kSelThreads - 1) / kSelThreads;
+  if (per <= 8) launch_select_up_l<8>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
+  else if (per <= 16) launch_select_up_l<16>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
+  else if (per <= 24) launch_select_up_l<24>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
+  else launch_select_up_l<32>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
+}
 
 }  // namespace
 }  // namespace moc
@@ -284,10 +510,23 @@ extern "C" int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void*
   if (nb == 0 || rows == 0) return MOC_OK;
   MOC_REQUIRE(x && W && y, "moc_gemv_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(W), "moc_gemv_bf16: x and W must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  const int64_t wbytes = rows * ldw * 2;
+  const int64_t max_rows = kGvLdsBytes / (2 * hidden);
+  if (hidden % 128 == 0 && hidden <= kGvMaxHidden && max_rows >= 16 &&
+      wbytes < (1LL << 31) - 1024) {
+    // balanced split over >= 256 workgroups with <= min(32, max_rows) rows each
+    const int64_t cap = max_rows < kGvMaxRows ? max_rows : kGvMaxRows;
+    int64_t nwg = (rows + cap - 1) / cap;
+    if (nwg < 256) nwg = rows < 256 ? rows : 256;
+    gemv_stream_kernel<<<dim3(static_cast<unsigned>(nwg)), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw, (int)rows, (int)hidden,
+        (int)nwg, (uint16_t*)y, ldy, (int)wbytes);
+    return check_launch("gemv_stream_kernel");
+  }
   const dim3 grid(static_cast<unsigned>((rows + 15) / 16)), block(256);
-  gemv16_kernel<<<grid, block, 0, as_stream(stream)>>>(
-      (const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw, (int)rows, (int)hidden,
-      (uint16_t*)y, ldy);
+  gemv16_kernel<<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw,
+                                        (int)rows, (int)hidden, (uint16_t*)y, ldy);
   return check_launch("gemv16_kernel");
 }
 
@@ -319,8 +558,8 @@ extern "C" int moc_selected_up_silu_bf16(const void* x, int64_t nb, int64_t hidd
 
 extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64_t hidden) {
   if (nb <= 0 || k <= 0 || hidden <= 0) return 0;
-  const DownPlan p = down_plan(nb, k, hidden);
-  return align256(static_cast<int64_t>(p.splits) * nb * hidden * 4);
+  const DownWs w = down_ws(nb, k, hidden);
+  return w.part_bytes + w.cnt_bytes;
 }
 
 extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
@@ -329,14 +568,17 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
                                       int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(idx_ok(idx_dtype), "moc_selected_down_bf16: bad index dtype");
   MOC_REQUIRE(nb >= 0 && k >= 1 && inter >= 1 && hidden >= 1, "moc_selected_down_bf16: bad shape");
-  MOC_REQUIRE(hidden % 8 == 0, "moc_selected_down_bf16: hidden must be a multiple of 8");
-  MOC_REQUIRE(nb <= 65535, "moc_selected_down_bf16: nb too large");
+  MOC_REQUIRE(hidden % 64 == 0, "moc_selected_down_bf16: hidden must be a multiple of 64");
+  MOC_REQUIRE(nb <= 65535 && nb * k < (1LL << 31), "moc_selected_down_bf16: too many rows");
   if (nb == 0) return MOC_OK;
   MOC_REQUIRE(z && idx && w_down_t && y, "moc_selected_down_bf16: null pointer");
   MOC_REQUIRE(aligned16(w_down_t), "moc_selected_down_bf16: w_down_t must be 16-byte aligned");
   const int64_t need = moc_selected_down_workspace_size(nb, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_selected_down_bf16: workspace of %lld bytes required", (long long)need);
+  const DownWs w = down_ws(nb, k, hidden);
+  int rc = moc_fill_zero(static_cast<char*>(workspace) + w.part_bytes, w.cnt_bytes, stream);
+  if (rc != MOC_OK) return rc;
   return launch_selected_down(z, idx, idx_dtype, nb, k, w_down_t, inter, hidden, y, workspace,
                               as_stream(stream));
 }
@@ -344,8 +586,7 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
 extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t k,
                                                         int64_t hidden) {
   if (nb <= 0 || k <= 0 || hidden <= 0 || inter <= 0) return 0;
-  return align256(nb * k * 4) + 2 * align256(nb * k * 2) +
-         moc_selected_down_workspace_size(nb, k, hidden);
+  return align256(nb * k * 4) + align256(nb * k * 2) + moc_selected_down_workspace_size(nb, k, hidden);
 }
 
 extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
@@ -353,24 +594,31 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
                                           const void* w_down_t, int64_t k, void* y,
                                           void* workspace, int64_t workspace_bytes,
                                           void* stream) {
-  MOC_REQUIRE(nb >= 0 && inter >= 1 && hidden >= 1, "moc_global_after_gate_bf16: bad shape");
+  MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_bf16: 0 <= nb <= 16 tokens");
+  MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64, "moc_global_after_gate_bf16: bad shape");
+  MOC_REQUIRE(hidden % 64 == 0, "moc_global_after_gate_bf16: hidden must be a multiple of 64");
   MOC_REQUIRE(k >= 1 && k <= inter, "invalid k");
   if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && gate_scores && w_up && w_down_t && y, "moc_global_after_gate_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(w_up) && aligned16(w_down_t),
+              "moc_global_after_gate_bf16: x and weights must be 16-byte aligned");
   const int64_t need = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_global_after_gate_bf16: workspace of %lld bytes required", (long long)need);
   char* ws = static_cast<char*>(workspace);
-  void* idx = ws;
+  int32_t* idx = reinterpret_cast<int32_t*>(ws);
   ws += align256(nb * k * 4);
-  void* vals = ws;
+  uint16_t* z = reinterpret_cast<uint16_t*>(ws);
   ws += align256(nb * k * 2);
-  void* z = ws;
-  ws += align256(nb * k * 2);
-  int rc = moc_topk_rows(MOC_BF16, gate_scores, nb, inter, inter, k, 0, vals, idx, MOC_I32,
-                         nullptr, 0, stream);
+  const DownWs w = down_ws(nb, k, hidden);
+  int* cnt = reinterpret_cast<int*>(ws + w.part_bytes);
+  const int ncnt = static_cast<int>(nb * (hidden / 64));
+  hipStream_t st = as_stream(stream);
+  int P = static_cast<int>(256 / nb);
+  if (P > k) P = static_cast<int>(k);
+  launch_select_up(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, P, w_up, idx, z, cnt,
+                   ncnt, st);
+  int rc = check_launch("select_up_kernel");
   if (rc != MOC_OK) return rc;
-  rc = moc_selected_up_silu_bf16(x, nb, hidden, vals, idx, MOC_I32, k, w_up, inter, z, stream);
-  if (rc != MOC_OK) return rc;
-  return moc_selected_down_bf16(z, idx, MOC_I32, nb, k, w_down_t, inter, hidden, y, ws,
-                                moc_selected_down_workspace_size(nb, k, hidden), stream);
+  return launch_selected_down(z, idx, MOC_I32, nb, k, w_down_t, inter, hidden, y, ws, st);
 }

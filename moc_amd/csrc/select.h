@@ -1,0 +1,402 @@
+// Selection of the k largest order keys of one row, by a group of NW waves
+// (NW = 1: one wave selects on its own, with no workgroup barrier; NW > 1:
+// the NW waves of a workgroup select one row together).
+//
+// Thread t of the group holds the order keys of the L contiguous channels
+// [t L, t L + L) in registers (L a multiple of 8; two 16-bit keys per
+// register for bf16 scores, one 32-bit key for f32).  Channels past the row
+// end hold the key 0, which no real value produces (real bf16/f32 keys are
+// >= 0x80 / 0x800000), so a padding key is never the k-th largest and
+// counting padding keys in the lowest bin never moves the threshold.
+//
+// select_threshold finds the k-th largest key T and how many T-valued
+// channels still have to be taken (krem) by an MSB-first radix select with
+// 8-bit digits (2 passes over the registers for 16-bit keys, 4 for 32-bit).
+// Each wave counts into its own 256-bin histogram in LDS, kept in four
+// copies (lane % 4 picks the copy) so that lanes hitting the same bin
+// collide four times less.  A key whose higher digits do not match the
+// prefix found so far is counted into one of 16 spare bins instead (a
+// branch-free unsigned min), so no pass needs a compare per key.  A wave's
+// LDS operations execute in program order, so a wave needs no barrier to
+// read back its own counts; with NW > 1 the NW wave histograms meet in a
+// double-buffered table behind one barrier per digit.
+//
+// select_ranks turns T into per-thread bit masks of the selected channels:
+// every channel above T, and the krem lowest-index T-valued channels (the
+// reference's tie rule), with the thread's first rank from one scan of the
+// packed (count > T, count == T) pair over the group.  select_emit then
+// visits the set bits, so the cost of the emit grows with the number of
+// selected channels a thread holds, not with L.
+#pragma once
+
+#include "common.h"
+
+namespace moc {
+
+typedef unsigned short sel_u16x2 __attribute__((ext_vector_type(2)));
+typedef short sel_s16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kSelBins = 256;
+constexpr int kSelSpare = 16;                                // bins for keys off the prefix
+constexpr int kSelCopyPitch = kSelBins + kSelSpare + 1;      // dwords per histogram copy
+constexpr int kSelWaveHist = 4 * kSelCopyPitch;
+
+// LDS dwords the selection of a group of NW waves needs.
+template <int NW>
+constexpr int select_lds_dwords() {
+  return NW * kSelWaveHist + (NW > 1 ? 2 * NW * kSelBins + NW : 0);
+}
+
+// Order keys of two packed bf16 values: 0x8000 + |v| for v >= 0 (and -0),
+// 0x8000 - |v| for v < 0, so keys compare as the values do; five packed
+// 16-bit operations for the pair.  NaN is fixed up by bf16x2_fix_nan.
+__device__ __forceinline__ uint32_t bf16x2_order_keys(uint32_t w, sel_u16x2& amax) {
+  const sel_u16x2 v = __builtin_bit_cast(sel_u16x2, w);
+  const sel_u16x2 m = __builtin_bit_cast(sel_u16x2, __builtin_bit_cast(sel_s16x2, w) >> 15);
+  const sel_u16x2 a = v & static_cast<unsigned short>(0x7FFF);
+  amax = __builtin_elementwise_max(amax, a);
+  return __builtin_bit_cast(uint32_t, ((a ^ m) + static_cast<unsigned short>(0x8000)) - m);
+}
+
+// NaN (either sign) ranks above +inf (key 0xFF80) and all NaNs are equal:
+// bf16x2_order_keys maps a NaN to (0xFF80, 0xFFFF] or [0x0001, 0x007F],
+// ranges no number reaches; both become 0xFFFF.
+__device__ __forceinline__ uint32_t bf16x2_fix_nan(uint32_t key2) {
+  uint32_t r = key2;
+  const uint32_t lo = key2 & 0xFFFFu, hi = key2 >> 16;
+  if (lo > 0xFF80u || (lo != 0u && lo < 0x80u)) r |= 0xFFFFu;
+  if (hi > 0xFF80u || (hi != 0u && hi < 0x80u)) r |= 0xFFFF0000u;
+  return r;
+}
+
+// Order key of one f32 value with the same rules (NaN -> 0xFFFFFFFF, -0 ->
+// +0): 0x80000000 + |v| for v >= 0, 0x80000000 - |v| for v < 0.
+__device__ __forceinline__ uint32_t f32_fast_order_key(uint32_t u) {
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return 0xFFFFFFFFu;
+  return (u & 0x80000000u) ? 0x80000000u - a : 0x80000000u + a;
+}
+
+// Words per thread: two 16-bit keys or one 32-bit key per register.
+template <bool BF16, int L>
+constexpr int sel_words() {
+  return BF16 ? L / 2 : L;
+}
+
+// Raw scores of channels [c0, c0 + L) of a row of n channels (BF16: uint16
+// bits, else f32 bits) into w, 0 past n; loaded by this thread directly.
+// vec: the row is 16-byte aligned, so whole 8-channel chunks load as
+// 16-byte vectors.
+template <bool BF16, int L>
+__device__ __forceinline__ void load_row_raw(const void* src, int n, int c0, bool vec,
+                                             uint32_t (&w)[sel_words<BF16, L>()]) {
+  static_assert(L % 8 == 0, "L must be a multiple of 8");
+  constexpr int W = sel_words<BF16, L>();
+  constexpr int WPC = BF16 ? 4 : 8;  // words per 8-channel chunk
+  constexpr int ESZ = BF16 ? 2 : 4;
+  const char* s = static_cast<const char*>(src);
+  if (vec) {
+#pragma unroll
+    for (int i = 0; i < L / 8; ++i) {
+      const int c = c0 + 8 * i;
+      if (c + 8 <= n) {
+        const uint4 a = *reinterpret_cast<const uint4*>(s + static_cast<int64_t>(c) * ESZ);
+        w[WPC * i + 0] = a.x; w[WPC * i + 1] = a.y; w[WPC * i + 2] = a.z; w[WPC * i + 3] = a.w;
+        if constexpr (!BF16) {
+          const uint4 b = *reinterpret_cast<const uint4*>(s + static_cast<int64_t>(c) * ESZ + 16);
+          w[WPC * i + 4] = b.x; w[WPC * i + 5] = b.y; w[WPC * i + 6] = b.z; w[WPC * i + 7] = b.w;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < WPC; ++q) w[WPC * i + q] = 0;
+      }
+    }
+  }
+  // element loads: everything without vec, else only the chunk that
+  // straddles the row end
+  if (!vec || (c0 < n && c0 + L > n)) {
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      const int chunk_end = c0 + 8 * (j / WPC) + 8;
+      if (!vec || chunk_end > n) {
+        if constexpr (BF16) {
+          const int c = c0 + 2 * j;
+          const uint16_t* e = reinterpret_cast<const uint16_t*>(s);
+          const uint32_t lo = c < n ? e[c] : 0u, hi = c + 1 < n ? e[c + 1] : 0u;
+          w[j] = lo | (hi << 16);
+        } else {
+          const int c = c0 + j;
+          w[j] = c < n ? reinterpret_cast<const uint32_t*>(s)[c] : 0u;
+        }
+      }
+    }
+  }
+}
+
+// The same through LDS: the group of NW waves (thread t) loads the row
+// coalesced into stage (64 NW L channels, 16-byte aligned), then each thread
+// reads its own L channels back with 16-byte LDS reads.  Used where a
+// thread's share is long: direct loads of long per-thread runs touch every
+// cache line from many load instructions.  stage may alias the select's
+// histograms: the last barrier here orders the reads before their reuse.
+template <int NW, bool BF16, int L>
+__device__ __forceinline__ void load_row_raw_staged(const void* src, int n, int t, bool vec,
+                                                    uint32_t* stage,
+                                                    uint32_t (&w)[sel_words<BF16, L>()]) {
+  constexpr int GT = 64 * NW;
+  constexpr int EPC = BF16 ? 8 : 4;        // elements per 16 bytes
+  constexpr int CPT = L / EPC;             // 16-byte chunks per thread
+  constexpr int ESZ = BF16 ? 2 : 4;
+  const char* s = static_cast<const char*>(src);
+  uint4* st4 = reinterpret_cast<uint4*>(stage);
+  if (vec) {
+    const int nfull = n / EPC;
+    uint4 v[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = t + GT * i;
+      if (ch < nfull) {
+        v[i] = *reinterpret_cast<const uint4*>(s + static_cast<int64_t>(ch) * 16);
+      } else {
+        uint32_t e[4] = {0u, 0u, 0u, 0u};
+        if (ch == nfull) {  // the chunk that straddles the row end
+#pragma unroll
+          for (int q = 0; q < EPC; ++q) {
+            const int c = ch * EPC + q;
+            if (c < n) {
+              if (BF16) e[q / 2] |= static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(s)[c]) << (16 * (q & 1));
+              else e[q] = reinterpret_cast<const uint32_t*>(s)[c];
+            }
+          }
+        }
+        v[i] = make_uint4(e[0], e[1], e[2], e[3]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) st4[t + GT * i] = v[i];
+  } else {
+    constexpr int EPT = L;  // elements per thread, coalesced over the group
+    uint32_t v[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int c = t + GT * i;
+      v[i] = c < n ? (BF16 ? static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(s)[c])
+                           : reinterpret_cast<const uint32_t*>(s)[c])
+                   : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int c = t + GT * i;
+      if (BF16) reinterpret_cast<uint16_t*>(stage)[c] = static_cast<uint16_t>(v[i]);
+      else stage[c] = v[i];
+    }
+  }
+  if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const uint4 a = st4[t * CPT + i];
+    w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
+  }
+  (void)ESZ;
+  if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+}
+
+// Raw scores in w (channels [c0, c0 + L)) -> order keys, key 0 past n.
+// transform 1 ranks by |SiLU(v)| rounded to the score type instead of v
+// (key_of gives that key for one raw value).
+template <bool BF16, int L, typename KeyOf>
+__device__ __forceinline__ void raw_to_keys(int n, int c0, int transform, KeyOf key_of,
+                                            uint32_t (&w)[sel_words<BF16, L>()]) {
+  constexpr int W = sel_words<BF16, L>();
+  if (transform == 0) {
+    if constexpr (BF16) {
+      sel_u16x2 amax = {0, 0};
+#pragma unroll
+      for (int j = 0; j < W; ++j) w[j] = bf16x2_order_keys(w[j], amax);
+      if (__builtin_expect(amax.x > 0x7F80 || amax.y > 0x7F80, 0)) {
+#pragma unroll
+        for (int j = 0; j < W; ++j) w[j] = bf16x2_fix_nan(w[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < W; ++j) w[j] = f32_fast_order_key(w[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < W; ++j)
+      w[j] = BF16 ? (key_of(w[j] & 0xFFFFu) | (key_of(w[j] >> 16) << 16)) : key_of(w[j]);
+  }
+  // padding channels -> key 0
+  if (c0 + L > n) {
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      if constexpr (BF16) {
+        const int c = c0 + 2 * j;
+        if (c >= n) w[j] = 0;
+        else if (c + 1 >= n) w[j] &= 0xFFFFu;
+      } else {
+        if (c0 + j >= n) w[j] = 0;
+      }
+    }
+  }
+}
+
+template <int NW, int W, int KEY_BITS>
+__device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_t k,
+                                                 uint32_t* lds, uint32_t& thr, uint32_t& krem) {
+  const int t = (NW > 1) ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x & 63);
+  const int lane = t & 63, wave = t >> 6;
+  uint32_t* hist = lds + wave * kSelWaveHist;
+  uint32_t* mine = hist + (lane & 3) * kSelCopyPitch;
+  uint32_t* wtab = lds + NW * kSelWaveHist;  // [2][NW][256], only for NW > 1
+  const uint32_t spare = kSelBins + (lane >> 2);  // this lane's spare bin
+  uint32_t prefix = 0;
+  krem = k;
+#pragma unroll
+  for (int pass = 0; pass < KEY_BITS / 8; ++pass) {
+    const int shift = KEY_BITS - 8 * (pass + 1);
+    const uint32_t phi = (pass == 0) ? 0u : prefix >> (shift + 8);
+#pragma unroll
+    for (int i = 0; i < (kSelWaveHist + 63) / 64; ++i)
+      if (lane + 64 * i < kSelWaveHist) hist[lane + 64 * i] = 0;
+    __builtin_amdgcn_wave_barrier();
+    auto bump = [&](uint32_t bin) {
+      __hip_atomic_fetch_add(&mine[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+    };
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+      if constexpr (KEY_BITS == 16) {
+        if (pass == 0) {
+          bump((w[j] >> 8) & 0xFFu);
+          bump(w[j] >> 24);
+        } else {
+          // (key - phi:00) per half; off-prefix keys land at >= 256 -> spare
+          const sel_u16x2 x = __builtin_elementwise_min(
+              __builtin_bit_cast(sel_u16x2, w[j]) - static_cast<unsigned short>(phi << 8),
+              sel_u16x2{static_cast<unsigned short>(spare), static_cast<unsigned short>(spare)});
+          bump(x.x);
+          bump(x.y);
+        }
+      } else {
+        const uint32_t x = (w[j] >> shift) - (phi << 8);
+        bump(pass == 0 ? x : min(x, spare));
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // lane l owns bins 255 - 4 l - m (m = 0..3): descending bins in lane order
+    uint32_t s[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int bin = kSelBins - 1 - 4 * lane - m;
+      s[m] = hist[bin] + hist[kSelCopyPitch + bin] + hist[2 * kSelCopyPitch + bin] +
+             hist[3 * kSelCopyPitch + bin];
+    }
+    if constexpr (NW > 1) {
+      uint32_t* tab = wtab + (pass & 1) * NW * kSelBins;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) tab[wave * kSelBins + 4 * lane + m] = s[m];
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        s[m] = 0;
+#pragma unroll
+        for (int q = 0; q < NW; ++q) s[m] += tab[q * kSelBins + 4 * lane + m];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // keys in bins >= bin: scan over lanes, then within the lane
+    const uint32_t tot = s[0] + s[1] + s[2] + s[3];
+    uint32_t ge = wave_inclusive_scan(tot) - tot;
+    int hit_m = -1;
+    uint32_t hit_gt = 0;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t gt = ge;
+      ge += s[m];
+      if (gt < krem && ge >= krem) {
+        hit_m = m;
+        hit_gt = gt;
+      }
+    }
+    const int src = __ffsll(static_cast<unsigned long long>(__ballot(hit_m >= 0))) - 1;
+    const uint32_t pb = static_cast<uint32_t>(kSelBins - 1 - 4 * src - __shfl(hit_m, src, 64));
+    krem -= __shfl(hit_gt, src, 64);
+    prefix |= pb << shift;
+  }
+  thr = prefix;
+}
+
+// take[d] bit i: channel c0 + 32 d + i is selected; first: rank of the
+// thread's first selected channel.  With NW > 1 this uses the table behind
+// the histograms and one workgroup barrier.
+template <int NW, int L, bool BF16>
+__device__ __forceinline__ void select_ranks(const uint32_t (&w)[sel_words<BF16, L>()],
+                                             uint32_t thr, uint32_t krem, uint32_t* lds,
+                                             uint32_t (&take)[(L + 31) / 32], uint32_t& first) {
+  constexpr int D = (L + 31) / 32;
+  uint32_t eqb[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) take[d] = eqb[d] = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const uint32_t key = BF16 ? ((w[i / 2] >> (16 * (i & 1))) & 0xFFFFu) : w[i];
+    take[i / 32] |= (key > thr ? 1u : 0u) << (i % 32);
+    eqb[i / 32] |= (key == thr ? 1u : 0u) << (i % 32);
+  }
+  uint32_t cgt = 0, ceq = 0;
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    cgt += __popc(take[d]);
+    ceq += __popc(eqb[d]);
+  }
+  // one scan of the packed pair (group totals stay below 2^16)
+  const uint32_t v = (cgt << 16) | ceq;
+  const uint32_t incl = wave_inclusive_scan(v);
+  uint32_t ex = incl - v;
+  if constexpr (NW > 1) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t* tab = lds + NW * kSelWaveHist + 2 * NW * kSelBins;
+    if (lane == 63) tab[wave] = incl;
+    __syncthreads();
+    for (int q = 0; q < wave; ++q) ex += tab[q];
+  }
+  const uint32_t gt_before = ex >> 16, eq_before = ex & 0xFFFFu;
+  first = gt_before + min(krem, eq_before);
+  uint32_t allow = krem > eq_before ? krem - eq_before : 0u;
+  // the lowest-index `allow` T-valued channels of this thread
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    const uint32_t n = __popc(eqb[d]);
+    if (allow >= n) {
+      take[d] |= eqb[d];
+      allow -= n;
+    } else {
+      uint32_t e = eqb[d];
+      for (uint32_t q = 0; q < allow; ++q) {
+        take[d] |= e & (0u - e);
+        e &= e - 1u;
+      }
+      allow = 0;
+    }
+  }
+}
+
+// Calls on_sel(channel, rank) for every selected channel of the thread, in
+// channel order.
+template <int L, typename OnSel>
+__device__ __forceinline__ void select_emit(const uint32_t (&take)[(L + 31) / 32], int c0,
+                                            uint32_t first, OnSel&& on_sel) {
+  uint32_t pos = first;
+#pragma unroll
+  for (int d = 0; d < (L + 31) / 32; ++d) {
+    uint32_t bits = take[d];
+    while (bits) {
+      const int i = __ffs(bits) - 1;
+      on_sel(c0 + 32 * d + i, pos);
+      ++pos;
+      bits &= bits - 1u;
+    }
+  }
+}
+
+}  // namespace moc

@@ -12,15 +12,21 @@
 // the selected channels in ascending channel order (the reference leaves the
 // order unspecified, sorted=False), so row r of idx is strictly increasing.
 //
-// Top-K algorithm: one workgroup per row.  The row's order keys are staged in
-// LDS, each thread then owns a contiguous chunk in registers.  An MSB-first
-// radix *select* (8-bit digits, 2 passes for bf16 keys, 4 for f32) finds the
-// exact threshold key T and the number r of T-valued channels that still have
-// to be taken.  Two block scans then give each thread (a) how many T-valued
-// channels precede its chunk, which resolves the lower-index tie rule, and
-// (b) its output offset, which compacts the selection in channel order.
+// Top-K algorithm: one wave per row (up to four rows per workgroup, no
+// workgroup barrier).  The row's order keys are staged in the wave's LDS
+// (16-byte loads).  An MSB-first radix *select* with 4-bit digits over
+// lane-private histograms (4 passes over the keys for bf16 scores, 8 for f32;
+// select.h) finds the exact threshold key T and the number r of T-valued
+// channels still to take.  One walk over the row in chunks of 64 channels
+// then ranks the selected channels by ballots (the r lowest-index T-valued
+// channels are taken) and writes them in channel order, with the bit mask
+// words straight from the chunk ballots.
+#include <algorithm>
+#include <type_traits>
+
 #include "abi.h"
 #include "common.h"
+#include "select.h"
 
 namespace moc {
 namespace {
@@ -28,174 +34,163 @@ namespace {
 constexpr int kTopkThreads = 256;
 constexpr int kMaxTopkInter = 16384;
 
+// Order key of a raw score (bf16 or f32 bits); transform 1 ranks by
+// |SiLU(g)| rounded to the score dtype (moc/ffn.py:335).
 template <bool BF16>
-__device__ __forceinline__ uint32_t load_key(const void* base, int64_t i, int transform) {
+__device__ __forceinline__ uint32_t score_key(uint32_t raw, int transform) {
   if (BF16) {
-    uint16_t b = static_cast<const uint16_t*>(base)[i];
-    if (transform == 1) {  // |SiLU(g)| rounded to the score dtype (moc/ffn.py:335)
-      b = f32_to_bf16(fabsf(silu_f32(bf16_to_f32(b))));
-    }
+    uint16_t b = static_cast<uint16_t>(raw);
+    if (transform == 1) b = f32_to_bf16(fabsf(silu_f32(bf16_to_f32(b))));
     return bf16_order_key(b);
   } else {
-    uint32_t u = static_cast<const uint32_t*>(base)[i];
+    uint32_t u = raw;
     if (transform == 1) u = __float_as_uint(fabsf(silu_f32(__uint_as_float(u))));
     return f32_order_key(u);
   }
 }
 
-template <bool BF16, int ITEMS, typename IdxT>
+template <bool BF16>
+__device__ __forceinline__ uint32_t load_key(const void* base, int64_t i, int transform) {
+  const uint32_t raw = BF16 ? static_cast<uint32_t>(static_cast<const uint16_t*>(base)[i])
+                            : static_cast<const uint32_t*>(base)[i];
+  return score_key<BF16>(raw, transform);
+}
+
+// Row-group shape: NW waves select one row; a workgroup holds RPW groups.
+template <int NW>
+constexpr int topk_rows_per_wg() {
+  return NW == 1 ? 4 : 1;
+}
+
+// Thread t of a row group holds channels [t L, t L + L) (select.h).  Per
+// group LDS: first the staged row, then, in the same space, the select's
+// histograms, the row's mask words (mask output only; assembled with LDS OR
+// and stored coalesced) and the list of the k selected channel ids in rank
+// order (stored coalesced).
+template <bool BF16, int NW, int L>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
-    const void* __restrict__ scores, int64_t ld, int inter, int k, int transform,
-    void* __restrict__ vals, IdxT* __restrict__ idx, uint32_t* __restrict__ mask,
-    int64_t mask_ld) {
-  constexpr int KEY_BITS = BF16 ? 16 : 32;
-  extern __shared__ uint32_t lds_dyn[];  // keys staging, later reused as flags
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t wtot[16];
-  __shared__ uint32_t pick[2];
+    const void* __restrict__ scores, int64_t ld, int64_t rows, int inter, int k, int transform,
+    int vec, int group_dwords, void* __restrict__ vals, void* __restrict__ idx, int idx_dtype,
+    uint32_t* __restrict__ mask, int64_t mask_ld) {
+  constexpr int ESZ = BF16 ? 2 : 4;
+  constexpr int GT = 64 * NW;  // threads per row group
+  constexpr int D = (L + 31) / 32;
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds_dyn[];
+  const int grp = threadIdx.x / GT, t = threadIdx.x % GT;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * topk_rows_per_wg<NW>() + grp;
+  if (row >= rows) return;  // whole row groups only; NW > 1 has one group per workgroup
+  uint32_t* lds = lds_dyn + grp * group_dwords;
+  const char* src = static_cast<const char*>(scores) + row * ld * ESZ;
+  const int c0 = t * L;
+  const int mwords = (inter + 31) / 32;
+  const int mask_dwords = mask != nullptr ? (mwords + 3) / 4 * 4 : 0;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
-  const int64_t row = blockIdx.x;
-  const size_t esz = BF16 ? 2 : 4;
-  const void* src = static_cast<const char*>(scores) + row * ld * esz;
+  // 1. order keys of this thread's channels (coalesced through LDS)
+  uint32_t w[sel_words<BF16, L>()];
+  load_row_raw_staged<NW, BF16, L>(src, inter, t, vec != 0, lds, w);
+  raw_to_keys<BF16, L>(inter, c0, transform, [](uint32_t r) { return score_key<BF16>(r, 1); }, w);
 
-  // 1. stage order keys (coalesced), 2. pull my contiguous chunk to registers
-  uint16_t* keys16 = reinterpret_cast<uint16_t*>(lds_dyn);
-  for (int i = tid; i < inter; i += kTopkThreads) {
-    const uint32_t key = load_key<BF16>(src, i, transform);
-    if (BF16) keys16[i] = static_cast<uint16_t>(key); else lds_dyn[i] = key;
-  }
-  __syncthreads();
-  const int chunk = (inter + kTopkThreads - 1) / kTopkThreads;
-  const int beg = min(tid * chunk, inter);
-  const int n = min(beg + chunk, inter) - beg;
-  uint32_t key[ITEMS];
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    key[j] = 0;
-    if (j < n) key[j] = BF16 ? static_cast<uint32_t>(keys16[beg + j]) : lds_dyn[beg + j];
+  // 2. threshold and the selected channels of this thread
+  uint32_t thr, krem, take[D], first;
+  select_threshold<NW, sel_words<BF16, L>(), BF16 ? 16 : 32>(w, static_cast<uint32_t>(k), lds,
+                                                             thr, krem);
+  select_ranks<NW, L, BF16>(w, thr, krem, lds, take, first);
+
+  // 3. selected channels in channel order: ids into the group's LDS list
+  //    (rank order), then out to HBM coalesced, with values and the index
+  //    type conversion
+  uint16_t* list = reinterpret_cast<uint16_t*>(lds + select_lds_dwords<NW>() + mask_dwords);
+  select_emit<L>(take, c0, first, [&](int c, uint32_t pos) { list[pos] = static_cast<uint16_t>(c); });
+  if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+  using KT = typename std::conditional<BF16, uint16_t, uint32_t>::type;
+  const KT* raw = reinterpret_cast<const KT*>(src);
+  auto copy_out = [&](auto* idx_row) {
+    using IT = typename std::remove_pointer<decltype(idx_row)>::type;
+    for (int e = t; e < k; e += GT) idx_row[e] = static_cast<IT>(list[e]);
+  };
+  if (idx_dtype == MOC_I16) copy_out(static_cast<int16_t*>(idx) + row * k);
+  else if (idx_dtype == MOC_I32) copy_out(static_cast<int32_t*>(idx) + row * k);
+  else copy_out(static_cast<int64_t*>(idx) + row * k);
+  if (vals != nullptr) {
+    KT* vals_row = static_cast<KT*>(vals) + row * k;
+    for (int e = t; e < k; e += GT) vals_row[e] = raw[list[e]];
   }
 
-  // 3. MSB-first radix select of the k-th largest key
-  uint32_t prefix = 0, pmask = 0;
-  uint32_t krem = static_cast<uint32_t>(k);
-#pragma unroll
-  for (int shift = KEY_BITS - 8; shift >= 0; shift -= 8) {
-    hist[tid] = 0;  // kTopkThreads == 256 bins
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < ITEMS; ++j) {
-      if (j < n && (key[j] & pmask) == prefix) atomicAdd(&hist[(key[j] >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    // thread t looks at bin 255-t; inclusive scan over t = #elements with digit >= bin
-    const uint32_t h = hist[255 - tid];
-    const uint32_t inc = wave_inclusive_scan(h);
-    if (lane == kWave - 1) wtot[wave] = inc;
-    __syncthreads();
-    uint32_t before = 0;
-    for (int w = 0; w < wave; ++w) before += wtot[w];
-    const uint32_t ge = before + inc;
-    const uint32_t gt = ge - h;
-    if (gt < krem && ge >= krem) {
-      pick[0] = 255u - tid;
-      pick[1] = krem - gt;
-    }
-    __syncthreads();
-    prefix |= pick[0] << shift;
-    pmask |= 255u << shift;
-    krem = pick[1];
-    __syncthreads();
-  }
-  const uint32_t thr = prefix;
-
-  // 4. tie resolution + compaction in channel order
-  uint32_t cgt = 0, ceq = 0;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if (j < n) {
-      cgt += key[j] > thr;
-      ceq += key[j] == thr;
-    }
-  }
-  uint32_t total;
-  const uint32_t eq_before = block_exclusive_scan(ceq, wtot, &total);
-  const uint32_t take_eq = (krem > eq_before) ? min(krem - eq_before, ceq) : 0u;
-  uint32_t pos = block_exclusive_scan(cgt + take_eq, wtot, &total);
-
-  uint8_t* flags = reinterpret_cast<uint8_t*>(lds_dyn);
-  IdxT* idx_row = idx + row * k;
-  uint32_t eq_seen = 0;
-#pragma unroll
-  for (int j = 0; j < ITEMS; ++j) {
-    if (j < n) {
-      bool sel = key[j] > thr;
-      if (key[j] == thr) {
-        sel = (eq_before + eq_seen) < krem;
-        ++eq_seen;
-      }
-      const int ch = beg + j;
-      if (sel) {
-        idx_row[pos] = static_cast<IdxT>(ch);
-        if (vals != nullptr) {
-          if (BF16) static_cast<uint16_t*>(vals)[row * k + pos] = static_cast<const uint16_t*>(src)[ch];
-          else static_cast<uint32_t*>(vals)[row * k + pos] = static_cast<const uint32_t*>(src)[ch];
-        }
-        ++pos;
-      }
-      flags[ch] = sel ? 1 : 0;
-    }
-  }
+  // 4. optional bit mask
   if (mask != nullptr) {
-    __syncthreads();
-    const int words = (inter + 31) / 32;
-    for (int w = tid; w < words; w += kTopkThreads) {
-      uint32_t bits = 0;
-      const int c0 = w * 32;
-      const int cn = min(32, inter - c0);
-      for (int b = 0; b < cn; ++b) bits |= static_cast<uint32_t>(flags[c0 + b]) << b;
-      mask[row * mask_ld + w] = bits;
+    uint32_t* mw = lds + select_lds_dwords<NW>();
+    for (int i = t; i < mwords; i += GT) mw[i] = 0;
+    if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+    const int sh = c0 & 31;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const uint32_t bits = take[d];
+      if (bits != 0u) {
+        const int word = (c0 + 32 * d) >> 5;
+        atomicOr(&mw[word], bits << sh);
+        if (sh != 0 && (bits >> (32 - sh)) != 0u) atomicOr(&mw[word + 1], bits >> (32 - sh));
+      }
     }
+    if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+    uint32_t* mask_row = mask + row * mask_ld;
+    for (int i = t; i < mwords; i += GT) mask_row[i] = mw[i];
   }
 }
 
-template <bool BF16, int ITEMS>
-int launch_topk_items(const void* scores, int64_t rows, int inter, int64_t ld, int k,
-                      int transform, void* vals, void* idx, int idx_dtype, uint32_t* mask,
-                      int64_t mask_ld, hipStream_t st) {
-  const size_t lds = static_cast<size_t>(inter) * (BF16 ? 2 : 4);
-  const dim3 grid(static_cast<unsigned>(rows)), block(kTopkThreads);
-  switch (idx_dtype) {
-    case MOC_I16:
-      topk_rows_kernel<BF16, ITEMS, int16_t><<<grid, block, lds, st>>>(
-          scores, ld, inter, k, transform, vals, static_cast<int16_t*>(idx), mask, mask_ld);
-      break;
-    case MOC_I32:
-      topk_rows_kernel<BF16, ITEMS, int32_t><<<grid, block, lds, st>>>(
-          scores, ld, inter, k, transform, vals, static_cast<int32_t*>(idx), mask, mask_ld);
-      break;
-    default:
-      topk_rows_kernel<BF16, ITEMS, int64_t><<<grid, block, lds, st>>>(
-          scores, ld, inter, k, transform, vals, static_cast<int64_t*>(idx), mask, mask_ld);
-      break;
-  }
+template <bool BF16, int NW, int L>
+int launch_topk_kernel(const void* scores, int64_t rows, int inter, int64_t ld, int k,
+                       int transform, void* vals, void* idx, int idx_dtype, uint32_t* mask,
+                       int64_t mask_ld, hipStream_t st) {
+  constexpr int esz = BF16 ? 2 : 4;
+  constexpr int rpw = topk_rows_per_wg<NW>();
+  const int mwords = (inter + 31) / 32;
+  const int sel_dwords = select_lds_dwords<NW>() + (mask != nullptr ? (mwords + 3) / 4 * 4 : 0) +
+                         (k + 1) / 2;
+  const int stage_dwords = 64 * NW * L * esz / 4;
+  const int group_dwords = (std::max(sel_dwords, stage_dwords) + 3) / 4 * 4;
+  const size_t lds = static_cast<size_t>(group_dwords) * 4 * rpw;
+  const int vec = (reinterpret_cast<uintptr_t>(scores) % 16 == 0 && (ld * esz) % 16 == 0) ? 1 : 0;
+  const dim3 grid(static_cast<unsigned>((rows + rpw - 1) / rpw)), block(64 * NW * rpw);
+  topk_rows_kernel<BF16, NW, L><<<grid, block, lds, st>>>(scores, ld, rows, inter, k, transform, vec,
+                                                          group_dwords, vals, idx, idx_dtype, mask,
+                                                          mask_ld);
   return check_launch("topk_rows_kernel");
 }
 
+// One wave per row while a thread's share fits 128 (f32) or 256 (bf16)
+// channels in registers; wider f32 rows use two waves per row.
 template <bool BF16>
 int launch_topk(const void* scores, int64_t rows, int inter, int64_t ld, int k, int transform,
                 void* vals, void* idx, int idx_dtype, uint32_t* mask, int64_t mask_ld,
                 hipStream_t st) {
-  const int chunk = (inter + kTopkThreads - 1) / kTopkThreads;
-  if (chunk <= 8)
-    return launch_topk_items<BF16, 8>(scores, rows, inter, ld, k, transform, vals, idx, idx_dtype, mask, mask_ld, st);
-  if (chunk <= 16)
-    return launch_topk_items<BF16, 16>(scores, rows, inter, ld, k, transform, vals, idx, idx_dtype, mask, mask_ld, st);
-  if (chunk <= 32)
-    return launch_topk_items<BF16, 32>(scores, rows, inter, ld, k, transform, vals, idx, idx_dtype, mask, mask_ld, st);
-  return launch_topk_items<BF16, 64>(scores, rows, inter, ld, k, transform, vals, idx, idx_dtype, mask, mask_ld, st);
+#define MOC_TOPK(NW, L) \
+  return launch_topk_kernel<BF16, NW, L>(scores, rows, inter, ld, k, transform, vals, idx, idx_dtype, mask, mask_ld, st)
+#define MOC_TOPK_L8(NW, per)                                             \
+  switch ((per + 7) / 8) {                                               \
+    case 1: MOC_TOPK(NW, 8);   case 2: MOC_TOPK(NW, 16);                 \
+    case 3: MOC_TOPK(NW, 24);  case 4: MOC_TOPK(NW, 32);                 \
+    case 5: MOC_TOPK(NW, 40);  case 6: MOC_TOPK(NW, 48);                 \
+    case 7: MOC_TOPK(NW, 56);  case 8: MOC_TOPK(NW, 64);                 \
+    case 9: MOC_TOPK(NW, 72);  case 10: MOC_TOPK(NW, 80);                \
+    case 11: MOC_TOPK(NW, 88); case 12: MOC_TOPK(NW, 96);                \
+    case 13: MOC_TOPK(NW, 104); case 14: MOC_TOPK(NW, 112);              \
+    case 15: MOC_TOPK(NW, 120); default: MOC_TOPK(NW, 128);              \
+  }
+  const int per1 = (inter + 63) / 64;
+  if (per1 <= 128) {
+    MOC_TOPK_L8(1, per1);
+  }
+  if constexpr (BF16) {
+    if (per1 <= 160) MOC_TOPK(1, 160);
+    if (per1 <= 192) MOC_TOPK(1, 192);
+    if (per1 <= 224) MOC_TOPK(1, 224);
+    MOC_TOPK(1, 256);
+  } else {
+    const int per2 = (inter + 127) / 128;
+    MOC_TOPK_L8(2, per2);
+  }
+#undef MOC_TOPK_L8
+#undef MOC_TOPK
 }
 
 // ---------------------------------------------------------------------------
