@@ -207,8 +207,7 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
     x = torch.randn(nb, d, device="cuda", generator=gen).to(torch.bfloat16)
     gate = [torch.empty(nb, inter, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
     ys = [torch.empty(nb, d, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
-    wsb = K.global_after_gate_workspace_bytes(nb, inter, k, d)
-    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    ws = K.global_after_gate_workspace(nb, inter, k, d, "cuda")
 
     def run_all():
         for (wg, wu, wdt), g, y in zip(layers, gate, ys):

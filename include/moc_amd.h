@@ -166,9 +166,13 @@ int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t 
                                              int64_t hidden);
 
 /* Global-MoC decode after the gate: Top-K of gate_scores[nb, inter], selected
- * Up * SiLU, selected Down -> y[nb, hidden]
+ * Up * SiLU, selected Down -> y[nb, hidden], in one kernel launch
  * (moc_native::optimized_global_after_gate_bf16, optimized_global_moc_ext.cu:
- * 457-540, optimized_global_moc_ext.cpp:61-76,92). */
+ * 457-540, optimized_global_moc_ext.cpp:61-76,92).
+ * The workspace starts with 64 KB of arrival counters that must be zero
+ * before the first call with that workspace (e.g. hipMemset once after
+ * allocation); every call, of any shape, leaves them zero again.  Calls
+ * sharing a workspace must not overlap. */
 int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
                                int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
                                void* y, void* workspace, int64_t workspace_bytes, void* stream);

@@ -58,21 +58,47 @@ __device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + ex
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// Wave64 reductions / scans through cross-lane shuffles.
+// Wave64 reductions / scans with DPP row operations (VALU, no LDS round
+// trip), rows of 16 lanes joined with row_bcast / readlane.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  // lanes whose source is outside the row, or in a masked row, read 0
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, BANK_MASK, true));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ uint32_t wave_read_lane(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
+// Sum over the 64 lanes, returned to every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror: every lane holds its row's sum
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Inclusive prefix sum over lanes 0..63 (Hillis-Steele within rows, then
+// row 0's total into row 1 and rows 0-1's total into rows 2-3).
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const uint32_t t = __shfl_up(v, off, kWave);
-    if (lane >= off) v += t;
-  }
+  v += dpp_u32<0x111>(v);       // row_shr:1
+  v += dpp_u32<0x112>(v);       // row_shr:2
+  v += dpp_u32<0x114>(v);       // row_shr:4
+  v += dpp_u32<0x118>(v);       // row_shr:8
+  v += dpp_u32<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_u32<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
   return v;
 }
 

@@ -3,17 +3,20 @@
 // memory latency: the gate projection streams all of W_gate, the selected
 // Up/Down kernels stream only the selected rows of W_up and W_down^T.
 //
-//  moc_gemv_bf16              gate projection G = x W_gate^T.  A workgroup
-//                             owns <= 32 consecutive rows, pulls all of them
-//                             into LDS with direct-to-LDS loads in one go
-//                             (every byte of its share in flight at once),
-//                             then runs MFMA 16x16x32 (tokens padded to 16)
-//  moc_global_after_gate_bf16 (1) select + Up: every workgroup of a token
-//                             recomputes the token's Top-K from G (radix
-//                             select in LDS, lower index on ties) and
-//                             computes z = bf16(bf16(SiLU(g)) bf16(x.W_up[c]))
-//                             for its own slice of the selected ranks;
-//                             (2) selected Down
+//  moc_gemv_bf16              gate projection G = x W_gate^T.  Up to 4
+//                             tokens: one wave per row, whole rows in flight,
+//                             f32 FMA.  More tokens: a workgroup owns <= 32
+//                             consecutive rows, pulls all of them into LDS
+//                             with direct-to-LDS loads in one go, then runs
+//                             MFMA 16x16x32 (tokens padded to 16)
+//  moc_global_after_gate_bf16 two launches: (1) one workgroup per token
+//                             ranks the token's Top-K from G (radix select,
+//                             lower index on ties); (2) every workgroup of a
+//                             token computes z = bf16(bf16(SiLU(g))
+//                             bf16(x.W_up[c])) for its slice of the ranks and
+//                             the Down contribution of that slice to its
+//                             column block; partials are added in a fixed
+//                             order by the last workgroup of each block
 //  moc_selected_down_bf16     y[b] = sum_j z[b,j] W_down^T[idx[b,j]]: a
 //                             workgroup per (64-column block, 128 selected
 //                             rows), 128-byte row segments, partial sums
@@ -229,91 +232,266 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// Select + Up.  Workgroup (b, p) of P per token: (1) token b's gate row as
-// order keys in registers (512 threads), (2) the k-th largest key and the
-// ranks of the selected channels in ascending channel order, ties toward
-// the lower index (select.h; the same rule and result as moc_topk_rows),
-// (3) for the ranks [p k / P, (p+1) k / P):
-// u = x_b . W_up[c] (one wave per channel, f32), z = bf16(bf16(SiLU(g)) *
-// bf16(u)); writes idx[b, rank] and z[b, rank].  Workgroup 0 also clears the
-// down kernel's arrival counters.
+// Gate GEMV for 1..4 tokens: one wave per row, the whole row requested at
+// once (lane l: 16-byte chunks l + 64 i), x in registers, f32 FMA dot
+// products and a wave reduction.  With ~one row per wave every byte of W is
+// in flight within one memory latency.
 // ---------------------------------------------------------------------------
-constexpr int kSelWaves = 8;
+template <int NB, int CHN>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                        const uint16_t* __restrict__ W, int64_t ldw,
+                                                        int rows, int hidden,
+                                                        uint16_t* __restrict__ y, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = hidden / 8;
+  uint4 wv[CHN];
+#pragma unroll
+  for (int i = 0; i < CHN; ++i) {
+    const int c = lane + 64 * i;
+    wv[i] = c < nch ? *reinterpret_cast<const uint4*>(W + static_cast<int64_t>(row) * ldw + c * 8)
+                    : make_uint4(0, 0, 0, 0);
+  }
+  float acc[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    acc[t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      const uint4 xv = c < nch ? *reinterpret_cast<const uint4*>(x + t * ldx + c * 8) : make_uint4(0, 0, 0, 0);
+      acc[t] = dot8(wv[i], xv, acc[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    const float tot = wave_sum(acc[t]);
+    if (lane == 0) y[t * ldy + row] = f32_to_bf16(tot);
+  }
+}
+
+template <int NB>
+void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, int rows, int hidden,
+                      void* y, int64_t ldy, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+  const int chn = (hidden / 8 + 63) / 64;
+#define MOC_GR(C)                                                                                 \
+  gemv_rows_kernel<NB, C><<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (const uint16_t*)W, ldw, \
+                                                   rows, hidden, (uint16_t*)y, ldy)
+  if (chn <= 1) MOC_GR(1);
+  else if (chn <= 2) MOC_GR(2);
+  else if (chn <= 4) MOC_GR(4);
+  else MOC_GR(8);
+#undef MOC_GR
+}
+
+// ---------------------------------------------------------------------------
+// Decode after the gate, two launches.
+//
+// select_list_kernel: one workgroup per token b.  Token b's gate row as order
+// keys in registers, the k-th largest key and the ranks of the selected
+// channels in ascending channel order, ties toward the lower index
+// (select.h; the same rule and result as moc_topk_rows).  Writes the ranked
+// list: channel ids and bf16(SiLU(g)) of the selected channels.
+//
+// up_down_kernel: workgroup (b, p, cb): token b, slice p of P of the k
+// ranks, column block cb of CB (CW = hidden / CB columns of y).
+//  (1) the W_down^T row segments [cb CW, cb CW + CW) of the slice's channels
+//      are requested first, then u = x_b . W_up[c] (whole rows, four
+//      channels in flight per wave) and z = bf16(bf16(SiLU(g)) * bf16(u));
+//  (2) the segment sums over the slice are written to part[b][p] with
+//      device-coherent stores; the last of the P workgroups of (b, cb) to
+//      arrive adds the P partials in a fixed order and writes y[b, cb CW ..].
+// The CB workgroups of one (b, p) are numbered nb P apart, so with nb P a
+// multiple of 8 they share an XCD (and its L2) and read the W_up rows they
+// all need from HBM once.  Arrival counters must be zero when a call starts;
+// every call leaves them zero.
+// ---------------------------------------------------------------------------
+constexpr int kSelWaves = 4;
 constexpr int kSelThreads = 64 * kSelWaves;
+constexpr int kSelCopies = 16;     // one workgroup per CU: LDS is plentiful
+constexpr int kUdThreads = 512;
+constexpr int kFusedMaxSel = 256;  // ranks per up_down workgroup (k / P)
+constexpr int kUpPerWave = 4;      // W_up rows in flight per wave
+constexpr int kDownBatch = 4;      // W_down^T segments in flight per thread
 
-// Thread t holds the gate keys of channels [t L, t L + L) (select.h).
 template <int L>
-__global__ __launch_bounds__(kSelThreads) void select_up_kernel(
-    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
-    int k, int P, const uint16_t* __restrict__ w_up, int32_t* __restrict__ idx_out,
-    uint16_t* __restrict__ z_out, int* __restrict__ cnt, int ncnt) {
-  extern __shared__ __attribute__((aligned(16))) char dyn[];
-  int* list_ch = reinterpret_cast<int*>(dyn);                        // [ceil(k/P)]
-  uint16_t* list_g = reinterpret_cast<uint16_t*>(list_ch + (k + P - 1) / P);
-  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves>()];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.x / P, p = blockIdx.x - b * P;
-  if (blockIdx.x == 0)
-    for (int i = tid; i < ncnt; i += kSelThreads) cnt[i] = 0;
-
-  // 1. token b's gate keys
+__global__ __launch_bounds__(kSelThreads) void select_list_kernel(
+    const uint16_t* __restrict__ gate, int inter, int k, int* __restrict__ list_ch,
+    float* __restrict__ list_sg) {
+  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves, kSelCopies>()];
+  __shared__ __attribute__((aligned(16))) uint32_t row_lds[kSelThreads * L / 2];  // raw row
+  extern __shared__ uint16_t ranked[];  // [k] selected channel ids in rank order
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
   const uint16_t* grow = gate + static_cast<int64_t>(b) * inter;
   const int c0 = tid * L;
   uint32_t w[sel_words<true, L>()];
-  load_row_raw<true, L>(grow, inter, c0, (reinterpret_cast<uintptr_t>(grow) & 15) == 0, w);
+  load_row_raw_staged<kSelWaves, true, L>(grow, inter, tid, (reinterpret_cast<uintptr_t>(grow) & 15) == 0,
+                                          row_lds, w, false);
   raw_to_keys<true, L>(inter, c0, 0, [](uint32_t r) { return r; }, w);
-
-  // 2. threshold, then this workgroup's ranks [p k / P, (p+1) k / P) of the
-  //    selected channels (channel order, ties toward the lower index)
   uint32_t thr, krem, take[(L + 31) / 32], first;
-  select_threshold<kSelWaves, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k), sel_lds, thr,
-                                                        krem);
-  select_ranks<kSelWaves, L, true>(w, thr, krem, sel_lds, take, first);
+  select_threshold<kSelWaves, kSelCopies, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k),
+                                                                    sel_lds, thr, krem);
+  select_ranks<kSelWaves, kSelCopies, L, true>(w, thr, krem, sel_lds, take, first);
+  select_emit<L>(take, c0, first, [&](int c, uint32_t pos) { ranked[pos] = static_cast<uint16_t>(c); });
+  __syncthreads();
+  // the list out coalesced, with bf16(SiLU(g)) from the staged row
+  const uint16_t* raw = reinterpret_cast<const uint16_t*>(row_lds);
+  for (int e = tid; e < k; e += kSelThreads) {
+    const int c = ranked[e];
+    list_ch[static_cast<int64_t>(b) * k + e] = c;
+    list_sg[static_cast<int64_t>(b) * k + e] = round_bf16(silu_f32(bf16_to_f32(raw[c])));
+  }
+}
+
+template <int CW>
+__global__ __launch_bounds__(kUdThreads) void up_down_kernel(
+    const uint16_t* __restrict__ x, int hidden, int k, int P, int CB,
+    const int* __restrict__ list_ch, const float* __restrict__ list_sg,
+    const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ wdt, float* __restrict__ part,
+    int* __restrict__ cnt, uint16_t* __restrict__ y) {
+  constexpr int QN = CW / 8;            // 16-byte chunks per row segment
+  constexpr int S = kUdThreads / QN;    // row segments summed in parallel
+  static_assert(S * QN == kUdThreads, "CW / 8 must divide the workgroup");
+  constexpr int NW = kUdThreads / 64;
+  __shared__ int sch[kFusedMaxSel];
+  __shared__ float sv[kFusedMaxSel];  // bf16(SiLU(g)), then z
+  __shared__ float red[S][CW + 1];
+  __shared__ int last;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbp = static_cast<int>(gridDim.x) / CB;
+  const int cb = static_cast<int>(blockIdx.x) / nbp, bp = static_cast<int>(blockIdx.x) - cb * nbp;
+  const int b = bp / P, p = bp - b * P;
   const int lo = static_cast<int>(static_cast<int64_t>(p) * k / P);
   const int hi = static_cast<int>(static_cast<int64_t>(p + 1) * k / P);
-  select_emit<L>(take, c0, first, [&](int c, uint32_t pos) {
-    if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) {
-      list_ch[pos - lo] = c;
-      list_g[pos - lo] = grow[c];
-    }
-  });
+  const int nsel = hi - lo;
+  for (int e = tid; e < nsel; e += kUdThreads) {
+    sch[e] = list_ch[static_cast<int64_t>(b) * k + lo + e];
+    sv[e] = list_sg[static_cast<int64_t>(b) * k + lo + e];
+  }
   __syncthreads();
 
-  // 3. selected Up * SiLU: one wave per channel, up to four channels in
-  //    flight per wave
-  const int cpr = hidden / 8;
-  const uint16_t* xb = x + static_cast<int64_t>(b) * hidden;
-  const int nsel = hi - lo;
-  for (int e0 = wave * 4; e0 < nsel; e0 += 4 * kSelWaves) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int c = lane; c < cpr; c += 64) {
-      const uint4 xv = *reinterpret_cast<const uint4*>(xb + c * 8);
-      uint4 wv[4];
+  // 1. first batch of W_down^T segments in flight, then selected Up * SiLU
+  const int q = tid % QN, sl = tid / QN;
+  const int col = cb * CW + q * 8;
+  uint4 dv[kDownBatch];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = e0 + u;
-        wv[u] = (e < nsel)
-                    ? *reinterpret_cast<const uint4*>(w_up + static_cast<int64_t>(list_ch[e]) * hidden + c * 8)
-                    : make_uint4(0, 0, 0, 0);
+  for (int j = 0; j < kDownBatch; ++j) {
+    const int e = sl + S * j;
+    dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+                     : make_uint4(0, 0, 0, 0);
+  }
+  const int nch = hidden / 8;
+  const uint16_t* xb = x + static_cast<int64_t>(b) * hidden;
+  for (int e0 = wave * kUpPerWave; e0 < nsel; e0 += kUpPerWave * NW) {
+    float acc[kUpPerWave] = {};
+    for (int cbase = 0; cbase < nch; cbase += 256) {
+      uint4 wv[kUpPerWave][4], xv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = cbase + lane + 64 * i;
+        xv[i] = c < nch ? *reinterpret_cast<const uint4*>(xb + c * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kUpPerWave; ++u) {
+          const int e = e0 + u;
+          wv[u][i] = (e < nsel && c < nch)
+                         ? *reinterpret_cast<const uint4*>(w_up + static_cast<int64_t>(sch[e]) * hidden + c * 8)
+                         : make_uint4(0, 0, 0, 0);
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] = dot8(wv[u], xv, acc[u]);
+      for (int u = 0; u < kUpPerWave; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[u] = dot8(wv[u][i], xv[i], acc[u]);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int e = e0 + u;
+    for (int u = 0; u < kUpPerWave; ++u) {
       const float tot = wave_sum(acc[u]);
-      if (lane == 0 && e < nsel) {
-        const int ch = list_ch[e];
-        const float uu = round_bf16(tot);
-        const float sg = round_bf16(silu_f32(bf16_to_f32(list_g[e])));
-        const int64_t o = static_cast<int64_t>(b) * k + lo + e;
-        idx_out[o] = ch;
-        z_out[o] = f32_to_bf16(sg * uu);
+      const int e = e0 + u;
+      if (lane == 0 && e < nsel) sv[e] = round_bf16(sv[e] * round_bf16(tot));
+    }
+  }
+  __syncthreads();
+
+  // 2. segment sums of z_e W_down^T[c_e, col .. col + 8) over this slot's e
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int e0 = 0; e0 < nsel; e0 += S * kDownBatch) {
+    if (e0 > 0) {
+#pragma unroll
+      for (int j = 0; j < kDownBatch; ++j) {
+        const int e = e0 + sl + S * j;
+        dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+                         : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kDownBatch; ++j) {
+      const int e = e0 + sl + S * j;
+      const float zz = e < nsel ? sv[e] : 0.f;
+      const uint32_t a[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = fmaf(zz, __uint_as_float(a[i] << 16), acc[2 * i]);
+        acc[2 * i + 1] = fmaf(zz, __uint_as_float(a[i] & 0xFFFF0000u), acc[2 * i + 1]);
       }
     }
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[sl][q * 8 + i] = acc[i];
+  __syncthreads();
+  // Partials go through to the device-coherent level (agent-scope atomic
+  // stores) and are waited for before the arrival count is bumped; the last
+  // workgroup reads them back with agent-scope loads.
+  if (tid < CW) {
+    float t = 0.f;
+    for (int r = 0; r < S; ++r) t += red[r][tid];
+    __hip_atomic_store(part + static_cast<int64_t>(bp) * hidden + cb * CW + tid, t, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&cnt[b * CB + cb], 1);
+    last = (prev == P - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  // Thread (g, c) of G = 512 / CW groups sums partials p = g, g + G, ...
+  // of column c, 16 independent loads in flight at a time; the G group sums
+  // are then added in group order.
+  {
+    constexpr int G = kUdThreads / CW;
+    constexpr int kLoads = 16;
+    const int c = tid % CW, g = tid / CW;
+    const float* p0 = part + static_cast<int64_t>(b) * P * hidden + cb * CW + c;
+    float t = 0.f;
+    for (int pi0 = g; pi0 < P; pi0 += G * kLoads) {
+      float v[kLoads];
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) {
+        const int pi = pi0 + G * u;
+        v[u] = pi < P ? __hip_atomic_load(p0 + static_cast<int64_t>(pi) * hidden, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kLoads; ++u) t += v[u];
+    }
+    reinterpret_cast<float*>(red)[tid] = t;  // red holds S (CW + 1) >= 512 floats
+  }
+  __syncthreads();
+  if (tid < CW) {
+    constexpr int G = kUdThreads / CW;
+    const float* flat = reinterpret_cast<const float*>(red);
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) t += flat[g * CW + tid];
+    y[static_cast<int64_t>(b) * hidden + cb * CW + tid] = f32_to_bf16(t);
+  }
+  if (tid == 0) cnt[b * CB + cb] = 0;  // ready for the next call
 }
 
 // ---------------------------------------------------------------------------
@@ -473,25 +651,40 @@ int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t 
   return check_launch("selected_down_kernel");
 }
 
-template <int L>
-void launch_select_up_l(const void* x, int hidden, const void* gate, int inter, int k, int nb,
-                        int P, const void* w_up, int32_t* idx, uint16_t* z, int* cnt, int ncnt,
-                        hipStream_t st) {
-  const int per = (k + P - 1) / P;
-  const size_t lds = static_cast<size_t>(per) * 6;
-  select_up_kernel<L><<<dim3(static_cast<unsigned>(nb * P)), kSelThreads, lds, st>>>(
-      (const uint16_t*)x, hidden, (const uint16_t*)gate, inter, k, P, (const uint16_t*)w_up, idx,
-      z, cnt, ncnt);
+// up_down launch shape: CW = 256 columns per block when hidden allows (else
+// 64), P (a power of two, <= k, with k / P <= kFusedMaxSel) rank slices so
+// that nb P CB is about 512 workgroups (two per CU).
+struct FusedShape {
+  int CW, CB, P;
+};
+
+inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
+  FusedShape f;
+  f.CW = (hidden % 256 == 0) ? 256 : 64;
+  f.CB = static_cast<int>(hidden / f.CW);
+  int64_t P = 512 / (nb * f.CB);
+  int64_t p2 = 1;
+  while (p2 * 2 <= P) p2 *= 2;
+  P = p2 < 1 ? 1 : p2;
+  while ((k + P - 1) / P > kFusedMaxSel) P *= 2;
+  if (P > k) P = k;
+  f.P = static_cast<int>(P);
+  return f;
 }
 
-void launch_select_up(const void* x, int hidden, const void* gate, int inter, int k, int nb, int P,
-                      const void* w_up, int32_t* idx, uint16_t* z, int* cnt, int ncnt,
-                      hipStream_t st) {
+void launch_select_list(const void* gate, int inter, int k, int nb, int* list_ch, float* list_sg,
+                        hipStream_t st) {
   const int per = (inter + kSelThreads - 1) / kSelThreads;
-  if (per <= 8) launch_select_up_l<8>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
-  else if (per <= 16) launch_select_up_l<16>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
-  else if (per <= 24) launch_select_up_l<24>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
-  else launch_select_up_l<32>(x, hidden, gate, inter, k, nb, P, w_up, idx, z, cnt, ncnt, st);
+  const dim3 grid(static_cast<unsigned>(nb)), block(kSelThreads);
+#define MOC_SL(N) \
+  select_list_kernel<N><<<grid, block, static_cast<size_t>(k) * 2, st>>>((const uint16_t*)gate, inter, k, list_ch, list_sg)
+  if (per <= 8) MOC_SL(8);
+  else if (per <= 16) MOC_SL(16);
+  else if (per <= 24) MOC_SL(24);
+  else if (per <= 32) MOC_SL(32);
+  else if (per <= 48) MOC_SL(48);
+  else MOC_SL(64);
+#undef MOC_SL
 }
 
 }  // namespace
@@ -511,6 +704,15 @@ extern "C" int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void*
   MOC_REQUIRE(x && W && y, "moc_gemv_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(W), "moc_gemv_bf16: x and W must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
+  if (nb <= 4 && hidden <= 4096) {
+    switch (nb) {
+      case 1: launch_gemv_rows<1>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
+      case 2: launch_gemv_rows<2>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
+      case 3: launch_gemv_rows<3>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
+      default: launch_gemv_rows<4>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
+    }
+    return check_launch("gemv_rows_kernel");
+  }
   const int64_t wbytes = rows * ldw * 2;
   const int64_t max_rows = kGvLdsBytes / (2 * hidden);
   if (hidden % 128 == 0 && hidden <= kGvMaxHidden && max_rows >= 16 &&
@@ -583,10 +785,16 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
                               as_stream(stream));
 }
 
+// Workspace: a fixed 64 KB block of arrival counters (so the counters of one
+// call shape never overlap other data of another shape that reuses the
+// workspace), the ranked lists (channel ids, bf16(SiLU(g))), the partials.
+constexpr int64_t kFusedCounterBytes = 64 * 1024;
+
 extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t k,
                                                         int64_t hidden) {
-  if (nb <= 0 || k <= 0 || hidden <= 0 || inter <= 0) return 0;
-  return align256(nb * k * 4) + align256(nb * k * 2) + moc_selected_down_workspace_size(nb, k, hidden);
+  if (nb <= 0 || k <= 0 || hidden < 64 || inter <= 0) return 0;
+  const FusedShape f = fused_shape(nb, k, hidden);
+  return kFusedCounterBytes + 2 * align256(nb * k * 4) + nb * f.P * hidden * 4;
 }
 
 extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
@@ -605,20 +813,28 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
   const int64_t need = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_global_after_gate_bf16: workspace of %lld bytes required", (long long)need);
+  const FusedShape f = fused_shape(nb, k, hidden);
+  MOC_REQUIRE(nb * f.CB * 4 <= kFusedCounterBytes, "moc_global_after_gate_bf16: hidden too large");
   char* ws = static_cast<char*>(workspace);
-  int32_t* idx = reinterpret_cast<int32_t*>(ws);
+  int* cnt = reinterpret_cast<int*>(ws);
+  ws += kFusedCounterBytes;
+  int* list_ch = reinterpret_cast<int*>(ws);
   ws += align256(nb * k * 4);
-  uint16_t* z = reinterpret_cast<uint16_t*>(ws);
-  ws += align256(nb * k * 2);
-  const DownWs w = down_ws(nb, k, hidden);
-  int* cnt = reinterpret_cast<int*>(ws + w.part_bytes);
-  const int ncnt = static_cast<int>(nb * (hidden / 64));
+  float* list_sg = reinterpret_cast<float*>(ws);
+  ws += align256(nb * k * 4);
+  float* part = reinterpret_cast<float*>(ws);
   hipStream_t st = as_stream(stream);
-  int P = static_cast<int>(256 / nb);
-  if (P > k) P = static_cast<int>(k);
-  launch_select_up(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, P, w_up, idx, z, cnt,
-                   ncnt, st);
-  int rc = check_launch("select_up_kernel");
+  launch_select_list(gate_scores, (int)inter, (int)k, (int)nb, list_ch, list_sg, st);
+  int rc = check_launch("select_list_kernel");
   if (rc != MOC_OK) return rc;
-  return launch_selected_down(z, idx, MOC_I32, nb, k, w_down_t, inter, hidden, y, ws, st);
+  const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
+  if (f.CW == 256)
+    up_down_kernel<256><<<grid, block, 0, st>>>((const uint16_t*)x, (int)hidden, (int)k, f.P, f.CB,
+                                                 list_ch, list_sg, (const uint16_t*)w_up,
+                                                 (const uint16_t*)w_down_t, part, cnt, (uint16_t*)y);
+  else
+    up_down_kernel<64><<<grid, block, 0, st>>>((const uint16_t*)x, (int)hidden, (int)k, f.P, f.CB,
+                                                list_ch, list_sg, (const uint16_t*)w_up,
+                                                (const uint16_t*)w_down_t, part, cnt, (uint16_t*)y);
+  return check_launch("up_down_kernel");
 }

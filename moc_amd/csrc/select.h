@@ -12,14 +12,16 @@
 // select_threshold finds the k-th largest key T and how many T-valued
 // channels still have to be taken (krem) by an MSB-first radix select with
 // 8-bit digits (2 passes over the registers for 16-bit keys, 4 for 32-bit).
-// Each wave counts into its own 256-bin histogram in LDS, kept in four
-// copies (lane % 4 picks the copy) so that lanes hitting the same bin
-// collide four times less.  A key whose higher digits do not match the
-// prefix found so far is counted into one of 16 spare bins instead (a
-// branch-free unsigned min), so no pass needs a compare per key.  A wave's
-// LDS operations execute in program order, so a wave needs no barrier to
-// read back its own counts; with NW > 1 the NW wave histograms meet in a
-// double-buffered table behind one barrier per digit.
+// The group counts into one 256-bin LDS histogram kept in C copies (lane % C
+// picks the copy): LDS atomics serialise on lanes of one instruction that
+// hit the same address, and real scores pile into a few exponent bins, so
+// 16 copies make an atomic about twice as fast as 4 (at four times the
+// LDS to clear and read back).  A key
+// whose higher digits do not match the prefix found so far is counted into
+// a spare bin of its lane instead (a branch-free unsigned min), so no pass
+// needs a compare per key.  With NW = 1 the wave's own program order orders
+// its LDS operations; with NW > 1 workgroup barriers separate clearing,
+// counting and reading.
 //
 // select_ranks turns T into per-thread bit masks of the selected channels:
 // every channel above T, and the krem lowest-index T-valued channels (the
@@ -37,14 +39,18 @@ typedef unsigned short sel_u16x2 __attribute__((ext_vector_type(2)));
 typedef short sel_s16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kSelBins = 256;
-constexpr int kSelSpare = 16;                                // bins for keys off the prefix
-constexpr int kSelCopyPitch = kSelBins + kSelSpare + 1;      // dwords per histogram copy
-constexpr int kSelWaveHist = 4 * kSelCopyPitch;
+
+// Histogram layout for C copies (lane % C picks the copy): 256 bins, one
+// spare bin per lane sharing the copy, one pad dword.
+template <int C>
+constexpr int sel_copy_pitch() {
+  return kSelBins + 64 / C + 1;
+}
 
 // LDS dwords the selection of a group of NW waves needs.
-template <int NW>
+template <int NW, int C>
 constexpr int select_lds_dwords() {
-  return NW * kSelWaveHist + (NW > 1 ? 2 * NW * kSelBins + NW : 0);
+  return C * sel_copy_pitch<C>() + (NW > 1 ? NW : 0);
 }
 
 // Order keys of two packed bf16 values: 0x8000 + |v| for v >= 0 (and -0),
@@ -138,11 +144,12 @@ __device__ __forceinline__ void load_row_raw(const void* src, int n, int c0, boo
 // reads its own L channels back with 16-byte LDS reads.  Used where a
 // thread's share is long: direct loads of long per-thread runs touch every
 // cache line from many load instructions.  stage may alias the select's
-// histograms: the last barrier here orders the reads before their reuse.
+// histograms: with reuse, a last barrier orders the reads before that.
 template <int NW, bool BF16, int L>
 __device__ __forceinline__ void load_row_raw_staged(const void* src, int n, int t, bool vec,
                                                     uint32_t* stage,
-                                                    uint32_t (&w)[sel_words<BF16, L>()]) {
+                                                    uint32_t (&w)[sel_words<BF16, L>()],
+                                                    bool reuse = true) {
   constexpr int GT = 64 * NW;
   constexpr int EPC = BF16 ? 8 : 4;        // elements per 16 bytes
   constexpr int CPT = L / EPC;             // 16-byte chunks per thread
@@ -198,7 +205,9 @@ __device__ __forceinline__ void load_row_raw_staged(const void* src, int n, int 
     w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
   }
   (void)ESZ;
-  if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+  if (reuse) {
+    if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+  }
 }
 
 // Raw scores in w (channels [c0, c0 + L)) -> order keys, key 0 past n.
@@ -241,27 +250,30 @@ __device__ __forceinline__ void raw_to_keys(int n, int c0, int transform, KeyOf 
   }
 }
 
-template <int NW, int W, int KEY_BITS>
+template <int NW, int C, int W, int KEY_BITS>
 __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_t k,
-                                                 uint32_t* lds, uint32_t& thr, uint32_t& krem) {
+                                                 uint32_t* hist, uint32_t& thr, uint32_t& krem) {
+  static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 histogram copies");
+  constexpr int kPitch = sel_copy_pitch<C>();
+  constexpr int kHist = C * kPitch;
   const int t = (NW > 1) ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x & 63);
-  const int lane = t & 63, wave = t >> 6;
-  uint32_t* hist = lds + wave * kSelWaveHist;
-  uint32_t* mine = hist + (lane & 3) * kSelCopyPitch;
-  uint32_t* wtab = lds + NW * kSelWaveHist;  // [2][NW][256], only for NW > 1
-  const uint32_t spare = kSelBins + (lane >> 2);  // this lane's spare bin
+  const int lane = t & 63;
+  uint32_t* mine = hist + (lane % C) * kPitch;
+  const uint32_t spare = kSelBins + lane / C;  // this lane's spare bin in its copy
+  auto group_sync = [] {
+    if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
+  };
   uint32_t prefix = 0;
   krem = k;
 #pragma unroll
   for (int pass = 0; pass < KEY_BITS / 8; ++pass) {
     const int shift = KEY_BITS - 8 * (pass + 1);
     const uint32_t phi = (pass == 0) ? 0u : prefix >> (shift + 8);
-#pragma unroll
-    for (int i = 0; i < (kSelWaveHist + 63) / 64; ++i)
-      if (lane + 64 * i < kSelWaveHist) hist[lane + 64 * i] = 0;
-    __builtin_amdgcn_wave_barrier();
+    if (pass > 0) group_sync();  // every wave is done reading the last counts
+    for (int i = t; i < kHist; i += 64 * NW) hist[i] = 0;
+    group_sync();
     auto bump = [&](uint32_t bin) {
-      __hip_atomic_fetch_add(&mine[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+      __hip_atomic_fetch_add(&mine[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     };
 #pragma unroll
     for (int j = 0; j < W; ++j) {
@@ -282,45 +294,39 @@ __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_
         bump(pass == 0 ? x : min(x, spare));
       }
     }
-    __builtin_amdgcn_wave_barrier();
-    // lane l owns bins 255 - 4 l - m (m = 0..3): descending bins in lane order
-    uint32_t s[4];
+    group_sync();
+    // lane l owns bins 255 - 64 m - l (m = 0..3): every m a run of 64
+    // descending bins in lane order, so the reads are bank-conflict free
+    uint32_t s[4], ge[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const int bin = kSelBins - 1 - 4 * lane - m;
-      s[m] = hist[bin] + hist[kSelCopyPitch + bin] + hist[2 * kSelCopyPitch + bin] +
-             hist[3 * kSelCopyPitch + bin];
+      const int bin = kSelBins - 1 - 64 * m - lane;
+      uint32_t v = 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) v += hist[c * kPitch + bin];
+      s[m] = v;
     }
-    if constexpr (NW > 1) {
-      uint32_t* tab = wtab + (pass & 1) * NW * kSelBins;
+    // keys in bins >= bin
+    uint32_t base = 0;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) tab[wave * kSelBins + 4 * lane + m] = s[m];
-      __syncthreads();
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        s[m] = 0;
-#pragma unroll
-        for (int q = 0; q < NW; ++q) s[m] += tab[q * kSelBins + 4 * lane + m];
-      }
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t incl = wave_inclusive_scan(s[m]);
+      ge[m] = base + incl;
+      base += wave_read_lane(incl, 63);
     }
-    __builtin_amdgcn_wave_barrier();
-    // keys in bins >= bin: scan over lanes, then within the lane
-    const uint32_t tot = s[0] + s[1] + s[2] + s[3];
-    uint32_t ge = wave_inclusive_scan(tot) - tot;
     int hit_m = -1;
     uint32_t hit_gt = 0;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      const uint32_t gt = ge;
-      ge += s[m];
-      if (gt < krem && ge >= krem) {
+      const uint32_t gt = ge[m] - s[m];
+      if (gt < krem && ge[m] >= krem) {
         hit_m = m;
         hit_gt = gt;
       }
     }
     const int src = __ffsll(static_cast<unsigned long long>(__ballot(hit_m >= 0))) - 1;
-    const uint32_t pb = static_cast<uint32_t>(kSelBins - 1 - 4 * src - __shfl(hit_m, src, 64));
-    krem -= __shfl(hit_gt, src, 64);
+    const uint32_t pb = kSelBins - 1 - 64 * wave_read_lane(static_cast<uint32_t>(hit_m), src) - src;
+    krem -= wave_read_lane(hit_gt, src);
     prefix |= pb << shift;
   }
   thr = prefix;
@@ -329,7 +335,7 @@ __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_
 // take[d] bit i: channel c0 + 32 d + i is selected; first: rank of the
 // thread's first selected channel.  With NW > 1 this uses the table behind
 // the histograms and one workgroup barrier.
-template <int NW, int L, bool BF16>
+template <int NW, int C, int L, bool BF16>
 __device__ __forceinline__ void select_ranks(const uint32_t (&w)[sel_words<BF16, L>()],
                                              uint32_t thr, uint32_t krem, uint32_t* lds,
                                              uint32_t (&take)[(L + 31) / 32], uint32_t& first) {
@@ -355,7 +361,7 @@ __device__ __forceinline__ void select_ranks(const uint32_t (&w)[sel_words<BF16,
   uint32_t ex = incl - v;
   if constexpr (NW > 1) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t* tab = lds + NW * kSelWaveHist + 2 * NW * kSelBins;
+    uint32_t* tab = lds + C * sel_copy_pitch<C>();
     if (lane == 63) tab[wave] = incl;
     __syncthreads();
     for (int q = 0; q < wave; ++q) ex += tab[q];

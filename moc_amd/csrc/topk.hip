@@ -33,6 +33,9 @@ namespace {
 
 constexpr int kTopkThreads = 256;
 constexpr int kMaxTopkInter = 16384;
+// Histogram copies: 4 keeps a row's LDS small enough for three workgroups
+// per CU, which beats the cheaper atomics of more copies here.
+constexpr int kTopkCopies = 4;
 
 // Order key of a raw score (bf16 or f32 bits); transform 1 ranks by
 // |SiLU(g)| rounded to the score dtype (moc/ffn.py:335).
@@ -92,14 +95,14 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
 
   // 2. threshold and the selected channels of this thread
   uint32_t thr, krem, take[D], first;
-  select_threshold<NW, sel_words<BF16, L>(), BF16 ? 16 : 32>(w, static_cast<uint32_t>(k), lds,
+  select_threshold<NW, kTopkCopies, sel_words<BF16, L>(), BF16 ? 16 : 32>(w, static_cast<uint32_t>(k), lds,
                                                              thr, krem);
-  select_ranks<NW, L, BF16>(w, thr, krem, lds, take, first);
+  select_ranks<NW, kTopkCopies, L, BF16>(w, thr, krem, lds, take, first);
 
   // 3. selected channels in channel order: ids into the group's LDS list
   //    (rank order), then out to HBM coalesced, with values and the index
   //    type conversion
-  uint16_t* list = reinterpret_cast<uint16_t*>(lds + select_lds_dwords<NW>() + mask_dwords);
+  uint16_t* list = reinterpret_cast<uint16_t*>(lds + select_lds_dwords<NW, kTopkCopies>() + mask_dwords);
   select_emit<L>(take, c0, first, [&](int c, uint32_t pos) { list[pos] = static_cast<uint16_t>(c); });
   if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
   using KT = typename std::conditional<BF16, uint16_t, uint32_t>::type;
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
 
   // 4. optional bit mask
   if (mask != nullptr) {
-    uint32_t* mw = lds + select_lds_dwords<NW>();
+    uint32_t* mw = lds + select_lds_dwords<NW, kTopkCopies>();
     for (int i = t; i < mwords; i += GT) mw[i] = 0;
     if constexpr (NW > 1) __syncthreads(); else __builtin_amdgcn_wave_barrier();
     const int sh = c0 & 31;
@@ -144,7 +147,7 @@ int launch_topk_kernel(const void* scores, int64_t rows, int inter, int64_t ld, 
   constexpr int esz = BF16 ? 2 : 4;
   constexpr int rpw = topk_rows_per_wg<NW>();
   const int mwords = (inter + 31) / 32;
-  const int sel_dwords = select_lds_dwords<NW>() + (mask != nullptr ? (mwords + 3) / 4 * 4 : 0) +
+  const int sel_dwords = select_lds_dwords<NW, kTopkCopies>() + (mask != nullptr ? (mwords + 3) / 4 * 4 : 0) +
                          (k + 1) / 2;
   const int stage_dwords = 64 * NW * L * esz / 4;
   const int group_dwords = (std::max(sel_dwords, stage_dwords) + 3) / 4 * 4;

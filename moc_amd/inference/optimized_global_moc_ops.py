@@ -38,8 +38,7 @@ def make_optimized_global_moc_graph_runner(module, batch_size: int = 1):
     x_buf = torch.zeros(batch_size, hidden, device=device, dtype=dtype)
     gate_buf = torch.empty(batch_size, inter, device=device, dtype=dtype)
     y_buf = torch.empty(batch_size, hidden, device=device, dtype=dtype)
-    ws = torch.empty(max(1, K.global_after_gate_workspace_bytes(batch_size, inter, k, hidden)),
-                     dtype=torch.uint8, device=device)
+    ws = K.global_after_gate_workspace(batch_size, inter, k, hidden, device)
     up_w = module.up_proj.weight.contiguous()
     down_t = module._down_weight_t.contiguous()
     gate_w = module.gate_proj.weight.contiguous()

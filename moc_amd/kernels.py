@@ -304,6 +304,28 @@ def global_after_gate_workspace_bytes(nb: int, inter: int, k: int, hidden: int) 
     return N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
 
 
+_WS_CACHE: dict = {}
+
+
+def _decode_workspace(device, nbytes: int) -> torch.Tensor:
+    """A zero-initialised workspace per device, grown on demand.  The decode
+    kernel's arrival counters must start at zero and every call leaves them
+    zero, so the buffer is reused without clearing (calls on one device must
+    not overlap)."""
+    key = (device.type, device.index)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros((max(nbytes, 256),), dtype=torch.uint8, device=device)
+        _WS_CACHE[key] = ws
+    return ws
+
+
+def global_after_gate_workspace(nb: int, inter: int, k: int, hidden: int, device) -> torch.Tensor:
+    """A fresh zero-initialised workspace for global_after_gate."""
+    nbytes = global_after_gate_workspace_bytes(nb, inter, k, hidden)
+    return torch.zeros((max(nbytes, 256),), dtype=torch.uint8, device=device)
+
+
 def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, workspace=None,
                       out=None) -> torch.Tensor:
     N.require_device(x, gate_scores, up_weight, down_weight_t)
@@ -314,8 +336,10 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
         raise ValueError("up_weight and down_weight_t must be [intermediate, hidden]")
     y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
     ws_bytes = N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
-    if workspace is None or workspace.numel() < ws_bytes:
-        workspace = _empty((max(ws_bytes, 1),), torch.uint8, x.device)
+    if workspace is None:
+        workspace = _decode_workspace(x.device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"global_after_gate: workspace of {ws_bytes} bytes required")
     N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
            wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), workspace.data_ptr(), ws_bytes,
            N.stream_of(x))

@@ -243,7 +243,8 @@ def test_global_decode_path_1b(nb):
     close(y, O.selected_down(z.cpu(), idx_ref, wd.t().contiguous()), rtol=1e-2, atol=1e-3)
     y2 = K().global_after_gate(xd, G, wud, wdt, k)
     close(y2, y_ref)
-    close(y2, y, rtol=0, atol=0)
+    # the fused path sums the same f32 products in another order
+    close(y2, y, rtol=1e-2, atol=1e-3)
 
 
 def test_grouped_2of8_integer_inputs_bitexact():
