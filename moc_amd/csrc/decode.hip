@@ -9,10 +9,9 @@
 //                             consecutive rows, pulls all of them into LDS
 //                             with direct-to-LDS loads in one go, then runs
 //                             MFMA 16x16x32 (tokens padded to 16)
-//  moc_global_after_gate_bf16 two launches: (1) one workgroup per token
-//                             ranks the token's Top-K from G (radix select,
-//                             lower index on ties); (2) every workgroup of a
-//                             token computes z = bf16(bf16(SiLU(g))
+//  moc_global_after_gate_bf16 one launch: every workgroup of a token ranks
+//                             the token's Top-K from G (radix select, lower
+//                             index on ties), computes z = bf16(bf16(SiLU(g))
 //                             bf16(x.W_up[c])) for its slice of the ranks and
 //                             the Down contribution of that slice to its
 //                             column block; partials are added in a fixed
@@ -287,16 +286,15 @@ void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, in
 }
 
 // ---------------------------------------------------------------------------
-// Decode after the gate, two launches.
-//
-// select_list_kernel: one workgroup per token b.  Token b's gate row as order
-// keys in registers, the k-th largest key and the ranks of the selected
-// channels in ascending channel order, ties toward the lower index
-// (select.h; the same rule and result as moc_topk_rows).  Writes the ranked
-// list: channel ids and bf16(SiLU(g)) of the selected channels.
-//
-// up_down_kernel: workgroup (b, p, cb): token b, slice p of P of the k
-// ranks, column block cb of CB (CW = hidden / CB columns of y).
+// Decode after the gate, one launch.  Workgroup (b, p, cb): token b, slice p
+// of P of the k selected ranks, column block cb of CB (CW = hidden / CB
+// columns of y); about one workgroup per CU.
+//  (0) token b's gate row, staged in LDS, as order keys in registers; the
+//      k-th largest key and the ranks of the selected channels in ascending
+//      channel order, ties toward the lower index (select.h; the same rule
+//      and result as moc_topk_rows).  Every workgroup of the token ranks the
+//      row itself (cheaper than a separate launch plus a round trip through
+//      HBM) and keeps its ranks [p k / P, (p+1) k / P);
 //  (1) the W_down^T row segments [cb CW, cb CW + CW) of the slice's channels
 //      are requested first, then u = x_b . W_up[c] (whole rows, four
 //      channels in flight per wave) and z = bf16(bf16(SiLU(g)) * bf16(u));
@@ -308,54 +306,24 @@ void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, in
 // all need from HBM once.  Arrival counters must be zero when a call starts;
 // every call leaves them zero.
 // ---------------------------------------------------------------------------
-constexpr int kSelWaves = 4;
-constexpr int kSelThreads = 64 * kSelWaves;
-constexpr int kSelCopies = 16;     // one workgroup per CU: LDS is plentiful
 constexpr int kUdThreads = 512;
-constexpr int kFusedMaxSel = 256;  // ranks per up_down workgroup (k / P)
+constexpr int kSelWaves = kUdThreads / 64;
+constexpr int kSelCopies = 8;
+constexpr int kFusedMaxSel = 256;  // ranks per workgroup (k / P)
 constexpr int kUpPerWave = 4;      // W_up rows in flight per wave
 constexpr int kDownBatch = 4;      // W_down^T segments in flight per thread
 
-template <int L>
-__global__ __launch_bounds__(kSelThreads) void select_list_kernel(
-    const uint16_t* __restrict__ gate, int inter, int k, int* __restrict__ list_ch,
-    float* __restrict__ list_sg) {
-  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves, kSelCopies>()];
-  __shared__ __attribute__((aligned(16))) uint32_t row_lds[kSelThreads * L / 2];  // raw row
-  extern __shared__ uint16_t ranked[];  // [k] selected channel ids in rank order
-  const int tid = threadIdx.x;
-  const int b = blockIdx.x;
-  const uint16_t* grow = gate + static_cast<int64_t>(b) * inter;
-  const int c0 = tid * L;
-  uint32_t w[sel_words<true, L>()];
-  load_row_raw_staged<kSelWaves, true, L>(grow, inter, tid, (reinterpret_cast<uintptr_t>(grow) & 15) == 0,
-                                          row_lds, w, false);
-  raw_to_keys<true, L>(inter, c0, 0, [](uint32_t r) { return r; }, w);
-  uint32_t thr, krem, take[(L + 31) / 32], first;
-  select_threshold<kSelWaves, kSelCopies, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k),
-                                                                    sel_lds, thr, krem);
-  select_ranks<kSelWaves, kSelCopies, L, true>(w, thr, krem, sel_lds, take, first);
-  select_emit<L>(take, c0, first, [&](int c, uint32_t pos) { ranked[pos] = static_cast<uint16_t>(c); });
-  __syncthreads();
-  // the list out coalesced, with bf16(SiLU(g)) from the staged row
-  const uint16_t* raw = reinterpret_cast<const uint16_t*>(row_lds);
-  for (int e = tid; e < k; e += kSelThreads) {
-    const int c = ranked[e];
-    list_ch[static_cast<int64_t>(b) * k + e] = c;
-    list_sg[static_cast<int64_t>(b) * k + e] = round_bf16(silu_f32(bf16_to_f32(raw[c])));
-  }
-}
-
-template <int CW>
-__global__ __launch_bounds__(kUdThreads) void up_down_kernel(
-    const uint16_t* __restrict__ x, int hidden, int k, int P, int CB,
-    const int* __restrict__ list_ch, const float* __restrict__ list_sg,
-    const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ wdt, float* __restrict__ part,
-    int* __restrict__ cnt, uint16_t* __restrict__ y) {
+template <int L, int CW>
+__global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
+    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
+    int k, int P, int CB, const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ wdt,
+    float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y) {
   constexpr int QN = CW / 8;            // 16-byte chunks per row segment
   constexpr int S = kUdThreads / QN;    // row segments summed in parallel
   static_assert(S * QN == kUdThreads, "CW / 8 must divide the workgroup");
   constexpr int NW = kUdThreads / 64;
+  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves, kSelCopies>()];
+  __shared__ __attribute__((aligned(16))) uint32_t row_lds[kUdThreads * L / 2];  // raw gate row
   __shared__ int sch[kFusedMaxSel];
   __shared__ float sv[kFusedMaxSel];  // bf16(SiLU(g)), then z
   __shared__ float red[S][CW + 1];
@@ -368,9 +336,27 @@ __global__ __launch_bounds__(kUdThreads) void up_down_kernel(
   const int lo = static_cast<int>(static_cast<int64_t>(p) * k / P);
   const int hi = static_cast<int>(static_cast<int64_t>(p + 1) * k / P);
   const int nsel = hi - lo;
-  for (int e = tid; e < nsel; e += kUdThreads) {
-    sch[e] = list_ch[static_cast<int64_t>(b) * k + lo + e];
-    sv[e] = list_sg[static_cast<int64_t>(b) * k + lo + e];
+
+  // 0. selection; this workgroup's ranks [lo, hi)
+  {
+    const uint16_t* grow = gate + static_cast<int64_t>(b) * inter;
+    const int c0 = tid * L;
+    uint32_t w[sel_words<true, L>()];
+    load_row_raw_staged<kSelWaves, true, L>(grow, inter, tid,
+                                            (reinterpret_cast<uintptr_t>(grow) & 15) == 0, row_lds, w,
+                                            false);
+    raw_to_keys<true, L>(inter, c0, 0, [](uint32_t r) { return r; }, w);
+    uint32_t thr, krem, take[(L + 31) / 32], first;
+    select_threshold<kSelWaves, kSelCopies, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k),
+                                                                      sel_lds, thr, krem);
+    select_ranks<kSelWaves, kSelCopies, L, true>(w, thr, krem, sel_lds, take, first);
+    const uint16_t* raw = reinterpret_cast<const uint16_t*>(row_lds);
+    select_emit<L>(take, c0, first, [&](int c, uint32_t pos) {
+      if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) {
+        sch[pos - lo] = c;
+        sv[pos - lo] = round_bf16(silu_f32(bf16_to_f32(raw[c])));
+      }
+    });
   }
   __syncthreads();
 
@@ -651,9 +637,9 @@ int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t 
   return check_launch("selected_down_kernel");
 }
 
-// up_down launch shape: CW = 256 columns per block when hidden allows (else
-// 64), P (a power of two, <= k, with k / P <= kFusedMaxSel) rank slices so
-// that nb P CB is about 512 workgroups (two per CU).
+// Launch shape: CW = 256 columns per block when hidden allows (else 64), P
+// (a power of two, <= k, with k / P <= kFusedMaxSel) rank slices so that
+// nb P CB is about 256 workgroups (one per CU).
 struct FusedShape {
   int CW, CB, P;
 };
@@ -662,7 +648,7 @@ inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
   FusedShape f;
   f.CW = (hidden % 256 == 0) ? 256 : 64;
   f.CB = static_cast<int>(hidden / f.CW);
-  int64_t P = 512 / (nb * f.CB);
+  int64_t P = 256 / (nb * f.CB);
   int64_t p2 = 1;
   while (p2 * 2 <= P) p2 *= 2;
   P = p2 < 1 ? 1 : p2;
@@ -672,19 +658,22 @@ inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
   return f;
 }
 
-void launch_select_list(const void* gate, int inter, int k, int nb, int* list_ch, float* list_sg,
-                        hipStream_t st) {
-  const int per = (inter + kSelThreads - 1) / kSelThreads;
-  const dim3 grid(static_cast<unsigned>(nb)), block(kSelThreads);
-#define MOC_SL(N) \
-  select_list_kernel<N><<<grid, block, static_cast<size_t>(k) * 2, st>>>((const uint16_t*)gate, inter, k, list_ch, list_sg)
-  if (per <= 8) MOC_SL(8);
-  else if (per <= 16) MOC_SL(16);
-  else if (per <= 24) MOC_SL(24);
-  else if (per <= 32) MOC_SL(32);
-  else if (per <= 48) MOC_SL(48);
-  else MOC_SL(64);
-#undef MOC_SL
+template <int CW>
+void launch_fused(const void* x, int hidden, const void* gate, int inter, int k, int nb,
+                  const FusedShape& f, const void* w_up, const void* wdt, float* part, int* cnt,
+                  void* y, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
+  const int per = (inter + kUdThreads - 1) / kUdThreads;
+#define MOC_FU(N)                                                                               \
+  select_up_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)x, hidden,               \
+                                                       (const uint16_t*)gate, inter, k, f.P, f.CB, \
+                                                       (const uint16_t*)w_up, (const uint16_t*)wdt, \
+                                                       part, cnt, (uint16_t*)y)
+  if (per <= 8) MOC_FU(8);
+  else if (per <= 16) MOC_FU(16);
+  else if (per <= 24) MOC_FU(24);
+  else MOC_FU(32);
+#undef MOC_FU
 }
 
 }  // namespace
@@ -787,14 +776,14 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
 
 // Workspace: a fixed 64 KB block of arrival counters (so the counters of one
 // call shape never overlap other data of another shape that reuses the
-// workspace), the ranked lists (channel ids, bf16(SiLU(g))), the partials.
+// workspace), then the partial sums.
 constexpr int64_t kFusedCounterBytes = 64 * 1024;
 
 extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t k,
                                                         int64_t hidden) {
   if (nb <= 0 || k <= 0 || hidden < 64 || inter <= 0) return 0;
   const FusedShape f = fused_shape(nb, k, hidden);
-  return kFusedCounterBytes + 2 * align256(nb * k * 4) + nb * f.P * hidden * 4;
+  return kFusedCounterBytes + nb * f.P * hidden * 4;
 }
 
 extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
@@ -817,24 +806,13 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
   MOC_REQUIRE(nb * f.CB * 4 <= kFusedCounterBytes, "moc_global_after_gate_bf16: hidden too large");
   char* ws = static_cast<char*>(workspace);
   int* cnt = reinterpret_cast<int*>(ws);
-  ws += kFusedCounterBytes;
-  int* list_ch = reinterpret_cast<int*>(ws);
-  ws += align256(nb * k * 4);
-  float* list_sg = reinterpret_cast<float*>(ws);
-  ws += align256(nb * k * 4);
-  float* part = reinterpret_cast<float*>(ws);
+  float* part = reinterpret_cast<float*>(ws + kFusedCounterBytes);
   hipStream_t st = as_stream(stream);
-  launch_select_list(gate_scores, (int)inter, (int)k, (int)nb, list_ch, list_sg, st);
-  int rc = check_launch("select_list_kernel");
-  if (rc != MOC_OK) return rc;
-  const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
   if (f.CW == 256)
-    up_down_kernel<256><<<grid, block, 0, st>>>((const uint16_t*)x, (int)hidden, (int)k, f.P, f.CB,
-                                                 list_ch, list_sg, (const uint16_t*)w_up,
-                                                 (const uint16_t*)w_down_t, part, cnt, (uint16_t*)y);
+    launch_fused<256>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, w_up, w_down_t, part,
+                      cnt, y, st);
   else
-    up_down_kernel<64><<<grid, block, 0, st>>>((const uint16_t*)x, (int)hidden, (int)k, f.P, f.CB,
-                                                list_ch, list_sg, (const uint16_t*)w_up,
-                                                (const uint16_t*)w_down_t, part, cnt, (uint16_t*)y);
-  return check_launch("up_down_kernel");
+    launch_fused<64>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, w_up, w_down_t, part,
+                     cnt, y, st);
+  return check_launch("select_up_down_kernel");
 }
