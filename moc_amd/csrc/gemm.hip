@@ -282,25 +282,41 @@ __device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, i
 
 // ---------------------------------------------------------------- epilogue
 // Each wave stages 32 rows x 128 columns of its results in its own LDS
-// region and writes them back as 16-byte row segments.
+// region and writes them back as 16-byte row segments.  The accumulators
+// hold transposed blocks, so a lane's four consecutive elements r = 4q..4q+3
+// are four consecutive columns of one row: one packed conversion pair and one
+// 8-byte (bf16) or 16-byte (f32) LDS write each.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
+}
+
 template <bool OUT_F32>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][4],
                                            int row0, int col0, int wm, int wn, int wave, int lane) {
   constexpr int kEsz = OUT_F32 ? 4 : 2;
-  constexpr int kPitch = 128 * kEsz + 16;       // bytes; +16 puts row+4 on other banks
+  // row pitch: 16-byte aligned, +16 bytes so that rows r and r + 1 start on
+  // different banks
+  constexpr int kPitch = 128 * kEsz + 16;
   char* reg = lds + wave * (32 * kPitch);
   const bool vec = g.vec_store != 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    // 32x32 accumulator layout: lane l, element r -> row 8(r/4) + 4(l/32) + r%4, col l%32
+    char* rowp = reg + (lane & 31) * kPitch;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        char* q = reg + row * kPitch + (32 * j + (lane & 31)) * kEsz;
-        if (OUT_F32) *reinterpret_cast<float*>(q) = acc[i][j][r];
-        else *reinterpret_cast<uint16_t*>(q) = f32_to_bf16(acc[i][j][r]);
+      for (int q = 0; q < 4; ++q) {
+        char* dst = rowp + (32 * j + 8 * q + 4 * (lane >> 5)) * kEsz;
+        const f32x16_t& a = acc[i][j];
+        if (OUT_F32) {
+          *reinterpret_cast<float4*>(dst) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+        } else {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(a[4 * q], a[4 * q + 1]),
+                                                      pack_bf16x2(a[4 * q + 2], a[4 * q + 3]));
+        }
       }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
     // read back: 16-byte segments, 16 per row (bf16: 8 per row)
@@ -435,7 +451,9 @@ void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
       for (int idx = 0; idx < 16; ++idx) {
         const int i = idx >> 2, j = idx & 3;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cb][i], fb[cb][j], acc[i][j], 0, 0, 0);
+        // B as the MFMA's first operand: acc[i][j] holds the block transposed,
+        // lane l: row 32 i + l % 32, columns 32 j + 8(r/4) + 4(l/32) + r % 4
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[cb][j], fa[cb][i], acc[i][j], 0, 0, 0);
         if (more && idx < 4) fa[cb ^ 1][idx] = fa_map.read(lds, idx, ks + 1, so);
         if (more && idx >= 4 && idx < 8) fb[cb ^ 1][idx - 4] = fb_map.read(lds, idx - 4, ks + 1, so);
         if (idx == 9 && tnext < nk) stage_load(tnext, tnext % kStages, ks);

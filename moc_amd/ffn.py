@@ -80,6 +80,31 @@ def _check_inputs(x, gate_w, up_w, down_w, strict_aux: bool, index_save_dtype):
             f"{gate_w.dtype}/{up_w.dtype}/{down_w.dtype}")
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for independent GEMMs:
+    a 256x256-tile GEMM whose tile count leaves CUs idle in its last round
+    (or a short selection/elementwise kernel) overlaps another one instead."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(key)
+    if s is None:
+        s = torch.cuda.Stream(device=device)
+        _SIDE_STREAMS[key] = s
+    return s
+
+
+def _on_side(side, tensors, fn):
+    """Run fn() on `side` after the current stream's queued work; tensors
+    made on the current stream and used there are kept alive for it."""
+    side.wait_stream(torch.cuda.current_stream(side.device))
+    with torch.cuda.stream(side):
+        fn()
+    for t in tensors:
+        t.record_stream(side)
+
+
 def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool):
     """Shared MoC forward: G -> select -> U -> sparse aux -> D.
 
@@ -91,6 +116,10 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     rows = x2.shape[0]
     g = K.padded_empty(rows, inter, x.dtype, x.device)
     K.linear(x2, gate_w, out=g)
+    # U = x Wu^T runs on the side stream, beside the selection over G
+    side = _side_stream(x.device)
+    u = K.padded_empty(rows, inter, x.dtype, x.device)
+    _on_side(side, (x2, up_w, u), lambda: K.linear(x2, up_w, out=u))
     if selection == "topk":
         vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype)
     elif selection == "post_silu_abs":
@@ -100,8 +129,7 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     else:
         raise ValueError(selection)
     del g
-    u = K.padded_empty(rows, inter, x.dtype, x.device)
-    K.linear(x2, up_w, out=u)
+    torch.cuda.current_stream(x.device).wait_stream(side)
     u_s, s_s, z_s, z_full = K.sparse_forward_aux(vals, idx, u, inter, want_s=save_s, want_z=save_s)
     del u
     wd = K.aligned_rows(down_w)
@@ -118,24 +146,40 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     """Shared MoC backward (moc/ffn.py:175-259 and the GCP form :423-497).
 
     dWd = go^T Z, gZ = go Wd, (gG, gU) = sparse_backward_aux, dWg = gG^T x,
-    dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products)."""
+    dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products).
+
+    The weight gradients (176 tiles of 256x256 at the 1b shape: two thirds
+    of the CUs) run on the side stream, dWd beside gZ and the aux kernel,
+    dWg and dWu beside dX."""
     d = x.shape[-1]
     inter = gate_w.shape[0]
+    dev = x.device
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev)
     x2 = K.aligned_rows(x.reshape(-1, d))
     go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
     if gcp:
         s_s, z_s = K.gcp_recompute(g_s, u_s)
     z_full = K.scatter_sparse_to_dense(z_s, idx, inter)
-    grad_down_w = K.gemm(go.t(), z_full, out_dtype=down_w.dtype)
+    grad_down_w = torch.empty(go.shape[1], inter, dtype=down_w.dtype, device=dev)
+    _on_side(side, (go, z_full, grad_down_w), lambda: K.gemm(go.t(), z_full, out=grad_down_w,
+                                                             out_dtype=grad_down_w.dtype))
     del z_full
     wd = K.aligned_rows(down_w)
-    gz = K.padded_empty(go.shape[0], inter, x.dtype, x.device)
+    gz = K.padded_empty(go.shape[0], inter, x.dtype, dev)
     K.gemm(go, wd, out=gz)
     grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
     del gz
-    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=gate_w.dtype)
-    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=up_w.dtype)
+    grad_gate_w = torch.empty(inter, d, dtype=gate_w.dtype, device=dev)
+    grad_up_w = torch.empty(inter, d, dtype=up_w.dtype, device=dev)
+
+    def weight_grads():
+        K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype)
+        K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype)
+
+    _on_side(side, (grad_g, grad_u, x2, grad_gate_w, grad_up_w), weight_grads)
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
+    main.wait_stream(side)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
 
 

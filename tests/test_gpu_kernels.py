@@ -87,6 +87,25 @@ def test_gemm_bf16_layouts(a_kc, b_kc, mnk):
     bf16_close(out16, ref, ulps=1, atol=1e-3)
 
 
+@pytest.mark.parametrize("a_kc,b_kc", [(True, True), (False, False), (True, False), (False, True)])
+def test_gemm_weight_gradient_shape(a_kc, b_kc):
+    """176 output tiles of 256x256 (the weight-gradient shape class) against
+    a torch fp32 reference on the device; repeated calls are bit-identical."""
+    M, Nn, Kk = 2048, 5461, 1000
+    g = torch.Generator(device=DEV).manual_seed(7)
+    a = torch.randn(M, Kk, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randn(Kk, Nn, device=DEV, generator=g).to(torch.bfloat16)
+    ref = a.float() @ b.float()
+    ad = K().aligned_rows(a) if a_kc else a.t().contiguous().t()
+    bd = K().aligned_rows(b.t().contiguous()).t() if b_kc else K().aligned_rows(b)
+    first = K().gemm(ad, bd, out_dtype=torch.float32)
+    close(first, ref, rtol=1e-4, atol=2e-3)
+    again = K().gemm(ad, bd, out_dtype=torch.float32)
+    assert torch.equal(first, again)
+    out16 = K().gemm(ad, bd)
+    bf16_close(out16, ref, ulps=1, atol=2e-3)
+
+
 def test_gemm_dual_product_and_f32():
     g = gen(2)
     a, a2 = torch.randn(200, 72, generator=g), torch.randn(200, 40, generator=g)
