@@ -108,6 +108,15 @@ int moc_gather_dense_to_sparse(int dtype, const void* dense, int64_t ld, const v
 int moc_gcp_recompute(int dtype, const void* g_sparse, const void* u_sparse, int64_t n,
                       void* s_sparse, void* z_sparse, void* stream);
 
+/* GCP recompute and the scatter of z in one pass: s_sparse = bf16(SiLU(g)),
+ * z_full[r, idx[r,j]] = bf16(s * u), zeros elsewhere (incl. pad columns up
+ * to ld) (moc/ffn.py:435-442).  bf16 only; z_full rows 16-byte aligned with
+ * ld a multiple of 8 and <= 8192.  s_sparse may be NULL. */
+int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const void* u_sparse,
+                              const void* idx, int idx_dtype, int64_t rows, int64_t k,
+                              int64_t inter, void* s_sparse, void* z_full, int64_t ld,
+                              void* stream);
+
 /* grad_g, grad_u dense [rows, out_ld] (zero-filled) from grad_z_full at idx:
  * grad_u = s*gz, grad_g = u*gz*SiLU'(g) (moc/training/triton_sparse_aux.py:
  * 363-423; bf16 follows the materialised-bf16 chain at :376-400, f32 the fused

@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "moc_scatter_sparse_to_dense": (_int, [_int, _vp, _vp, _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "moc_gather_dense_to_sparse": (_int, [_int, _vp, _i64, _vp, _int, _i64, _i64, _vp, _vp]),
     "moc_gcp_recompute": (_int, [_int, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "moc_gcp_recompute_scatter": (_int, [_int, _vp, _vp, _vp, _int, _i64, _i64, _i64, _vp, _vp,
+                                         _i64, _vp]),
     "moc_sparse_backward_aux": (_int, [_int, _vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                        _i64, _vp, _vp, _i64, _vp]),
     "moc_gemm": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp,

@@ -11,11 +11,15 @@
 //   moc_sparse_backward_aux    <- sparse_backward_aux     (:363-423; bf16 chain :376-400,
 //                                                          fp32 kernel :139-182)
 //   moc_gcp_recompute          <- _MoCGCPFunction.backward recompute (moc/ffn.py:435-436)
+//   moc_gcp_recompute_scatter  <- the same recompute followed by the scatter of z
+//                                 (moc/ffn.py:435-437) in one pass
 //
-// Dense outputs are cleared by a fill kernel inside the same entry point (no
-// hipMemsetAsync, so the calls stay valid inside a captured HIP graph).
-// Elementwise work is one thread per selected entry; every kernel is bound by
-// HBM traffic.
+// bf16 with 16-byte aligned dense rows (the FFN's padded buffers) runs the
+// row form: one workgroup per row, dense rows staged and built in LDS and
+// moved with 16-byte accesses, zeros included.  Otherwise dense outputs are
+// cleared by a fill kernel inside the same entry point (no hipMemsetAsync,
+// so the calls stay valid inside a captured HIP graph) and elementwise work
+// is one thread per selected entry.  Every kernel is bound by HBM traffic.
 #include "abi.h"
 #include "common.h"
 
@@ -148,6 +152,222 @@ __global__ __launch_bounds__(256) void sparse_backward_aux_kernel(
   grad_u[row * out_ld + ch] = E::st(gu);
 }
 
+// ---------------------------------------------------------------------------
+// Row form (bf16, dense rows 16-byte aligned with a pitch that is a multiple
+// of 8 and <= kRowMaxLd): one workgroup per row.  Dense inputs are staged in
+// LDS with 16-byte loads, dense outputs are built in LDS (zeros plus the
+// selected values) and written back whole with 16-byte stores, so the dense
+// tensors are read and written once, coalesced, and need no separate
+// zero-fill launch.  The per-entry arithmetic is the same as above.
+// ---------------------------------------------------------------------------
+// Threads per row: 512 for the backward row (its per-entry bf16 chain is
+// the heaviest), 256 for the others.
+constexpr int kRowThreadsBwd = 512;
+constexpr int kRowThreads = 256;
+constexpr int64_t kRowMaxLd = 8192;  // three staged rows fit the default 64 KB of LDS
+
+template <int NT>
+__device__ __forceinline__ void row_zero(uint16_t* buf, int64_t ld) {
+  for (int64_t c = threadIdx.x; c < ld / 8; c += NT)
+    reinterpret_cast<uint4*>(buf)[c] = make_uint4(0, 0, 0, 0);
+}
+// All of a thread's (<= 4) 16-byte loads are issued before any is stored, so
+// staging a row costs one memory latency.
+template <int NT>
+__device__ __forceinline__ void row_load(uint16_t* buf, const uint16_t* src, int64_t ld) {
+  constexpr int kMax = static_cast<int>(kRowMaxLd / 8 / NT);
+  uint4 v[kMax];
+#pragma unroll
+  for (int q = 0; q < kMax; ++q) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(NT) * q;
+    v[q] = c < ld / 8 ? reinterpret_cast<const uint4*>(src)[c] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < kMax; ++q) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(NT) * q;
+    if (c < ld / 8) reinterpret_cast<uint4*>(buf)[c] = v[q];
+  }
+}
+template <int NT>
+__device__ __forceinline__ void row_store(uint16_t* dst, const uint16_t* buf, int64_t ld) {
+  for (int64_t c = threadIdx.x; c < ld / 8; c += NT)
+    reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(buf)[c];
+}
+
+// Row-form arithmetic.  RNE to bf16 with the gfx950 packed conversion (NaN
+// keeps the canonical 0x7FC0 of f32_to_bf16), and one exp per entry for both
+// sigmoid(g) and SiLU(g) = g / (1 + exp(-g)).
+typedef float rf32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 rbf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t to_bf16(float f) {
+  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((rf32x2_t){f, 0.0f}, rbf16x2_t));
+  return f != f ? uint16_t(0x7FC0u) : static_cast<uint16_t>(w & 0xFFFFu);
+}
+__device__ __forceinline__ float rnd(float f) { return bf16_to_f32(to_bf16(f)); }
+
+// The entries of a row are taken kRowPer per thread at a time; the first
+// group's sparse loads are issued before the dense row is staged, so the two
+// memory latencies overlap.
+constexpr int kRowPer = 4;
+
+template <typename IdxT, int NT>
+struct RowEntries {
+  int64_t ch[kRowPer];
+  uint16_t a[kRowPer], b[kRowPer], c[kRowPer];
+  // entries e0 + threadIdx.x + NT q of row `row`; a/b/c from up to
+  // three sparse [rows, k] tensors (null: not loaded)
+  __device__ __forceinline__ void load(const IdxT* idx, const uint16_t* pa, const uint16_t* pb,
+                                       const uint16_t* pc, int64_t row, int k, int e0) {
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q) {
+      const int e = e0 + threadIdx.x + NT * q;
+      const int64_t i = row * k + e;
+      const bool ok = e < k;
+      ch[q] = ok ? static_cast<int64_t>(idx[i]) : -1;
+      a[q] = (ok && pa) ? pa[i] : uint16_t(0);
+      b[q] = (ok && pb) ? pb[i] : uint16_t(0);
+      c[q] = (ok && pc) ? pc[i] : uint16_t(0);
+    }
+  }
+};
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRowThreads) void scatter_rows_kernel(
+    const uint16_t* __restrict__ sparse, const IdxT* __restrict__ idx, int k, int64_t inter,
+    uint16_t* __restrict__ dense, int64_t ld) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
+  const int64_t row = blockIdx.x;
+  RowEntries<IdxT, kRowThreads> r;
+  r.load(idx, sparse, nullptr, nullptr, row, k, 0);
+  row_zero<kRowThreads>(rbuf, ld);
+  __syncthreads();
+  for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
+    if (e0 > 0) r.load(idx, sparse, nullptr, nullptr, row, k, e0);
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q)
+      if (r.ch[q] >= 0 && r.ch[q] < inter) rbuf[r.ch[q]] = r.a[q];
+  }
+  __syncthreads();
+  row_store<kRowThreads>(dense + row * ld, rbuf, ld);
+}
+
+// GCP recompute fused with the scatter of z: s = bf16(SiLU(g)),
+// z = bf16(s * u) per selected entry (torch's F.silu and product on bf16
+// tensors), s to s_s, z into the dense row.
+template <typename IdxT>
+__global__ __launch_bounds__(kRowThreads) void gcp_scatter_rows_kernel(
+    const uint16_t* __restrict__ g_s, const uint16_t* __restrict__ u_s,
+    const IdxT* __restrict__ idx, int k, int64_t inter, uint16_t* __restrict__ s_s,
+    uint16_t* __restrict__ z_full, int64_t ld) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
+  const int64_t row = blockIdx.x;
+  RowEntries<IdxT, kRowThreads> r;
+  r.load(idx, g_s, u_s, nullptr, row, k, 0);
+  row_zero<kRowThreads>(rbuf, ld);
+  __syncthreads();
+  for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
+    if (e0 > 0) r.load(idx, g_s, u_s, nullptr, row, k, e0);
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q) {
+      const int e = e0 + threadIdx.x + kRowThreads * q;
+      if (e >= k) continue;
+      const float s = rnd(silu_f32(bf16_to_f32(r.a[q])));
+      if (s_s) s_s[row * k + e] = to_bf16(s);
+      if (r.ch[q] >= 0 && r.ch[q] < inter) rbuf[r.ch[q]] = to_bf16(s * bf16_to_f32(r.b[q]));
+    }
+  }
+  __syncthreads();
+  row_store<kRowThreads>(z_full + row * ld, rbuf, ld);
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRowThreads) void forward_aux_rows_kernel(
+    const uint16_t* __restrict__ vals, const IdxT* __restrict__ idx,
+    const uint16_t* __restrict__ u_full, int64_t u_ld, int k, int64_t inter,
+    uint16_t* __restrict__ u_s, uint16_t* __restrict__ s_s, uint16_t* __restrict__ z_s,
+    uint16_t* __restrict__ z_full, int64_t z_ld) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
+  uint16_t* urow = rbuf;        // [u_ld]
+  uint16_t* zrow = rbuf + u_ld;  // [z_ld]
+  const int64_t row = blockIdx.x;
+  RowEntries<IdxT, kRowThreads> r;
+  r.load(idx, vals, nullptr, nullptr, row, k, 0);
+  row_load<kRowThreads>(urow, u_full + row * u_ld, u_ld);
+  row_zero<kRowThreads>(zrow, z_ld);
+  __syncthreads();
+  for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
+    if (e0 > 0) r.load(idx, vals, nullptr, nullptr, row, k, e0);
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q) {
+      const int64_t ch = r.ch[q];
+      if (ch < 0 || ch >= inter) continue;  // malformed index or past k: never touch memory
+      const int64_t i = row * k + e0 + threadIdx.x + kRowThreads * q;
+      const float g = bf16_to_f32(r.a[q]);
+      const uint16_t u_raw = urow[ch];
+      const float s = rnd(g * sigmoid_f32(g));
+      const uint16_t z = to_bf16(s * bf16_to_f32(u_raw));
+      if (u_s) u_s[i] = u_raw;
+      if (s_s) s_s[i] = to_bf16(s);
+      if (z_s) z_s[i] = z;
+      zrow[ch] = z;
+    }
+  }
+  __syncthreads();
+  row_store<kRowThreads>(z_full + row * z_ld, zrow, z_ld);
+}
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
+    const IdxT* __restrict__ idx, const uint16_t* __restrict__ g_s,
+    const uint16_t* __restrict__ u_s, const uint16_t* __restrict__ s_s,
+    const uint16_t* __restrict__ gz_full, int64_t gz_ld, int k, int64_t inter,
+    uint16_t* __restrict__ grad_g, uint16_t* __restrict__ grad_u, int64_t out_ld) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
+  uint16_t* gzrow = rbuf;                  // [gz_ld]
+  uint16_t* ggrow = rbuf + gz_ld;          // [out_ld]
+  uint16_t* gurow = rbuf + gz_ld + out_ld;  // [out_ld]
+  const int64_t row = blockIdx.x;
+  RowEntries<IdxT, kRowThreadsBwd> r;
+  r.load(idx, g_s, u_s, s_s, row, k, 0);
+  row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_ld);
+  row_zero<kRowThreadsBwd>(ggrow, out_ld);
+  row_zero<kRowThreadsBwd>(gurow, out_ld);
+  __syncthreads();
+  for (int e0 = 0; e0 < k; e0 += kRowThreadsBwd * kRowPer) {
+    if (e0 > 0) r.load(idx, g_s, u_s, s_s, row, k, e0);
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q) {
+      const int64_t ch = r.ch[q];
+      if (ch < 0 || ch >= inter) continue;
+      const float gz = bf16_to_f32(gzrow[ch]);
+      const float g = bf16_to_f32(r.a[q]);
+      const float u = bf16_to_f32(r.b[q]);
+      const float den = 1.0f + expf(-g);
+      const float s = s_s ? bf16_to_f32(r.c[q]) : rnd(g / den);
+      // the reference's bf16 chain (see sparse_backward_aux_kernel)
+      const float gs = rnd(u * gz);
+      const float gu = rnd(s * gz);
+      const float sig = rnd(1.0f / den);
+      const float t1 = rnd(1.0f - sig);
+      const float t2 = rnd(g * t1);
+      const float t3 = rnd(1.0f + t2);
+      const float d = rnd(sig * t3);
+      ggrow[ch] = to_bf16(gs * d);
+      gurow[ch] = to_bf16(gu);
+    }
+  }
+  __syncthreads();
+  row_store<kRowThreadsBwd>(grad_g + row * out_ld, ggrow, out_ld);
+  row_store<kRowThreadsBwd>(grad_u + row * out_ld, gurow, out_ld);
+}
+
+// The row form applies to bf16 dense rows that are 16-byte aligned with a
+// pitch that is a multiple of 8 elements and at most kRowMaxLd.
+inline bool row_form_ok(const void* p, int64_t ld) {
+  return ld % 8 == 0 && ld <= kRowMaxLd && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}
+
 inline dim3 grid_for(int64_t n) { return dim3(static_cast<unsigned>((n + 255) / 256)); }
 
 bool idx_ok(int d) { return d == MOC_I16 || d == MOC_I32 || d == MOC_I64; }
@@ -183,6 +403,17 @@ extern "C" int moc_sparse_forward_aux(int dtype, const void* topk_vals, const vo
   MOC_REQUIRE(topk_vals && idx && u_full, "moc_sparse_forward_aux: null input");
   hipStream_t st = as_stream(stream);
   const size_t esz = dtype == MOC_BF16 ? 2 : 4;
+  if (dtype == MOC_BF16 && z_full != nullptr && rows < (1LL << 31) && row_form_ok(z_full, z_ld) &&
+      row_form_ok(u_full, u_ld)) {
+    const size_t lds = static_cast<size_t>(u_ld + z_ld) * 2;
+#define MOC_FWDR(T)                                                                           \
+  forward_aux_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(     \
+      (const uint16_t*)topk_vals, (const T*)idx, (const uint16_t*)u_full, u_ld, (int)k, inter, \
+      (uint16_t*)u_sparse, (uint16_t*)s_sparse, (uint16_t*)z_sparse, (uint16_t*)z_full, z_ld)
+    MOC_IDX_DISPATCH(idx_dtype, MOC_FWDR);
+#undef MOC_FWDR
+    return check_launch("forward_aux_rows_kernel");
+  }
   if (z_full) {
     const int rc = moc_fill_zero(z_full, rows * z_ld * static_cast<int64_t>(esz), stream);
     if (rc != MOC_OK) return rc;
@@ -211,11 +442,20 @@ extern "C" int moc_scatter_sparse_to_dense(int dtype, const void* sparse, const 
               "moc_scatter_sparse_to_dense: bad shape");
   if (rows == 0) return MOC_OK;
   MOC_REQUIRE(sparse && idx && dense, "moc_scatter_sparse_to_dense: null pointer");
+  hipStream_t st = as_stream(stream);
+  if (dtype == MOC_BF16 && rows < (1LL << 31) && row_form_ok(dense, ld)) {
+    const size_t lds = static_cast<size_t>(ld) * 2;
+#define MOC_SCATR(T)                                                                          \
+  scatter_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(         \
+      (const uint16_t*)sparse, (const T*)idx, (int)k, inter, (uint16_t*)dense, ld)
+    MOC_IDX_DISPATCH(idx_dtype, MOC_SCATR);
+#undef MOC_SCATR
+    return check_launch("scatter_rows_kernel");
+  }
   const size_t esz = dtype == MOC_BF16 ? 2 : 4;
   int rc = moc_fill_zero(dense, rows * ld * static_cast<int64_t>(esz), stream);
   if (rc != MOC_OK) return rc;
   const int64_t n = rows * k;
-  hipStream_t st = as_stream(stream);
 #define MOC_SCAT(T)                                                                              \
   if (dtype == MOC_BF16)                                                                         \
     scatter_kernel<uint16_t, T><<<grid_for(n), 256, 0, st>>>((const uint16_t*)sparse, (const T*)idx, \
@@ -281,6 +521,19 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
   if (rows == 0) return MOC_OK;
   MOC_REQUIRE(idx && g_sparse && u_sparse && gz_full && grad_g && grad_u,
               "moc_sparse_backward_aux: null pointer");
+  if (dtype == MOC_BF16 && rows < (1LL << 31) && row_form_ok(gz_full, gz_ld) &&
+      row_form_ok(grad_g, out_ld) && row_form_ok(grad_u, out_ld)) {
+    hipStream_t st = as_stream(stream);
+    const size_t lds = static_cast<size_t>(gz_ld + 2 * out_ld) * 2;
+#define MOC_BWDR(T)                                                                          \
+  backward_aux_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
+      (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                   \
+      (const uint16_t*)s_sparse, (const uint16_t*)gz_full, gz_ld, (int)k, inter,              \
+      (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld)
+    MOC_IDX_DISPATCH(idx_dtype, MOC_BWDR);
+#undef MOC_BWDR
+    return check_launch("backward_aux_rows_kernel");
+  }
   const size_t esz = dtype == MOC_BF16 ? 2 : 4;
   int rc = moc_fill_zero(grad_g, rows * out_ld * static_cast<int64_t>(esz), stream);
   if (rc == MOC_OK) rc = moc_fill_zero(grad_u, rows * out_ld * static_cast<int64_t>(esz), stream);
@@ -300,4 +553,28 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
   MOC_IDX_DISPATCH(idx_dtype, MOC_BWD);
 #undef MOC_BWD
   return check_launch("sparse_backward_aux_kernel");
+}
+
+extern "C" int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const void* u_sparse,
+                                         const void* idx, int idx_dtype, int64_t rows, int64_t k,
+                                         int64_t inter, void* s_sparse, void* z_full, int64_t ld,
+                                         void* stream) {
+  MOC_REQUIRE(dtype == MOC_BF16, "moc_gcp_recompute_scatter: bf16 only");
+  MOC_REQUIRE(idx_ok(idx_dtype), "moc_gcp_recompute_scatter: bad index dtype");
+  MOC_REQUIRE(rows >= 0 && rows < (1LL << 31) && k >= 1 && inter >= k && ld >= inter,
+              "moc_gcp_recompute_scatter: bad shape");
+  if (rows == 0) return MOC_OK;
+  MOC_REQUIRE(g_sparse && u_sparse && idx && z_full, "moc_gcp_recompute_scatter: null pointer");
+  MOC_REQUIRE(row_form_ok(z_full, ld),
+              "moc_gcp_recompute_scatter: z_full rows must be 16-byte aligned, pitch a multiple of 8 "
+              "and <= %lld", (long long)kRowMaxLd);
+  hipStream_t st = as_stream(stream);
+  const size_t lds = static_cast<size_t>(ld) * 2;
+#define MOC_GCPS(T)                                                                           \
+  gcp_scatter_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(     \
+      (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const T*)idx, (int)k, inter,     \
+      (uint16_t*)s_sparse, (uint16_t*)z_full, ld)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_GCPS);
+#undef MOC_GCPS
+  return check_launch("gcp_scatter_rows_kernel");
 }

@@ -158,9 +158,12 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     side = _side_stream(dev)
     x2 = K.aligned_rows(x.reshape(-1, d))
     go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
-    if gcp:
-        s_s, z_s = K.gcp_recompute(g_s, u_s)
-    z_full = K.scatter_sparse_to_dense(z_s, idx, inter)
+    if gcp and x.dtype == torch.bfloat16 and K.round_up(inter, 8) <= 8192:
+        s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter)
+    else:
+        if gcp:
+            s_s, z_s = K.gcp_recompute(g_s, u_s)
+        z_full = K.scatter_sparse_to_dense(z_s, idx, inter)
     grad_down_w = torch.empty(go.shape[1], inter, dtype=down_w.dtype, device=dev)
     _on_side(side, (go, z_full, grad_down_w), lambda: K.gemm(go.t(), z_full, out=grad_down_w,
                                                              out_dtype=grad_down_w.dtype))

@@ -237,6 +237,11 @@ def test_sparse_aux_forward_backward(dtype):
     close(ku, gu, **tol)
     kg2, ku2 = K().sparse_backward_aux(ti, vals.to(DEV), u_s.to(DEV), None, GZ.to(DEV), inter)
     close(kg2, gg, **tol)
+    if dtype == torch.bfloat16:
+        # the fused GCP recompute + scatter equals the two-step form bit for bit
+        fs, fz = K().gcp_recompute_scatter(vals.to(DEV), u_s.to(DEV), ti, inter)
+        assert torch.equal(fs.cpu(), ks.cpu())
+        assert torch.equal(fz.cpu(), K().scatter_sparse_to_dense(kz, ti, inter).cpu())
 
 
 # ------------------------------------------------------------------- decode
