@@ -83,11 +83,11 @@ def _check_inputs(x, gate_w, up_w, down_w, strict_aux: bool, index_save_dtype):
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(device) -> torch.cuda.Stream:
-    """A second stream per device (default priority) for independent GEMMs:
-    a 256x256-tile GEMM whose tile count leaves CUs idle in its last round
-    (or a short selection/elementwise kernel) overlaps another one instead."""
-    key = device.index if device.index is not None else torch.cuda.current_device()
+def _side_stream(device, which: int = 0) -> torch.cuda.Stream:
+    """Extra streams per device (default priority) for independent GEMMs: a
+    256x256-tile GEMM whose tile count leaves CUs idle in its last round (or
+    a short selection/elementwise kernel) overlaps another one instead."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), which)
     s = _SIDE_STREAMS.get(key)
     if s is None:
         s = torch.cuda.Stream(device=device)
@@ -149,8 +149,8 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products).
 
     The weight gradients (176 tiles of 256x256 at the 1b shape: two thirds
-    of the CUs) run on the side stream, dWd beside gZ and the aux kernel,
-    dWg and dWu beside dX."""
+    of the CUs) run on side streams, dWd beside gZ and the aux kernel, dWg
+    and dWu (each on its own stream) beside dX."""
     d = x.shape[-1]
     inter = gate_w.shape[0]
     dev = x.device
@@ -175,14 +175,14 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     del gz
     grad_gate_w = torch.empty(inter, d, dtype=gate_w.dtype, device=dev)
     grad_up_w = torch.empty(inter, d, dtype=up_w.dtype, device=dev)
-
-    def weight_grads():
-        K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype)
-        K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype)
-
-    _on_side(side, (grad_g, grad_u, x2, grad_gate_w, grad_up_w), weight_grads)
+    side2 = _side_stream(dev, 1)
+    _on_side(side, (grad_g, x2, grad_gate_w),
+             lambda: K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype))
+    _on_side(side2, (grad_u, x2, grad_up_w),
+             lambda: K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype))
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
     main.wait_stream(side)
+    main.wait_stream(side2)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
 
 
