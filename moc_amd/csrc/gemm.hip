@@ -32,11 +32,13 @@
 // operand whose K is not a multiple of 64 goes through registers with
 // element masking (one tile per launch).
 //
-// Tiling: 256x256 C tile per 256-thread workgroup, four waves of 128x128
-// (4x4 blocks of 32x32), K step 64, two LDS stages (128 KB), one barrier per
-// K step; the next tile's loads are in flight during the MFMAs.  Workgroup
-// ids are remapped so that each XCD (ids are dealt round-robin over the 8
-// XCDs) works on a contiguous, M-grouped run of tiles that shares its L2.
+// Tiling: 256x256 C tile per workgroup, K step 64, two LDS stages (128 KB).
+// The main kernel (gemm_pp_kernel) runs eight waves of 128x64, two per SIMD,
+// that alternate between MFMA phases and LDS/memory phases (see there); a
+// four-wave kernel (128x128 per wave, one barrier per K step) covers operands
+// whose buffer offsets could wrap 32 bits.  Workgroup ids are remapped so
+// that each XCD (ids are dealt round-robin over the 8 XCDs) works on a
+// contiguous, M-grouped run of tiles that shares its L2.
 //
 // f32 operands use a plain FMA kernel (parity path for f32 models).
 #include "abi.h"
@@ -83,6 +85,7 @@ struct GemmArgs {
   int64_t ldc;
   int tiles_m, tiles_n;
   int vec_store;  // C rows are 16-byte aligned: vector epilogue stores
+  int pp;         // the 512-thread kernel may run this product
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -185,8 +188,8 @@ struct TileMap {
   // Pull the K tile at k0 into L2 ahead of its real loads: one 16-byte load
   // per 128-byte line of the tile, landing in a shared LDS sink.  KC: one
   // tile row per thread; MN: a quarter k-row (128 bytes) per thread.
-  __device__ __forceinline__ void prefetch(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
-                                           int row0, uint32_t sink, int tid) const {
+  static __device__ __forceinline__ void prefetch(__amdgpu_buffer_rsrc_t rsrc, const Operand& o,
+                                                  int k0, int row0, uint32_t sink, int tid) {
     uint32_t off;
     if (KC) {
       const int r = row0 + tid;
@@ -221,42 +224,45 @@ struct TileMap {
 // computed once; block, k step and stage enter as added offsets.
 template <bool KC>
 struct FragMap {
-  uint32_t base[4];   // KC: one per k16 step; MN: one per 32-wide block
+  // Byte address of the lane's fragment for block 0, k16 step 0, stage 0.
+  // The other fragments differ only in bits that no other term touches, so
+  // they are one XOR away: KC fragments of k16 step ks at base ^ 32 ks (the
+  // swizzled chunk index (2 ks + l/32) ^ swz = ((l/32) ^ swz) ^ 2 ks), MN
+  // fragments of block bi at base ^ 64 bi (the chunk index c + 4 bi, c % 4 =
+  // c, sets bits 2-3 of c when the wave's offset is a multiple of 128, or for
+  // bi < 2).  Keeping one register per operand matters for the 512-thread
+  // kernel, whose 256-register budget holds 128 accumulators and a K tile of
+  // fragments.
+  uint32_t base;
 
-  // region: LDS byte of this operand's stage-0 tile; wofs: the wave's 128-row
-  // offset inside the 256-row tile
+  // region: LDS byte of this operand's stage-0 tile; wofs: the wave's row
+  // offset inside the 256-row tile (a multiple of 64; of 128 if blocks 2-3
+  // of an MN operand are read)
   __device__ __forceinline__ void init(uint32_t region, int wofs, int lane) {
     if (KC) {
       // rows wofs + 32 blk + (lane & 31): row & 15 = lane & 15
       const uint32_t row = static_cast<uint32_t>(wofs + (lane & 31)) * (kBK * 2);
       const int swz = kc_swz(lane & 15);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        base[ks] = (ks < kBK / 16)
-                       ? region + row + static_cast<uint32_t>(((2 * ks + (lane >> 5)) ^ swz) * 16)
-                       : 0;
+      base = region + row + static_cast<uint32_t>(((lane >> 5) ^ swz) * 16);
     } else {
       // lane = 16 g + i reads k-row 8(g >> 1) + i/4 (+16 ks) and columns
       // m = blk + 16(g & 1) + 4(i & 3) .. +3 of chunk m/8
       const int i = lane & 15, g = lane >> 4;
       const int r = 8 * (g >> 1) + (i >> 2);
       const int swz = mn_swz(i >> 2);
-      const uint32_t b = region + r * 512 + 8 * (i & 1);
-#pragma unroll
-      for (int bi = 0; bi < 4; ++bi) {
-        const int c = (wofs + 32 * bi + 16 * (g & 1) + 4 * (i & 3)) >> 3;
-        base[bi] = b + 16 * (c ^ swz);
-      }
+      const int c = (wofs + 16 * (g & 1) + 4 * (i & 3)) >> 3;
+      base = region + r * 512 + 8 * (i & 1) + 16 * (c ^ swz);
     }
   }
 
-  // so: byte offset of the stage's tile
+  // so: byte offset of the stage's tile (a multiple of 32 KB, so adding it
+  // before the XOR is the same as after)
   __device__ __forceinline__ bf16x8_t read(const char* lds, int blk, int ks, uint32_t so) const {
     if (KC) {
-      const char* p = lds + (base[ks] + so) + blk * (32 * kBK * 2);
+      const char* p = lds + ((base + so) ^ (32u * ks)) + blk * (32 * kBK * 2);
       return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
     } else {
-      const char* p = lds + (base[blk] + so) + ks * 8192;
+      const char* p = lds + ((base + so) ^ (64u * blk)) + ks * 8192;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
       const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * 512));
       const i16x4_t v[2] = {lo, hi};
@@ -293,20 +299,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
-template <bool OUT_F32>
-__device__ __forceinline__ void store_tile(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][4],
-                                           int row0, int col0, int wm, int wn, int wave, int lane) {
+template <bool OUT_F32, int NJ>
+__device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][NJ],
+                                             int row0, int col0, int wm, int wn, int wave, int lane) {
   constexpr int kEsz = OUT_F32 ? 4 : 2;
+  constexpr int kCols = 32 * NJ;  // columns of the wave's tile
   // row pitch: 16-byte aligned, +16 bytes so that rows r and r + 1 start on
   // different banks
-  constexpr int kPitch = 128 * kEsz + 16;
+  constexpr int kPitch = kCols * kEsz + 16;
   char* reg = lds + wave * (32 * kPitch);
   const bool vec = g.vec_store != 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     char* rowp = reg + (lane & 31) * kPitch;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         char* dst = rowp + (32 * j + 8 * q + 4 * (lane >> 5)) * kEsz;
@@ -319,8 +326,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, char* lds, const f
         }
       }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
-    // read back: 16-byte segments, 16 per row (bf16: 8 per row)
-    constexpr int kSegs = 128 * kEsz / 16;          // per row
+    // read back: 16-byte segments
+    constexpr int kSegs = kCols * kEsz / 16;        // per row
     constexpr int kIters = 32 * kSegs / 64;
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
@@ -481,7 +488,267 @@ void gemm_bf16_kernel(GemmArgs g) {
     compute(st, t + kStages - 1, t + kStages - 1 + kPrefetch);
   }
   __syncthreads();  // every wave is done with the LDS stages
-  store_tile<OUT_F32>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+  store_tile_w<OUT_F32, 4>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong variant: 512 threads, two waves per SIMD.
+//
+// The same 256x256 C tile and 64-deep K tiles in the same two LDS stages, but
+// eight waves of 128x64 (4x2 blocks of 32x32, 128 accumulators per lane) in
+// two groups.  Waves 0-3 (group 0) and 4-7 (group 1) sit one per SIMD each,
+// and the groups alternate between a compute phase (the 32 MFMAs of one K
+// tile, fragments already in registers) and a memory phase (all fragments of
+// the next K tile from LDS, plus, for group 0, the direct-to-LDS loads of the
+// tile after it; for group 1 the L2 prefetch), with one workgroup barrier
+// between phases:
+//   phase 2t:    group 0 reads K tile t, loads tile t+1   | group 1 MFMAs tile t-1
+//   phase 2t+1:  group 0 MFMAs tile t                     | group 1 reads K tile t
+// so each SIMD's matrix pipe is fed by one wave while the other waits on LDS
+// and memory.  Tile t+1 lands in the stage of tile t-1, whose last reader
+// (group 1, phase 2t-1) is past a barrier; group 0 waits for its loads at the
+// end of its compute phase, a whole K tile after issuing them.
+// ---------------------------------------------------------------------------
+constexpr int kPpThreads = 512;
+
+// One 16-byte load into the LDS sink for line `idx` of slice `slice` (of n)
+// of the K tile at k0: a KC tile is 256 rows of 128 bytes, an MN tile 64
+// k-rows of four 128-byte lines.  Lines past the operand read as zero.
+template <bool KC>
+__device__ __forceinline__ void prefetch_slice(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
+                                               int row0, uint32_t sink, int idx, int slice, int n) {
+  uint32_t off;
+  if (KC) {
+    const int r = row0 + slice * (256 / n) + idx;
+    off = (r < o.ext && k0 < o.K) ? static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + k0) * 2)
+                                  : kOob;
+  } else {
+    const int kr = k0 + slice * (64 / n) + (idx >> 2);
+    off = kr < o.K ? static_cast<uint32_t>((static_cast<int64_t>(kr) * o.ld + row0 + 64 * (idx & 3)) * 2)
+                   : kOob;
+  }
+  dma16(rsrc, __builtin_amdgcn_readfirstlane(sink), off);
+}
+
+// Direct-to-LDS load offsets of one operand for a group-0 wave: the eight
+// loads of a tile differ by a uniform stride, so only load 0 is kept.
+template <bool KC>
+struct LoadMap {
+  uint32_t voff0;  // byte offset of load 0 at k = 0
+  int kchunk;      // KC: first k of this lane's chunk within a tile
+
+  // Rows past the extent (KC) and k-rows past K (MN) are not checked here:
+  // their offsets land past the end of the buffer resource and read as zero.
+  // The host guarantees that no such offset wraps around 2^32.
+  __device__ __forceinline__ void init(const Operand& o, int row0, int wave, int lane) {
+    if (KC) {
+      kchunk = 8 * ((lane % kCpr) ^ kc_swz((wave * kRowsPerLoad + lane / kCpr) & 15));
+      const int r = row0 + wave * kRowsPerLoad + lane / kCpr;
+      voff0 = static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + kchunk) * 2);
+    } else {
+      kchunk = 0;
+      const int r = wave * 2 + (lane >> 5);
+      const int c = (lane & 31) ^ mn_swz(r);
+      voff0 = static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + row0 + c * 8) * 2);
+    }
+  }
+
+  // All kLoads loads of the K tile at k0 into the tile at LDS byte `tile`
+  // (the placement of TileMap::issue2).  A KC chunk at k >= K reads as zero.
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
+                                        uint32_t tile, int wave) const {
+    const uint32_t jstride = KC ? static_cast<uint32_t>(4 * kRowsPerLoad * o.ld * 2)
+                                : static_cast<uint32_t>(8 * o.ld * 2);
+    const uint32_t kofs = KC ? static_cast<uint32_t>(k0) * 2u
+                             : static_cast<uint32_t>(static_cast<int64_t>(k0) * o.ld * 2);
+    uint32_t b = voff0 + kofs;
+    if (KC && k0 + kchunk >= o.K) b = kOob;  // kOob + j * jstride stays >= 2^31
+    // opaque: keeps the compiler from hoisting the eight offsets out of the
+    // K loop (they would stay live in registers the 512-thread kernel lacks)
+    asm volatile("" : "+v"(b));
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + (j * 4 + wave) * 1024);
+      dma16(rsrc, m0, b + j * jstride);
+    }
+  }
+
+  // KC, K % 8 != 0: zero the elements k >= K of the chunk that straddles K
+  // (its loads must have landed).
+  __device__ __forceinline__ void zero_straddle(char* lds, const Operand& o, int k0,
+                                                uint32_t tile, int wave, int lane) const {
+    const int k = k0 + kchunk;
+    if (!(k < o.K && o.K < k + 8)) return;
+    const int valid = o.K - k;  // 1 .. 7 elements stay
+    uint32_t keep[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      keep[d] = 2 * d + 1 < valid ? 0xFFFFFFFFu : (2 * d < valid ? 0x0000FFFFu : 0u);
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      uint4* q = reinterpret_cast<uint4*>(lds + tile + (j * 4 + wave) * 1024 + lane * 16);
+      uint4 v = *q;
+      v.x &= keep[0];
+      v.y &= keep[1];
+      v.z &= keep[2];
+      v.w &= keep[3];
+      *q = v;
+    }
+  }
+};
+
+template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL>
+__global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_pp_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  const int sw = wave & 3;
+  int tm, tn;
+  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int row0 = tm * kBM;
+  const int col0 = tn * kBN;
+  const int wm = (sw >> 1) * 128;
+  const int wn = (sw & 1) * 128 + grp * 64;
+  const uint32_t lds0 = lds_addr(lds);
+
+  const int nk0 = g.nk[0];
+  const int nk = nk0 + (DUAL ? g.nk[1] : 0);
+
+  FragMap<A_KC> fa_map;
+  FragMap<B_KC> fb_map;
+  fa_map.init(0, wm, lane);
+  fb_map.init(kBOffset, wn, lane);
+
+  f32x16_t acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  bf16x8_t fa[4][4], fb[4][2];  // [k16 step][block]
+  auto read_frags = [&](int st) {
+    const uint32_t so = st * kTileBytes;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
+    }
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+  };
+
+  // Workgroup barrier between phases; the scheduling fences keep the compiler
+  // from moving MFMAs or LDS reads across it (they touch registers only, so
+  // it otherwise would), which would merge the two phases.
+  auto phase_end = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  if (grp == 0) {
+    LoadMap<A_KC> ma0, ma1;
+    LoadMap<B_KC> mb0, mb1;
+    ma0.init(g.a[0], row0, sw, lane);
+    mb0.init(g.b[0], col0, sw, lane);
+    const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(g.a[0]), rb0 = make_rsrc(g.b[0]);
+    __amdgpu_buffer_rsrc_t ra1 = ra0, rb1 = rb0;
+    if (DUAL) {
+      ma1.init(g.a[1], row0, sw, lane);
+      mb1.init(g.b[1], col0, sw, lane);
+      ra1 = make_rsrc(g.a[1]);
+      rb1 = make_rsrc(g.b[1]);
+    }
+    auto load_tile = [&](int t) {
+      const int st = t % kStages;
+      const uint32_t at = lds0 + st * kTileBytes, bt = lds0 + kBOffset + st * kTileBytes;
+      if (DUAL && t >= nk0) {
+        const int k0 = (t - nk0) * kBK;
+        ma1.issue(ra1, g.a[1], k0, at, sw);
+        mb1.issue(rb1, g.b[1], k0, bt, sw);
+      } else {
+        const int k0 = t * kBK;
+        ma0.issue(ra0, g.a[0], k0, at, sw);
+        mb0.issue(rb0, g.b[0], k0, bt, sw);
+      }
+    };
+    // After tile t's loads have landed: zero KC elements beyond a K that is
+    // not a multiple of 8 (only the last tile of a product can need it).
+    auto fix_tile = [&](int t) {
+      const int st = t % kStages;
+      const uint32_t at = st * kTileBytes, bt = kBOffset + st * kTileBytes;
+      const bool p1 = DUAL && t >= nk0;
+      const Operand& oa = p1 ? g.a[1] : g.a[0];
+      const int k0 = (p1 ? t - nk0 : t) * kBK;
+      if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
+      if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane);
+      if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane);
+    };
+    load_tile(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    fix_tile(0);
+    phase_end();
+    for (int t = 0; t < nk; ++t) {
+      if (t + 1 < nk) load_tile(t + 1);
+      read_frags(t % kStages);
+      phase_end();  // phase 2t -> 2t+1
+      compute();
+      if (t + 1 < nk) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        fix_tile(t + 1);
+      }
+      phase_end();  // phase 2t+1 -> 2t+2
+    }
+  } else {
+    // L2 prefetch, shared out over the workgroups of an XCD: the 32
+    // concurrent tiles of an XCD form a 4 (M) x 8 (N) block (see tile_coords),
+    // so A tile tm is wanted by eight workgroups and B tile tn by four.  Each
+    // pulls its own eighth of A (by tn % 8) and quarter of B (by tm % 4):
+    // every line of the block is requested about once, ahead of the
+    // direct-to-LDS loads that then hit in L2.
+    const int ptid = tid - 256;
+    auto tile_prefetch = [&](int t) {
+      const uint32_t sink = lds0 + kSinkOffset;
+      const bool p1 = DUAL && t >= nk0;
+      const int k0 = (p1 ? t - nk0 : t) * kBK;
+      if (ptid < 32) {
+        const Operand& o = p1 ? g.a[1] : g.a[0];
+        prefetch_slice<A_KC>(make_rsrc(o), o, k0, row0, sink, ptid, tn & 7, 8);
+      } else if (ptid < 96) {
+        const Operand& o = p1 ? g.b[1] : g.b[0];
+        prefetch_slice<B_KC>(make_rsrc(o), o, k0, col0, sink, ptid - 32, tm & 3, 4);
+      }
+    };
+#pragma unroll
+    for (int p = 1; p <= kPrefetch; ++p)
+      if (p < nk) tile_prefetch(p);
+    phase_end();
+    for (int t = 0; t < nk; ++t) {
+      if (t > 0) compute();
+      phase_end();  // phase 2t -> 2t+1
+      read_frags(t % kStages);
+      if (t + 1 + kPrefetch < nk) tile_prefetch(t + 1 + kPrefetch);
+      phase_end();  // phase 2t+1 -> 2t+2
+    }
+    compute();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -548,6 +815,17 @@ template <bool A_KC, bool B_KC>
 void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n)), block(kThreads);
   const bool dual = a.nk[1] > 0;
+  if (a.pp) {
+    const dim3 pblock(kPpThreads);
+    if (out_f32) {
+      if (dual) gemm_pp_kernel<A_KC, B_KC, true, true><<<grid, pblock, 0, st>>>(a);
+      else gemm_pp_kernel<A_KC, B_KC, true, false><<<grid, pblock, 0, st>>>(a);
+    } else {
+      if (dual) gemm_pp_kernel<A_KC, B_KC, false, true><<<grid, pblock, 0, st>>>(a);
+      else gemm_pp_kernel<A_KC, B_KC, false, false><<<grid, pblock, 0, st>>>(a);
+    }
+    return;
+  }
   if (out_f32) {
     if (dual) gemm_bf16_kernel<A_KC, B_KC, true, true><<<grid, block, 0, st>>>(a);
     else gemm_bf16_kernel<A_KC, B_KC, true, false><<<grid, block, 0, st>>>(a);
@@ -657,6 +935,12 @@ extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* 
   a.tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   MOC_REQUIRE(static_cast<int64_t>(a.tiles_m) * a.tiles_n < (1LL << 31), "moc_gemm: too many tiles");
   const bool of = c_dtype == MOC_F32;
+  // The 512-thread kernel relies on the buffer range check for rows past an
+  // operand's extent: every offset it forms must stay below 2^32.
+  auto no_wrap = [](const Operand& o) {
+    return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
+  };
+  a.pp = no_wrap(a.a[0]) && no_wrap(a.b[0]) && no_wrap(a.a[1]) && no_wrap(a.b[1]);
   if (la && lb) launch_bf16<true, true>(a, of, st);
   else if (la && !lb) launch_bf16<true, false>(a, of, st);
   else if (!la && lb) launch_bf16<false, true>(a, of, st);

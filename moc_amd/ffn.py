@@ -158,7 +158,7 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     side = _side_stream(dev)
     x2 = K.aligned_rows(x.reshape(-1, d))
     go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
-    if gcp and x.dtype == torch.bfloat16 and K.round_up(inter, 8) <= 8192:
+    if gcp and x.dtype == torch.bfloat16 and K.row_pitch(inter, torch.bfloat16) <= 8192:
         s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter)
     else:
         if gcp:

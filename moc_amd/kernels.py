@@ -34,9 +34,21 @@ def _rows_view(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     return t, ld
 
 
+def row_pitch(cols: int, dtype) -> int:
+    """Row pitch (elements) of a padded [rows, cols] allocation: a multiple of
+    8 elements (16 bytes, the MFMA load unit), and of 128 bytes once a row
+    spans 1 KB, so that the GEMM's 128-byte row segments are whole L2 lines
+    (one request each instead of two)."""
+    esz = torch.empty((), dtype=dtype).element_size()
+    cols = max(cols, 1)
+    if cols * esz >= 1024:
+        return round_up(cols * esz, 128) // esz
+    return round_up(cols, 8)
+
+
 def padded_empty(rows: int, cols: int, dtype, device) -> torch.Tensor:
-    """[rows, cols] view of a [rows, round_up(cols, 8)] allocation."""
-    return _empty((rows, round_up(max(cols, 1), 8)), dtype, device)[:, :cols]
+    """[rows, cols] view of a [rows, row_pitch(cols)] allocation."""
+    return _empty((rows, row_pitch(cols, dtype)), dtype, device)[:, :cols]
 
 
 def aligned_rows(t: torch.Tensor) -> torch.Tensor:
