@@ -510,15 +510,19 @@ void gemm_bf16_kernel(GemmArgs g) {
 // end of its compute phase, a whole K tile after issuing them.
 // ---------------------------------------------------------------------------
 constexpr int kPpThreads = 512;
+constexpr int kG0Loads = 4;   // of the 8 loads per operand and wave, those group 0 issues
 
 // One 16-byte load into the LDS sink for line `idx` of slice `slice` (of n)
 // of the K tile at k0: a KC tile is 256 rows of 128 bytes, an MN tile 64
-// k-rows of four 128-byte lines.  Lines past the operand read as zero.
+// k-rows of four 128-byte lines.  Lines past the operand or the slice read
+// as zero.
 template <bool KC>
 __device__ __forceinline__ void prefetch_slice(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
                                                int row0, uint32_t sink, int idx, int slice, int n) {
   uint32_t off;
-  if (KC) {
+  if (idx >= 256 / n) {
+    off = kOob;
+  } else if (KC) {
     const int r = row0 + slice * (256 / n) + idx;
     off = (r < o.ext && k0 < o.K) ? static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + k0) * 2)
                                   : kOob;
@@ -530,8 +534,9 @@ __device__ __forceinline__ void prefetch_slice(__amdgpu_buffer_rsrc_t rsrc, cons
   dma16(rsrc, __builtin_amdgcn_readfirstlane(sink), off);
 }
 
-// Direct-to-LDS load offsets of one operand for a group-0 wave: the eight
-// loads of a tile differ by a uniform stride, so only load 0 is kept.
+// Direct-to-LDS load offsets of one operand for a wave (index 0-3 within its
+// group): the eight loads of a tile differ by a uniform stride, so only load
+// 0 is kept.
 template <bool KC>
 struct LoadMap {
   uint32_t voff0;  // byte offset of load 0 at k = 0
@@ -553,30 +558,34 @@ struct LoadMap {
     }
   }
 
-  // All kLoads loads of the K tile at k0 into the tile at LDS byte `tile`
-  // (the placement of TileMap::issue2).  A KC chunk at k >= K reads as zero.
-  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
-                                        uint32_t tile, int wave) const {
-    const uint32_t jstride = KC ? static_cast<uint32_t>(4 * kRowsPerLoad * o.ld * 2)
-                                : static_cast<uint32_t>(8 * o.ld * 2);
+  // Lane offset of load 0 of the K tile at k0; a KC chunk at k >= K reads as
+  // zero (kOob + j * stride stays >= 2^31).
+  __device__ __forceinline__ uint32_t tile_base(const Operand& o, int k0) const {
     const uint32_t kofs = KC ? static_cast<uint32_t>(k0) * 2u
                              : static_cast<uint32_t>(static_cast<int64_t>(k0) * o.ld * 2);
     uint32_t b = voff0 + kofs;
-    if (KC && k0 + kchunk >= o.K) b = kOob;  // kOob + j * jstride stays >= 2^31
-    // opaque: keeps the compiler from hoisting the eight offsets out of the
-    // K loop (they would stay live in registers the 512-thread kernel lacks)
+    if (KC && k0 + kchunk >= o.K) b = kOob;
+    // opaque: keeps the compiler from hoisting the per-load offsets out of
+    // the K loop (they would stay live in registers the 512-thread kernel
+    // lacks)
     asm volatile("" : "+v"(b));
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + (j * 4 + wave) * 1024);
-      dma16(rsrc, m0, b + j * jstride);
-    }
+    return b;
+  }
+
+  // Load j of the K tile whose tile_base is b into the tile at LDS byte
+  // `tile` (the placement of TileMap::issue2).
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, uint32_t b,
+                                        uint32_t tile, int wave, int j) const {
+    const uint32_t jstride = KC ? static_cast<uint32_t>(4 * kRowsPerLoad * o.ld * 2)
+                                : static_cast<uint32_t>(8 * o.ld * 2);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + (j * 4 + wave) * 1024);
+    dma16(rsrc, m0, b + j * jstride);
   }
 
   // KC, K % 8 != 0: zero the elements k >= K of the chunk that straddles K
   // (its loads must have landed).
   __device__ __forceinline__ void zero_straddle(char* lds, const Operand& o, int k0,
-                                                uint32_t tile, int wave, int lane) const {
+                                                uint32_t tile, int wave, int lane, int j0, int j1) const {
     const int k = k0 + kchunk;
     if (!(k < o.K && o.K < k + 8)) return;
     const int valid = o.K - k;  // 1 .. 7 elements stay
@@ -586,6 +595,7 @@ struct LoadMap {
       keep[d] = 2 * d + 1 < valid ? 0xFFFFFFFFu : (2 * d < valid ? 0x0000FFFFu : 0u);
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
+      if (j < j0 || j >= j1) continue;
       uint4* q = reinterpret_cast<uint4*>(lds + tile + (j * 4 + wave) * 1024 + lane * 16);
       uint4 v = *q;
       v.x &= keep[0];
@@ -642,14 +652,17 @@ void gemm_pp_kernel(GemmArgs g) {
       for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
     }
   };
+  // The 32 MFMAs of a K tile (order pinned).
   auto compute = [&]() {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
   };
 
   // Workgroup barrier between phases; the scheduling fences keep the compiler
@@ -661,56 +674,70 @@ void gemm_pp_kernel(GemmArgs g) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  if (grp == 0) {
-    LoadMap<A_KC> ma0, ma1;
-    LoadMap<B_KC> mb0, mb1;
-    ma0.init(g.a[0], row0, sw, lane);
-    mb0.init(g.b[0], col0, sw, lane);
-    const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(g.a[0]), rb0 = make_rsrc(g.b[0]);
-    __amdgpu_buffer_rsrc_t ra1 = ra0, rb1 = rb0;
-    if (DUAL) {
-      ma1.init(g.a[1], row0, sw, lane);
-      mb1.init(g.b[1], col0, sw, lane);
-      ra1 = make_rsrc(g.a[1]);
-      rb1 = make_rsrc(g.b[1]);
-    }
-    auto load_tile = [&](int t) {
-      const int st = t % kStages;
-      const uint32_t at = lds0 + st * kTileBytes, bt = lds0 + kBOffset + st * kTileBytes;
-      if (DUAL && t >= nk0) {
-        const int k0 = (t - nk0) * kBK;
-        ma1.issue(ra1, g.a[1], k0, at, sw);
-        mb1.issue(rb1, g.b[1], k0, bt, sw);
-      } else {
-        const int k0 = t * kBK;
-        ma0.issue(ra0, g.a[0], k0, at, sw);
-        mb0.issue(rb0, g.b[0], k0, bt, sw);
+  LoadMap<A_KC> ma0, ma1;
+  LoadMap<B_KC> mb0, mb1;
+  ma0.init(g.a[0], row0, sw, lane);
+  mb0.init(g.b[0], col0, sw, lane);
+  const __amdgpu_buffer_rsrc_t ra0 = make_rsrc(g.a[0]), rb0 = make_rsrc(g.b[0]);
+  __amdgpu_buffer_rsrc_t ra1 = ra0, rb1 = rb0;
+  if (DUAL) {
+    ma1.init(g.a[1], row0, sw, lane);
+    mb1.init(g.b[1], col0, sw, lane);
+    ra1 = make_rsrc(g.a[1]);
+    rb1 = make_rsrc(g.b[1]);
+  }
+  // Loads [j0, j1) of A and of B of K tile t into its stage.
+  auto load_tile = [&](int t, int j0, int j1) {
+    const int st = t % kStages;
+    const uint32_t at = lds0 + st * kTileBytes, bt = lds0 + kBOffset + st * kTileBytes;
+    const bool p1 = DUAL && t >= nk0;
+    const int k0 = (p1 ? t - nk0 : t) * kBK;
+    const Operand& oa = p1 ? g.a[1] : g.a[0];
+    const Operand& ob = p1 ? g.b[1] : g.b[0];
+    const LoadMap<A_KC>& la = p1 ? ma1 : ma0;
+    const LoadMap<B_KC>& lb = p1 ? mb1 : mb0;
+    const uint32_t ba = la.tile_base(oa, k0), bb = lb.tile_base(ob, k0);
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j)
+      if (j >= j0 && j < j1) {
+        la.issue(p1 ? ra1 : ra0, oa, ba, at, sw, j);
+        lb.issue(p1 ? rb1 : rb0, ob, bb, bt, sw, j);
       }
-    };
-    // After tile t's loads have landed: zero KC elements beyond a K that is
-    // not a multiple of 8 (only the last tile of a product can need it).
-    auto fix_tile = [&](int t) {
-      const int st = t % kStages;
-      const uint32_t at = st * kTileBytes, bt = kBOffset + st * kTileBytes;
-      const bool p1 = DUAL && t >= nk0;
-      const Operand& oa = p1 ? g.a[1] : g.a[0];
-      const int k0 = (p1 ? t - nk0 : t) * kBK;
-      if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
-      if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane);
-      if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane);
-    };
-    load_tile(0);
+  };
+  // After loads [j0, j1) of tile t have landed: zero KC elements beyond a K
+  // that is not a multiple of 8 (only the last tile of a product can need it).
+  auto fix_tile = [&](int t, int j0, int j1) {
+    const int st = t % kStages;
+    const uint32_t at = st * kTileBytes, bt = kBOffset + st * kTileBytes;
+    const bool p1 = DUAL && t >= nk0;
+    const Operand& oa = p1 ? g.a[1] : g.a[0];
+    const int k0 = (p1 ? t - nk0 : t) * kBK;
+    if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
+    // kchunk depends on the lane only, so the product-0 maps serve both
+    if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, j0, j1);
+    if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane, j0, j1);
+  };
+
+  // The loads of K tile t+1 are split between the groups: group 0 issues
+  // its share at the start of phase 2t, group 1 the rest at the start of
+  // phase 2t+1 (it would otherwise idle at the barrier there), and each
+  // waits for its own before the barrier that ends phase 2t+1.  Issuing a
+  // whole tile from one group stalls that group's phase: the address unit
+  // accepts a 1 KB load every ~25 cycles, 64 per tile.
+  if (grp == 0) {
+    load_tile(0, 0, kLoads);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    fix_tile(0);
+    fix_tile(0, 0, kLoads);
     phase_end();
     for (int t = 0; t < nk; ++t) {
-      if (t + 1 < nk) load_tile(t + 1);
+      // loads j of tile t+1 go out between the k16 steps' fragment reads
+      if (t + 1 < nk) load_tile(t + 1, 0, kG0Loads);
       read_frags(t % kStages);
       phase_end();  // phase 2t -> 2t+1
       compute();
       if (t + 1 < nk) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        fix_tile(t + 1);
+        fix_tile(t + 1, 0, kG0Loads);
       }
       phase_end();  // phase 2t+1 -> 2t+2
     }
@@ -718,20 +745,20 @@ void gemm_pp_kernel(GemmArgs g) {
     // L2 prefetch, shared out over the workgroups of an XCD: the 32
     // concurrent tiles of an XCD form a 4 (M) x 8 (N) block (see tile_coords),
     // so A tile tm is wanted by eight workgroups and B tile tn by four.  Each
-    // pulls its own eighth of A (by tn % 8) and quarter of B (by tm % 4):
-    // every line of the block is requested about once, ahead of the
-    // direct-to-LDS loads that then hit in L2.
-    const int ptid = tid - 256;
+    // pulls its own eighth of A (by tn % 8, wave 0 of the group) and quarter
+    // of B (by tm % 4, wave 1): every line of the block is requested about
+    // once, ahead of the direct-to-LDS loads that then hit in L2.  Waves 0
+    // and 1 issue exactly one load per prefetch, the others none.
     auto tile_prefetch = [&](int t) {
       const uint32_t sink = lds0 + kSinkOffset;
       const bool p1 = DUAL && t >= nk0;
       const int k0 = (p1 ? t - nk0 : t) * kBK;
-      if (ptid < 32) {
+      if (sw == 0) {
         const Operand& o = p1 ? g.a[1] : g.a[0];
-        prefetch_slice<A_KC>(make_rsrc(o), o, k0, row0, sink, ptid, tn & 7, 8);
-      } else if (ptid < 96) {
+        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, k0, row0, sink, lane, tn & 7, 8);
+      } else if (sw == 1) {
         const Operand& o = p1 ? g.b[1] : g.b[0];
-        prefetch_slice<B_KC>(make_rsrc(o), o, k0, col0, sink, ptid - 32, tm & 3, 4);
+        prefetch_slice<B_KC>(p1 ? rb1 : rb0, o, k0, col0, sink, lane, tm & 3, 4);
       }
     };
 #pragma unroll
@@ -741,8 +768,17 @@ void gemm_pp_kernel(GemmArgs g) {
     for (int t = 0; t < nk; ++t) {
       if (t > 0) compute();
       phase_end();  // phase 2t -> 2t+1
+      const bool pf = t + 1 + kPrefetch < nk;
+      if (t + 1 < nk) load_tile(t + 1, kG0Loads, kLoads);
+      if (pf) tile_prefetch(t + 1 + kPrefetch);
       read_frags(t % kStages);
-      if (t + 1 + kPrefetch < nk) tile_prefetch(t + 1 + kPrefetch);
+      if (t + 1 < nk) {
+        // the prefetch (one load, waves 0-1) was issued after this tile's
+        // loads and may stay in flight: vector memory loads retire in order
+        if (pf && sw < 2) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        fix_tile(t + 1, kG0Loads, kLoads);
+      }
       phase_end();  // phase 2t+1 -> 2t+2
     }
     compute();
