@@ -142,6 +142,24 @@ int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
              int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn, void* C,
              int64_t ldc, int c_dtype, void* stream);
 
+/* moc_gemm with a caller-provided device workspace (16-byte aligned).  A bf16
+ * product whose 256x256 output tiles fill at most half the CUs (the weight
+ * gradients of small models) then splits its K range over several
+ * workgroups per tile, writes f32 partial tiles into the workspace and sums
+ * them in a fixed order (results do not depend on timing).  With a null or
+ * too small workspace it is moc_gemm.  Same reference call sites as
+ * moc_gemm. */
+int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+                int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2, const void* A2,
+                int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn,
+                void* C, int64_t ldc, int c_dtype, void* workspace, int64_t workspace_bytes,
+                void* stream);
+
+/* Workspace bytes moc_gemm_ws uses for this shape on the current device (0:
+ * the product does not split).  No counterpart in the reference (its GEMMs
+ * are library calls). */
+int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2);
+
 /* ---------------------------------------------------------------- decode */
 /* y[b, r] = bf16(sum_h x[b,h] W[r,h]) for b < nb <= 16 tokens: the decode
  * gate projection (module.gate_proj(x) before

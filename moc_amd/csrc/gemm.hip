@@ -41,6 +41,8 @@
 // contiguous, M-grouped run of tiles that shares its L2.
 //
 // f32 operands use a plain FMA kernel (parity path for f32 models).
+#include <algorithm>
+
 #include "abi.h"
 #include "common.h"
 
@@ -86,6 +88,9 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int vec_store;  // C rows are 16-byte aligned: vector epilogue stores
   int pp;         // the 512-thread kernel may run this product
+  int ksplit;     // workgroups per C tile (split-K; 512-thread kernel only)
+  int kper;       // K tiles per split
+  int64_t ws_stride;  // f32 elements between the partial C matrices of two splits
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -607,7 +612,8 @@ struct LoadMap {
   }
 };
 
-template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL>
+// SPLIT: split-K launch (f32 partial tiles into the workspace slices).
+template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT>
 __global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
@@ -617,8 +623,12 @@ void gemm_pp_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2;
   const int sw = wave & 3;
+  // split-K: workgroup bid runs K tiles [split * kper, +kper) of its tile
+  // and writes an f32 partial tile into slice `split` of the workspace
+  const int split = SPLIT ? static_cast<int>(blockIdx.x % g.ksplit) : 0;
+  const int tbid = SPLIT ? static_cast<int>(blockIdx.x / g.ksplit) : static_cast<int>(blockIdx.x);
   int tm, tn;
-  tile_coords(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  tile_coords(tbid, g.tiles_m, g.tiles_n, tm, tn);
   const int row0 = tm * kBM;
   const int col0 = tn * kBN;
   const int wm = (sw >> 1) * 128;
@@ -626,7 +636,9 @@ void gemm_pp_kernel(GemmArgs g) {
   const uint32_t lds0 = lds_addr(lds);
 
   const int nk0 = g.nk[0];
-  const int nk = nk0 + (DUAL ? g.nk[1] : 0);
+  const int nk_all = nk0 + (DUAL ? g.nk[1] : 0);
+  const int kt0 = SPLIT ? split * g.kper : 0;           // first K tile of this workgroup
+  const int nk = SPLIT ? min(nk_all, kt0 + g.kper) : nk_all;  // one past its last
 
   FragMap<A_KC> fa_map;
   FragMap<B_KC> fb_map;
@@ -725,12 +737,11 @@ void gemm_pp_kernel(GemmArgs g) {
   // whole tile from one group stalls that group's phase: the address unit
   // accepts a 1 KB load every ~25 cycles, 64 per tile.
   if (grp == 0) {
-    load_tile(0, 0, kLoads);
+    load_tile(kt0, 0, kLoads);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    fix_tile(0, 0, kLoads);
+    fix_tile(kt0, 0, kLoads);
     phase_end();
-    for (int t = 0; t < nk; ++t) {
-      // loads j of tile t+1 go out between the k16 steps' fragment reads
+    for (int t = kt0; t < nk; ++t) {
       if (t + 1 < nk) load_tile(t + 1, 0, kG0Loads);
       read_frags(t % kStages);
       phase_end();  // phase 2t -> 2t+1
@@ -763,10 +774,10 @@ void gemm_pp_kernel(GemmArgs g) {
     };
 #pragma unroll
     for (int p = 1; p <= kPrefetch; ++p)
-      if (p < nk) tile_prefetch(p);
+      if (kt0 + p < nk) tile_prefetch(kt0 + p);
     phase_end();
-    for (int t = 0; t < nk; ++t) {
-      if (t > 0) compute();
+    for (int t = kt0; t < nk; ++t) {
+      if (t > kt0) compute();
       phase_end();  // phase 2t -> 2t+1
       const bool pf = t + 1 + kPrefetch < nk;
       if (t + 1 < nk) load_tile(t + 1, kG0Loads, kLoads);
@@ -784,7 +795,52 @@ void gemm_pp_kernel(GemmArgs g) {
     compute();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+  if (SPLIT) {
+    GemmArgs gs = g;
+    gs.C = static_cast<float*>(g.C) + split * g.ws_stride;
+    store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
+  } else {
+    store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+  }
+}
+
+// Sum of the ksplit f32 partial tiles of a split-K GEMM, in split order (the
+// result does not depend on timing), converted to the output type.  One
+// thread per four consecutive columns of a row.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t stride,
+                                                            int ksplit, int M, int N, int64_t ldw,
+                                                            void* __restrict__ C, int64_t ldc, int vec) {
+  const int qpr = (N + 3) / 4;
+  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (q >= static_cast<int64_t>(M) * qpr) return;
+  const int row = static_cast<int>(q / qpr), c = static_cast<int>(q % qpr) * 4;
+  const float* p = ws + row * ldw + c;
+  float4 s = *reinterpret_cast<const float4*>(p);
+  for (int i = 1; i < ksplit; ++i) {
+    const float4 v = *reinterpret_cast<const float4*>(p + i * stride);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  const float r[4] = {s.x, s.y, s.z, s.w};
+  if (OUT_F32) {
+    float* dst = static_cast<float*>(C) + row * ldc + c;
+    if (vec && c + 4 <= N) {
+      *reinterpret_cast<float4*>(dst) = s;
+    } else {
+      for (int e = 0; e < 4 && c + e < N; ++e) dst[e] = r[e];
+    }
+  } else {
+    uint16_t* dst = static_cast<uint16_t*>(C) + row * ldc + c;
+    if (vec && c + 4 <= N) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]));
+    } else {
+      for (int e = 0; e < 4 && c + e < N; ++e)
+        dst[e] = static_cast<uint16_t>(pack_bf16x2(r[e], 0.0f) & 0xFFFF);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -849,16 +905,19 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgsF32 g) {
 
 template <bool A_KC, bool B_KC>
 void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n)), block(kThreads);
+  const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n * a.ksplit)), block(kThreads);
   const bool dual = a.nk[1] > 0;
   if (a.pp) {
     const dim3 pblock(kPpThreads);
-    if (out_f32) {
-      if (dual) gemm_pp_kernel<A_KC, B_KC, true, true><<<grid, pblock, 0, st>>>(a);
-      else gemm_pp_kernel<A_KC, B_KC, true, false><<<grid, pblock, 0, st>>>(a);
+    if (a.ksplit > 1) {  // partial tiles are f32
+      if (dual) gemm_pp_kernel<A_KC, B_KC, true, true, true><<<grid, pblock, 0, st>>>(a);
+      else gemm_pp_kernel<A_KC, B_KC, true, false, true><<<grid, pblock, 0, st>>>(a);
+    } else if (out_f32) {
+      if (dual) gemm_pp_kernel<A_KC, B_KC, true, true, false><<<grid, pblock, 0, st>>>(a);
+      else gemm_pp_kernel<A_KC, B_KC, true, false, false><<<grid, pblock, 0, st>>>(a);
     } else {
-      if (dual) gemm_pp_kernel<A_KC, B_KC, false, true><<<grid, pblock, 0, st>>>(a);
-      else gemm_pp_kernel<A_KC, B_KC, false, false><<<grid, pblock, 0, st>>>(a);
+      if (dual) gemm_pp_kernel<A_KC, B_KC, false, true, false><<<grid, pblock, 0, st>>>(a);
+      else gemm_pp_kernel<A_KC, B_KC, false, false, false><<<grid, pblock, 0, st>>>(a);
     }
     return;
   }
@@ -892,16 +951,73 @@ bool make_operand(const void* p, int64_t ld, bool kc, int64_t ext, int64_t K, Op
   return true;
 }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Split-K plan of a bf16 GEMM: a product whose 256x256 tiles fill at most
+// half the CUs runs each tile as `ksplit` workgroups over consecutive ranges
+// of at least 4 K tiles.  ldw: row pitch of the f32 partials.
+struct SplitPlan {
+  int ksplit = 1;
+  int kper = 0;
+  int64_t ldw = 0;
+  int64_t bytes = 0;
+};
+
+SplitPlan plan_split(int64_t M, int64_t N, int nk) {
+  SplitPlan p;
+  p.kper = nk;
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const int cus = cu_count();
+  if (tiles <= 0 || 2 * tiles > cus) return p;
+  int ks = static_cast<int>(std::min<int64_t>(cus / tiles, nk / 4));
+  if (ks < 2) return p;
+  const int kper = (nk + ks - 1) / ks;
+  ks = (nk + kper - 1) / kper;
+  if (ks < 2) return p;
+  p.ksplit = ks;
+  p.kper = kper;
+  p.ldw = (N + 3) & ~3LL;
+  p.bytes = static_cast<int64_t>(ks) * M * p.ldw * 4;
+  return p;
+}
+
 }  // namespace
 }  // namespace moc
 
 using namespace moc;
+
+extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2) {
+  if (dtype != MOC_BF16 || M <= 0 || N <= 0 || K < 0 || K2 < 0) return 0;
+  const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
+  return plan_split(M, N, nk).bytes;
+}
 
 extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
                         int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
                         const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
                         int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
                         void* stream) {
+  return moc_gemm_ws(dtype, M, N, K, A, a_sm, a_sk, B, b_sk, b_sn, K2, A2, a2_sm, a2_sk, B2, b2_sk,
+                     b2_sn, C, ldc, c_dtype, nullptr, 0, stream);
+}
+
+extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+                           int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
+                           const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
+                           int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_gemm: dtype must be bf16 or f32");
   MOC_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K2 >= 0, "moc_gemm: negative extent");
   MOC_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && K2 < (1LL << 31),
@@ -977,9 +1093,39 @@ extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* 
     return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
   };
   a.pp = no_wrap(a.a[0]) && no_wrap(a.b[0]) && no_wrap(a.a[1]) && no_wrap(a.b[1]);
-  if (la && lb) launch_bf16<true, true>(a, of, st);
-  else if (la && !lb) launch_bf16<true, false>(a, of, st);
-  else if (!la && lb) launch_bf16<false, true>(a, of, st);
-  else launch_bf16<false, false>(a, of, st);
-  return check_launch("gemm_bf16_kernel");
+  a.ksplit = 1;
+  a.kper = a.nk[0] + a.nk[1];
+  a.ws_stride = 0;
+  const SplitPlan sp = plan_split(M, N, a.nk[0] + a.nk[1]);
+  const bool split = a.pp && sp.ksplit > 1 && workspace != nullptr && workspace_bytes >= sp.bytes &&
+                     reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
+  GemmArgs run = a;
+  if (split) {
+    // partial tiles in f32 go to the workspace; the reduction writes C
+    run.ksplit = sp.ksplit;
+    run.kper = sp.kper;
+    run.ws_stride = M * sp.ldw;
+    run.C = workspace;
+    run.ldc = sp.ldw;
+    run.vec_store = 1;
+  }
+  const bool of_run = split ? true : of;
+  if (la && lb) launch_bf16<true, true>(run, of_run, st);
+  else if (la && !lb) launch_bf16<true, false>(run, of_run, st);
+  else if (!la && lb) launch_bf16<false, true>(run, of_run, st);
+  else launch_bf16<false, false>(run, of_run, st);
+  if (!split) return check_launch("gemm_bf16_kernel");
+  {
+    const int rc = check_launch("gemm_bf16_kernel");
+    if (rc != MOC_OK) return rc;
+    const int64_t quads = M * ((N + 3) / 4);
+    const dim3 grid(static_cast<unsigned>((quads + 255) / 256));
+    if (of)
+      splitk_reduce_kernel<true><<<grid, 256, 0, st>>>(static_cast<const float*>(workspace), run.ws_stride,
+                                                       sp.ksplit, (int)M, (int)N, sp.ldw, C, ldc, a.vec_store);
+    else
+      splitk_reduce_kernel<false><<<grid, 256, 0, st>>>(static_cast<const float*>(workspace), run.ws_stride,
+                                                        sp.ksplit, (int)M, (int)N, sp.ldw, C, ldc, a.vec_store);
+    return check_launch("splitk_reduce_kernel");
+  }
 }

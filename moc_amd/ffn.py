@@ -83,16 +83,26 @@ def _check_inputs(x, gate_w, up_w, down_w, strict_aux: bool, index_save_dtype):
 _SIDE_STREAMS: dict = {}
 
 
-def _side_stream(device, which: int = 0) -> torch.cuda.Stream:
-    """Extra streams per device (default priority) for independent GEMMs: a
+def _side_stream(device) -> torch.cuda.Stream:
+    """A second stream per device (default priority) for independent work: a
     256x256-tile GEMM whose tile count leaves CUs idle in its last round (or
     a short selection/elementwise kernel) overlaps another one instead."""
-    key = (device.index if device.index is not None else torch.cuda.current_device(), which)
+    key = device.index if device.index is not None else torch.cuda.current_device()
     s = _SIDE_STREAMS.get(key)
     if s is None:
         s = torch.cuda.Stream(device=device)
         _SIDE_STREAMS[key] = s
     return s
+
+
+_CU_COUNT: dict = {}
+
+
+def _cu_count(device) -> int:
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    if key not in _CU_COUNT:
+        _CU_COUNT[key] = torch.cuda.get_device_properties(key).multi_processor_count
+    return _CU_COUNT[key]
 
 
 def _on_side(side, tensors, fn):
@@ -116,10 +126,19 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     rows = x2.shape[0]
     g = K.padded_empty(rows, inter, x.dtype, x.device)
     K.linear(x2, gate_w, out=g)
-    # U = x Wu^T runs on the side stream, beside the selection over G
+    # U = x Wu^T runs on the side stream, beside the selection over G, and
+    # so does the 16-byte-row copy of W_down (when its rows need one), which
+    # the backward reuses
     side = _side_stream(x.device)
     u = K.padded_empty(rows, inter, x.dtype, x.device)
-    _on_side(side, (x2, up_w, u), lambda: K.linear(x2, up_w, out=u))
+    wd = (K.padded_empty(down_w.shape[0], down_w.shape[1], down_w.dtype, x.device)
+          if K.needs_alignment(down_w) else down_w)
+
+    def side_work():
+        K.linear(x2, up_w, out=u)
+        K.aligned_rows(down_w, out=wd)
+
+    _on_side(side, (x2, up_w, u, down_w, wd), side_work)
     if selection == "topk":
         vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype)
     elif selection == "post_silu_abs":
@@ -132,25 +151,27 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     torch.cuda.current_stream(x.device).wait_stream(side)
     u_s, s_s, z_s, z_full = K.sparse_forward_aux(vals, idx, u, inter, want_s=save_s, want_z=save_s)
     del u
-    wd = K.aligned_rows(down_w)
     out = K.gemm(z_full, wd.t())
     del z_full
     kk = idx.shape[-1]
     shp = (*x.shape[:-1], kk)
     return (out.reshape(*x.shape[:-1], down_w.shape[0]), idx.reshape(shp), vals.reshape(shp),
             u_s.reshape(shp), None if s_s is None else s_s.reshape(shp),
-            None if z_s is None else z_s.reshape(shp))
+            None if z_s is None else z_s.reshape(shp), wd)
 
 
 def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool):
     """Shared MoC backward (moc/ffn.py:175-259 and the GCP form :423-497).
+    down_w may be the forward's 16-byte-row copy of W_down (same values).
 
     dWd = go^T Z, gZ = go Wd, (gG, gU) = sparse_backward_aux, dWg = gG^T x,
     dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products).
 
-    The weight gradients (176 tiles of 256x256 at the 1b shape: two thirds
-    of the CUs) run on side streams, dWd beside gZ and the aux kernel, dWg
-    and dWu (each on its own stream) beside dX."""
+    dWd (176 tiles of 256x256 at the 1b shape: two thirds of the CUs) runs on
+    the side stream beside gZ and the aux kernel.  dWg and dWu overlap dX
+    only when together they fill at most the CUs once; larger ones run in
+    order with dX (overlapping them measured slower at the 1b shape: the
+    concurrent GEMMs split each XCD's L2 between their tile groups)."""
     d = x.shape[-1]
     inter = gate_w.shape[0]
     dev = x.device
@@ -175,14 +196,18 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     del gz
     grad_gate_w = torch.empty(inter, d, dtype=gate_w.dtype, device=dev)
     grad_up_w = torch.empty(inter, d, dtype=up_w.dtype, device=dev)
-    side2 = _side_stream(dev, 1)
-    _on_side(side, (grad_g, x2, grad_gate_w),
-             lambda: K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype))
-    _on_side(side2, (grad_u, x2, grad_up_w),
-             lambda: K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype))
+
+    def weight_grads():
+        K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype)
+        K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype)
+
+    if 2 * K.gemm_tiles(inter, d) <= _cu_count(dev):
+        # small weight gradients leave most CUs idle: overlap them with dX
+        _on_side(side, (grad_g, grad_u, x2, grad_gate_w, grad_up_w), weight_grads)
+    else:
+        weight_grads()
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
     main.wait_stream(side)
-    main.wait_stream(side2)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
 
 
@@ -202,9 +227,9 @@ class _MoCFunction(torch.autograd.Function):
         _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
         inter = gate_w.shape[0]
         idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        out, idx, vals, u_s, s_s, z_s = _forward_common(
+        out, idx, vals, u_s, s_s, z_s, wd = _forward_common(
             x, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=True)
-        ctx.save_for_backward(x, idx, vals, u_s, s_s, z_s, gate_w, up_w, down_w)
+        ctx.save_for_backward(x, idx, vals, u_s, s_s, z_s, gate_w, up_w, wd)
         ctx.k = idx.shape[-1]
         ctx.inter = inter
         return out
@@ -250,9 +275,9 @@ class _MoCGCPFunction(torch.autograd.Function):
         _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
         inter = gate_w.shape[0]
         idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        out, idx, vals, u_s, _, _ = _forward_common(
+        out, idx, vals, u_s, _, _, wd = _forward_common(
             x, gate_w, up_w, down_w, k, "topk", idx_dtype, save_s=False)
-        ctx.save_for_backward(x, idx, vals, u_s, gate_w, up_w, down_w)
+        ctx.save_for_backward(x, idx, vals, u_s, gate_w, up_w, wd)
         ctx.k = k
         ctx.inter = inter
         return out

@@ -51,14 +51,29 @@ def padded_empty(rows: int, cols: int, dtype, device) -> torch.Tensor:
     return _empty((rows, row_pitch(cols, dtype)), dtype, device)[:, :cols]
 
 
-def aligned_rows(t: torch.Tensor) -> torch.Tensor:
-    """Row-major copy (if needed) whose rows are 16-byte aligned for MFMA loads."""
+def gemm_tiles(m: int, n: int) -> int:
+    """Workgroups (256x256 output tiles) of a bf16 GEMM with an [m, n] output."""
+    return ((m + 255) // 256) * ((n + 255) // 256)
+
+
+def needs_alignment(t: torch.Tensor) -> bool:
+    """True if aligned_rows(t) would copy: a bf16 matrix whose rows are not
+    16-byte aligned."""
     t, ld = _rows_view(t)
-    if t.dtype != torch.bfloat16:
+    return t.dtype == torch.bfloat16 and not (ld % 8 == 0 and t.data_ptr() % 16 == 0)
+
+
+def aligned_rows(t: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Row-major copy (if needed) whose rows are 16-byte aligned for MFMA loads.
+    `out`, if given, is the destination of the copy (a padded_empty of t's
+    shape); it is ignored when t needs no copy."""
+    t, ld = _rows_view(t)
+    if not needs_alignment(t):
         return t
-    if ld % 8 == 0 and t.data_ptr() % 16 == 0:
-        return t
-    out = padded_empty(t.shape[0], t.shape[1], t.dtype, t.device)
+    if out is None:
+        out = padded_empty(t.shape[0], t.shape[1], t.dtype, t.device)
+    elif out.shape != t.shape or out.dtype != t.dtype or out.stride(1) != 1 or out.stride(0) % 8:
+        raise ValueError("aligned_rows: out must be a padded [rows, cols] bf16 view")
     N.call("moc_copy_pad_2d", N.MOC_BF16, t.data_ptr(), t.shape[0], t.shape[1], ld,
            out.data_ptr(), out.stride(0), out.stride(0), N.stream_of(t))
     return out
@@ -266,9 +281,13 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
         a2p, a2s0, a2s1 = _operand(a2, bf16)
         b2p, b2s0, b2s1 = _operand(b2, bf16)
     ldc = out.stride(0) if M > 1 else max(Nn, 1)
-    N.call("moc_gemm", N.dtype_code(a.dtype), M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
+    code = N.dtype_code(a.dtype)
+    # products with few output tiles split K over a workspace of f32 partials
+    ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2) if bf16 else 0
+    ws = _empty((ws_bytes,), torch.uint8, a.device) if ws_bytes > 0 else None
+    N.call("moc_gemm_ws", code, M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
            bs0, bs1, K2, N.ptr(a2p), a2s0, a2s1, N.ptr(b2p), b2s0, b2s1, out.data_ptr(), ldc,
-           N.dtype_code(out_dtype), N.stream_of(a))
+           N.dtype_code(out_dtype), N.ptr(ws), ws_bytes, N.stream_of(a))
     return out
 
 

@@ -34,6 +34,11 @@ def K():
     return kernels
 
 
+def N():
+    from moc_amd import _native
+    return _native
+
+
 def gen(seed):
     return torch.Generator().manual_seed(seed)
 
@@ -104,6 +109,50 @@ def test_gemm_weight_gradient_shape(a_kc, b_kc):
     assert torch.equal(first, again)
     out16 = K().gemm(ad, bd)
     bf16_close(out16, ref, ulps=1, atol=2e-3)
+
+
+@pytest.mark.parametrize("layout", ["mnmn", "kcmn", "kckc"])
+@pytest.mark.parametrize("mnk", [(768, 2048, 8192), (520, 300, 5000), (72, 1000, 2048)])
+def test_gemm_split_k(layout, mnk):
+    """Products with few output tiles split K over f32 partials in a
+    workspace: results match the fp32 reference, do not depend on timing
+    (repeat equality) and agree with the unsplit kernel to f32 rounding."""
+    M, Nn, Kk = mnk
+    g = torch.Generator(device=DEV).manual_seed(11)
+    a = torch.randn(M, Kk, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randn(Kk, Nn, device=DEV, generator=g).to(torch.bfloat16)
+    ref = a.float() @ b.float()
+    ad = K().aligned_rows(a) if layout in ("kcmn", "kckc") else a.t().contiguous().t()
+    bd = K().aligned_rows(b.t().contiguous()).t() if layout == "kckc" else K().aligned_rows(b)
+    ws = N().query("moc_gemm_workspace_size", N().MOC_BF16, M, Nn, Kk, 0)
+    assert ws > 0, "shape expected to split"
+    first = K().gemm(ad, bd, out_dtype=torch.float32)
+    close(first, ref, rtol=1e-4, atol=3e-3)
+    assert torch.equal(first, K().gemm(ad, bd, out_dtype=torch.float32))
+    out16 = K().gemm(ad, bd)
+    bf16_close(out16, ref, ulps=1, atol=3e-3)
+    # the unsplit kernel (moc_gemm, no workspace) on the same operands
+    flat = torch.empty(M, Nn, device=DEV, dtype=torch.float32)
+    a_, as0, as1 = K()._operand(ad, True)
+    b_, bs0, bs1 = K()._operand(bd, True)
+    N().call("moc_gemm", N().MOC_BF16, M, Nn, Kk, a_.data_ptr(), as0, as1, b_.data_ptr(), bs0, bs1,
+             0, None, 0, 0, None, 0, 0, flat.data_ptr(), Nn, N().MOC_F32, N().stream_of(ad))
+    close(first, flat, rtol=1e-5, atol=3e-3)  # f32 sums of K products in another order
+
+
+def test_gemm_split_k_dual():
+    """dX-shaped dual product at a small width: the split runs across both
+    products' K tiles."""
+    g = torch.Generator(device=DEV).manual_seed(12)
+    T, I, d = 4096, 2048, 768
+    gg = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    gu = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    assert N().query("moc_gemm_workspace_size", N().MOC_BF16, T, d, I, I) > 0
+    out = K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32)
+    ref = gg.float() @ wg.float() + gu.float() @ wu.float()
+    close(out, ref, rtol=1e-4, atol=1e-3)
 
 
 def test_gemm_dual_product_and_f32():
