@@ -186,20 +186,20 @@ def gcp_recompute(g_sparse: torch.Tensor, u_sparse: torch.Tensor):
 
 
 def gcp_recompute_scatter(g_sparse: torch.Tensor, u_sparse: torch.Tensor, topk_idx: torch.Tensor,
-                          inter: int):
-    """GCP recompute fused with the scatter of z -> (s_sparse, z_full); z_full
-    is a zero-filled [rows, inter] view of a padded buffer.  bf16."""
+                          inter: int, want_s: bool = True):
+    """GCP recompute fused with the scatter of z -> (s_sparse | None, z_full);
+    z_full is a zero-filled [rows, inter] view of a padded buffer.  bf16."""
     N.require_device(g_sparse, u_sparse, topk_idx)
     g = _sparse_2d(g_sparse)
     u = _sparse_2d(u_sparse)
     idx = _sparse_2d(topk_idx)
     rows, k = g.shape
-    s = torch.empty_like(g)
+    s = torch.empty_like(g) if want_s else None
     z_full = padded_empty(rows, inter, g.dtype, g.device)
     N.call("moc_gcp_recompute_scatter", N.dtype_code(g.dtype), g.data_ptr(), u.data_ptr(),
-           idx.data_ptr(), N.idx_code(idx.dtype), rows, k, inter, s.data_ptr(), z_full.data_ptr(),
+           idx.data_ptr(), N.idx_code(idx.dtype), rows, k, inter, N.ptr(s), z_full.data_ptr(),
            z_full.stride(0), N.stream_of(g))
-    return s.reshape(g_sparse.shape), z_full
+    return (s.reshape(g_sparse.shape) if want_s else None), z_full
 
 
 def sparse_backward_aux(topk_idx: torch.Tensor, g_sparse: torch.Tensor, u_sparse: torch.Tensor,
