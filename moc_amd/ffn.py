@@ -124,12 +124,12 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     inter = gate_w.shape[0]
     x2 = K.aligned_rows(x.reshape(-1, d))
     rows = x2.shape[0]
-    g = K.padded_empty(rows, inter, x.dtype, x.device)
-    K.linear(x2, gate_w, out=g)
-    # U = x Wu^T runs on the side stream, beside the selection over G, and
-    # so does the 16-byte-row copy of W_down (when its rows need one), which
-    # the backward reuses
+    # U = x Wu^T runs on the side stream, launched before G so that the two
+    # GEMMs share the CUs (each alone leaves its last round half empty) and U
+    # also overlaps the selection over G; the 16-byte-row copy of W_down
+    # (when its rows need one), which the backward reuses, follows U there
     side = _side_stream(x.device)
+    g = K.padded_empty(rows, inter, x.dtype, x.device)
     u = K.padded_empty(rows, inter, x.dtype, x.device)
     wd = (K.padded_empty(down_w.shape[0], down_w.shape[1], down_w.dtype, x.device)
           if K.needs_alignment(down_w) else down_w)
@@ -139,6 +139,7 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
         K.aligned_rows(down_w, out=wd)
 
     _on_side(side, (x2, up_w, u, down_w, wd), side_work)
+    K.linear(x2, gate_w, out=g)
     if selection == "topk":
         vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype)
     elif selection == "post_silu_abs":
