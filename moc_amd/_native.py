@@ -131,18 +131,22 @@ def query(name: str, *args) -> int:
 
 def stream_of(t: torch.Tensor) -> int:
     """HIP stream torch currently uses on t's device (as an integer handle)."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def require_device(*tensors: torch.Tensor) -> None:
+    dev = None
     for t in tensors:
         if t is None:
             continue
         if not t.is_cuda:
             raise ValueError("MoC HIP kernels require ROCm device tensors")
-    devs = {t.device for t in tensors if t is not None}
-    if len(devs) > 1:
-        raise ValueError(f"MoC HIP kernels need all tensors on one device, got {sorted(map(str, devs))}")
+        d = t.get_device()
+        if dev is None:
+            dev = d
+        elif d != dev:
+            devs = sorted({str(x.device) for x in tensors if x is not None})
+            raise ValueError(f"MoC HIP kernels need all tensors on one device, got {devs}")
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -95,16 +95,6 @@ def _side_stream(device) -> torch.cuda.Stream:
     return s
 
 
-_CU_COUNT: dict = {}
-
-
-def _cu_count(device) -> int:
-    key = device.index if device.index is not None else torch.cuda.current_device()
-    if key not in _CU_COUNT:
-        _CU_COUNT[key] = torch.cuda.get_device_properties(key).multi_processor_count
-    return _CU_COUNT[key]
-
-
 def _on_side(side, tensors, fn):
     """Run fn() on `side` after the current stream's queued work; tensors
     made on the current stream and used there are kept alive for it."""
@@ -202,7 +192,7 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
         K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype)
         K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype)
 
-    if 2 * K.gemm_tiles(inter, d) <= _cu_count(dev):
+    if 2 * K.gemm_tiles(inter, d) <= K.cu_count(x.get_device()):
         # small weight gradients leave most CUs idle: overlap them with dX
         _on_side(side, (grad_g, grad_u, x2, grad_gate_w, grad_up_w), weight_grads)
     else:

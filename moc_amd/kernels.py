@@ -39,7 +39,7 @@ def row_pitch(cols: int, dtype) -> int:
     8 elements (16 bytes, the MFMA load unit), and of 128 bytes once a row
     spans 1 KB, so that the GEMM's 128-byte row segments are whole L2 lines
     (one request each instead of two)."""
-    esz = torch.empty((), dtype=dtype).element_size()
+    esz = dtype.itemsize
     cols = max(cols, 1)
     if cols * esz >= 1024:
         return round_up(cols * esz, 128) // esz
@@ -48,7 +48,18 @@ def row_pitch(cols: int, dtype) -> int:
 
 def padded_empty(rows: int, cols: int, dtype, device) -> torch.Tensor:
     """[rows, cols] view of a [rows, row_pitch(cols)] allocation."""
-    return _empty((rows, row_pitch(cols, dtype)), dtype, device)[:, :cols]
+    return _empty((rows, row_pitch(cols, dtype)), dtype, device).narrow(1, 0, cols)
+
+
+_CUS: dict = {}
+
+
+def cu_count(device_index: int) -> int:
+    """Compute units of a device (cached)."""
+    n = _CUS.get(device_index)
+    if n is None:
+        n = _CUS[device_index] = torch.cuda.get_device_properties(device_index).multi_processor_count
+    return n
 
 
 def gemm_tiles(m: int, n: int) -> int:
@@ -283,7 +294,9 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
     ldc = out.stride(0) if M > 1 else max(Nn, 1)
     code = N.dtype_code(a.dtype)
     # products with few output tiles split K over a workspace of f32 partials
-    ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2) if bf16 else 0
+    ws_bytes = 0
+    if bf16 and 2 * gemm_tiles(M, Nn) <= cu_count(a.get_device()):
+        ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2)
     ws = _empty((ws_bytes,), torch.uint8, a.device) if ws_bytes > 0 else None
     N.call("moc_gemm_ws", code, M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
            bs0, bs1, K2, N.ptr(a2p), a2s0, a2s1, N.ptr(b2p), b2s0, b2s1, out.data_ptr(), ldc,
