@@ -64,7 +64,33 @@ def parse_args():
     p.add_argument("--decode-groups", type=int, default=40)
     p.add_argument("--decode-iters", type=int, default=50)
     p.add_argument("--skip-extra", action="store_true", help="headline + rooflines only")
+    p.add_argument("--pmc-target", choices=["gemm", "copy"], default=None,
+                   help="only launch one workload 5 times (for rocprofv3 --pmc runs): the G "
+                        "GEMM of the 1b layer, or a plain 256 MiB copy kernel (counter scale)")
     return p.parse_args()
+
+
+def pmc_target(which: str) -> None:
+    """Minimal launches for the counter runs behind roofline.traffic."""
+    import torch
+    from moc_amd import _native as N
+    from moc_amd import kernels as K
+    N.load()
+    if which == "gemm":
+        x, wg, _, _, _ = seeded_inputs(BATCH1B * SEQ1B, D1B, I1B)
+        x, wg = x.cuda(), wg.cuda()
+        g = K.padded_empty(x.shape[0], I1B, torch.bfloat16, x.device)
+        for _ in range(5):
+            K.linear(x, wg, out=g)
+    else:
+        rows, cols = 16384, 8192  # 256 MiB of bf16 read and written
+        src = torch.ones(rows, cols, device="cuda", dtype=torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            N.call("moc_copy_pad_2d", N.MOC_BF16, src.data_ptr(), rows, cols, cols, dst.data_ptr(),
+                   cols, cols, N.stream_of(src))
+    torch.cuda.synchronize()
+    log(f"pmc target {which}: 5 launches done")
 
 
 # ----------------------------------------------------------------- helpers
@@ -127,6 +153,13 @@ def time_train_layer(m, x, go, steps, warmup):
     return wall * 1e3 / steps, summarize(fwd), summarize(bwd)
 
 
+# L2-miss (MALL/HBM side) bytes of one G launch at the 1b shape, from the
+# FETCH_SIZE / WRITE_SIZE counter runs in profiles/gemm_G_traffic.md, each
+# scaled by what the counter reads for a copy kernel of known size
+# (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).
+GEMM_G_TRAFFIC_BYTES = 593.6e6 + 179.3e6
+
+
 def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
     """HIP-event time of the eight GEMM launches of one MoC FFN fwd+bwd step at
     the layer's real shapes (the kernels and operand layouts the layer uses)."""
@@ -182,7 +215,10 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
     achieved = tot_flop / (tot_ms * 1e-3) / 1e12
     return {
         "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None,
+        "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+        "traffic": GEMM_G_TRAFFIC_BYTES if (t, d, inter) == (BATCH1B * SEQ1B, D1B, I1B) else None,
+        "traffic_note": "bytes per G launch (L2 misses to MALL/HBM; counter runs scaled by a copy "
+                        "kernel, profiles/gemm_G_traffic.md)",
         "kernel": "gemm_pp_kernel (v_mfma_f32_32x32x16_bf16), 8 launches/step",
         "algorithmic_flop_per_step": tot_flop, "gemm_ms_per_step": round(tot_ms, 4),
         "per_launch": per,
@@ -361,6 +397,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm device visible"}))
         sys.exit(1)
+    if args.pmc_target:
+        pmc_target(args.pmc_target)
+        return
     from moc_amd import _native
     _native.load()  # the HIP library must be there: no fallback
 
