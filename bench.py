@@ -64,9 +64,10 @@ def parse_args():
     p.add_argument("--decode-groups", type=int, default=40)
     p.add_argument("--decode-iters", type=int, default=50)
     p.add_argument("--skip-extra", action="store_true", help="headline + rooflines only")
-    p.add_argument("--pmc-target", choices=["gemm", "copy"], default=None,
-                   help="only launch one workload 5 times (for rocprofv3 --pmc runs): the G "
-                        "GEMM of the 1b layer, or a plain 256 MiB copy kernel (counter scale)")
+    p.add_argument("--pmc-target", choices=["gemm", "copy", "decode"], default=None,
+                   help="only launch one workload a few times (for rocprofv3 --pmc runs): the G "
+                        "GEMM of the 1b layer, a plain 256 MiB copy kernel (counter scale), or "
+                        "the B=1 decode layer over 8 weight sets")
     return p.parse_args()
 
 
@@ -82,6 +83,22 @@ def pmc_target(which: str) -> None:
         g = K.padded_empty(x.shape[0], I1B, torch.bfloat16, x.device)
         for _ in range(5):
             K.linear(x, wg, out=g)
+    elif which == "decode":
+        gen = torch.Generator(device="cuda").manual_seed(1234)
+        layers = []
+        for _ in range(8):
+            wg = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            wu = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            wdt = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            layers.append((wg, wu, wdt))
+        x = torch.randn(1, D1B, device="cuda", generator=gen).to(torch.bfloat16)
+        gate = torch.empty(1, I1B, device="cuda", dtype=torch.bfloat16)
+        y = torch.empty(1, D1B, device="cuda", dtype=torch.bfloat16)
+        ws = K.global_after_gate_workspace(1, I1B, K1B, D1B, "cuda")
+        for _ in range(3):
+            for wg, wu, wdt in layers:
+                K.gemv(x, wg, out=gate)
+                K.global_after_gate(x, gate, wu, wdt, K1B, workspace=ws, out=y)
     else:
         rows, cols = 16384, 8192  # 256 MiB of bf16 read and written
         src = torch.ones(rows, cols, device="cuda", dtype=torch.bfloat16)
@@ -158,6 +175,9 @@ def time_train_layer(m, x, go, steps, warmup):
 # scaled by what the counter reads for a copy kernel of known size
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).
 GEMM_G_TRAFFIC_BYTES = 593.6e6 + 179.3e6
+# the same for the B=1 decode layer (gate GEMV + fused select/up/down),
+# profiles/decode_B1_traffic.md
+DECODE_B1_TRAFFIC_BYTES = 22.48e6 + 9.33e6
 
 
 def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
@@ -422,7 +442,7 @@ def main():
     dec = [decode_bench(1, groups=args.decode_groups, iters=args.decode_iters)]
     d1 = dec[0]
     roof_dec = {"bound": "hbm", "achieved": d1["achieved_GBs"], "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": d1["frac_hbm"], "traffic": None,
+                "unit": "GB/s", "frac": d1["frac_hbm"], "traffic": DECODE_B1_TRAFFIC_BYTES,
                 "kernel": "decode layer (gate GEMV + Top-K + selected Up + selected Down), B=1",
                 "us": d1["us_median"], "bytes": d1["bytes"]}
     if not args.skip_extra:
