@@ -33,6 +33,38 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_to_f32(f32_to_bf16(f));
 }
 
+// RNE to bf16 with the gfx950 packed conversion; NaN keeps the canonical
+// 0x7FC0 of f32_to_bf16 (same bits as f32_to_bf16 for every input).
+typedef float cvt_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 cvt_bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  const uint32_t w =
+      __builtin_bit_cast(uint32_t, __builtin_convertvector((cvt_f32x2_t){f, 0.0f}, cvt_bf16x2_t));
+  return f != f ? uint16_t(0x7FC0u) : static_cast<uint16_t>(w & 0xFFFFu);
+}
+__device__ __forceinline__ float bf16_rnd(float f) { return bf16_to_f32(bf16_rne(f)); }
+
+// Backward of one selected entry of the sparse SwiGLU (bf16 chain of
+// moc/training/triton_sparse_aux.py:376-400): g, u the saved gate/up values,
+// gz the gradient of z = SiLU(g) * u; s = SiLU(g) as saved (bf16), or, when
+// have_s is false, recomputed as bf16(g / (1 + exp(-g))) (F.silu's formula,
+// moc/ffn.py:435-436).  One exp serves both SiLU and the sigmoid.
+__device__ __forceinline__ void sparse_bwd_entry(float g, float u, bool have_s, float s_saved,
+                                                 float gz, uint16_t& grad_g, uint16_t& grad_u) {
+  const float den = 1.0f + expf(-g);
+  const float s = have_s ? s_saved : bf16_rnd(g / den);
+  const float gs = bf16_rnd(u * gz);
+  const float gu = bf16_rnd(s * gz);
+  const float sig = bf16_rnd(1.0f / den);
+  const float t1 = bf16_rnd(1.0f - sig);
+  const float t2 = bf16_rnd(g * t1);
+  const float t3 = bf16_rnd(1.0f + t2);
+  const float d = bf16_rnd(sig * t3);
+  grad_g = bf16_rne(gs * d);
+  grad_u = bf16_rne(gu);
+}
+
 // ---------------------------------------------------------------------------
 // Order keys: unsigned integers whose natural order is the IEEE order of the
 // values.  -0.0 and +0.0 map to the same key (they compare equal as numbers)

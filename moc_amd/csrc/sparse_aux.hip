@@ -194,17 +194,9 @@ __device__ __forceinline__ void row_store(uint16_t* dst, const uint16_t* buf, in
     reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(buf)[c];
 }
 
-// Row-form arithmetic.  RNE to bf16 with the gfx950 packed conversion (NaN
-// keeps the canonical 0x7FC0 of f32_to_bf16), and one exp per entry for both
-// sigmoid(g) and SiLU(g) = g / (1 + exp(-g)).
-typedef float rf32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 rbf16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint16_t to_bf16(float f) {
-  const uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector((rf32x2_t){f, 0.0f}, rbf16x2_t));
-  return f != f ? uint16_t(0x7FC0u) : static_cast<uint16_t>(w & 0xFFFFu);
-}
-__device__ __forceinline__ float rnd(float f) { return bf16_to_f32(to_bf16(f)); }
+// Row-form arithmetic: RNE to bf16 with the gfx950 packed conversion.
+__device__ __forceinline__ uint16_t to_bf16(float f) { return bf16_rne(f); }
+__device__ __forceinline__ float rnd(float f) { return bf16_rnd(f); }
 
 // The entries of a row are taken kRowPer per thread at a time; the first
 // group's sparse loads are issued before the dense row is staged, so the two
@@ -340,21 +332,8 @@ __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     for (int q = 0; q < kRowPer; ++q) {
       const int64_t ch = r.ch[q];
       if (ch < 0 || ch >= inter) continue;
-      const float gz = bf16_to_f32(gzrow[ch]);
-      const float g = bf16_to_f32(r.a[q]);
-      const float u = bf16_to_f32(r.b[q]);
-      const float den = 1.0f + expf(-g);
-      const float s = s_s ? bf16_to_f32(r.c[q]) : rnd(g / den);
-      // the reference's bf16 chain (see sparse_backward_aux_kernel)
-      const float gs = rnd(u * gz);
-      const float gu = rnd(s * gz);
-      const float sig = rnd(1.0f / den);
-      const float t1 = rnd(1.0f - sig);
-      const float t2 = rnd(g * t1);
-      const float t3 = rnd(1.0f + t2);
-      const float d = rnd(sig * t3);
-      ggrow[ch] = to_bf16(gs * d);
-      gurow[ch] = to_bf16(gu);
+      sparse_bwd_entry(bf16_to_f32(r.a[q]), bf16_to_f32(r.b[q]), s_s != nullptr,
+                       bf16_to_f32(r.c[q]), bf16_to_f32(gzrow[ch]), ggrow[ch], gurow[ch]);
     }
   }
   __syncthreads();
