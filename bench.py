@@ -64,11 +64,60 @@ def parse_args():
     p.add_argument("--decode-groups", type=int, default=40)
     p.add_argument("--decode-iters", type=int, default=50)
     p.add_argument("--skip-extra", action="store_true", help="headline + rooflines only")
+    p.add_argument("--cfg5", action="store_true",
+                   help="only the 350m-model training step (config 5): tokens/s and peak "
+                        "memory, moc_gcp vs dense, one JSON line")
+    p.add_argument("--cfg5-steps", type=int, default=10)
     p.add_argument("--pmc-target", choices=["gemm", "copy", "decode"], default=None,
                    help="only launch one workload a few times (for rocprofv3 --pmc runs): the G "
                         "GEMM of the 1b layer, a plain 256 MiB copy kernel (counter scale), or "
                         "the B=1 decode layer over 8 weight sets")
     return p.parse_args()
+
+
+def cfg5_bench(steps: int) -> dict:
+    """Config 5: a 350m LLaMA training step (24 layers, d=1024, I=2736,
+    K=512), bf16 parameters, AdamW (0.9/0.999, wd 0, fused=False, lr 1e-3),
+    tokens [16, 256] uniform over the 32100-token vocabulary with labels =
+    tokens; 1 warmup step, then `steps` timed steps; peak memory after the
+    warmup (the method of benchmark_training_throughput.py:51-114 and
+    benchmark_memory.py:51-107).  Attention, norms and embeddings are stock
+    PyTorch; the FFN is this build's."""
+    import torch
+    from moc_amd import PRESETS, build_model
+    from dataclasses import replace
+    out = {}
+    for ffn_type in ("moc_gcp", "dense"):
+        torch.manual_seed(1234)
+        cfg = replace(PRESETS["350m"], vocab_size=32100, max_seq_len=256)
+        model = build_model(cfg, ffn_type=ffn_type).to("cuda", torch.bfloat16)
+        opt = torch.optim.AdamW(model.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0,
+                                fused=False)
+        gen = torch.Generator().manual_seed(1234)
+        tok = torch.randint(0, 32100, (16, 256), generator=gen).cuda()
+
+        def step():
+            _, loss = model(tok, labels=tok)
+            loss.backward()
+            opt.step()
+            opt.zero_grad(set_to_none=True)
+            return loss
+
+        loss0 = step()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        out[ffn_type] = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),
+                         "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 3),
+                         "loss_first": round(float(loss0), 4), "loss_last": round(float(loss), 4)}
+        log(f"cfg5 {ffn_type}: {out[ffn_type]}")
+        del model, opt
+        torch.cuda.empty_cache()
+    return out
 
 
 def pmc_target(which: str) -> None:
@@ -419,6 +468,10 @@ def main():
         sys.exit(1)
     if args.pmc_target:
         pmc_target(args.pmc_target)
+        return
+    if args.cfg5:
+        print(json.dumps({"config": "350m LLaMA training step (config 5), 16x256 tokens, bf16",
+                          "steps": args.cfg5_steps, "result": cfg5_bench(args.cfg5_steps)}))
         return
     from moc_amd import _native
     _native.load()  # the HIP library must be there: no fallback
