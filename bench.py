@@ -103,12 +103,12 @@ def cfg5_bench(steps: int) -> dict:
             opt.zero_grad(set_to_none=True)
             return loss
 
-        loss0 = step()
+        loss0 = step().detach()
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
         t0 = time.perf_counter()
         for _ in range(steps):
-            loss = step()
+            loss = step().detach()
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         out[ffn_type] = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),

@@ -97,12 +97,27 @@ def _side_stream(device) -> torch.cuda.Stream:
 
 def _on_side(side, tensors, fn):
     """Run fn() on `side` after the current stream's queued work; tensors
-    made on the current stream and used there are kept alive for it."""
+    made on the current stream and used there are kept alive for it.  With
+    side None, fn() runs on the current stream."""
+    if side is None:
+        fn()
+        return
     side.wait_stream(torch.cuda.current_stream(side.device))
     with torch.cuda.stream(side):
         fn()
     for t in tensors:
         t.record_stream(side)
+
+
+def _side_for(device, rows: int, inter: int):
+    """The side stream when the [rows, inter] GEMMs take several rounds of
+    256x256 tiles (their half-empty last rounds are worth filling), else None:
+    for one round or less the stream handoffs cost more host time (~40 us
+    per layer) than the overlap gains."""
+    if K.gemm_tiles(rows, inter) > K.cu_count(device.index if device.index is not None
+                                               else torch.cuda.current_device()):
+        return _side_stream(device)
+    return None
 
 
 def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool):
@@ -114,11 +129,12 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     inter = gate_w.shape[0]
     x2 = K.aligned_rows(x.reshape(-1, d))
     rows = x2.shape[0]
-    # U = x Wu^T runs on the side stream, launched before G so that the two
-    # GEMMs share the CUs (each alone leaves its last round half empty) and U
-    # also overlaps the selection over G; the 16-byte-row copy of W_down
-    # (when its rows need one), which the backward reuses, follows U there
-    side = _side_stream(x.device)
+    # U = x Wu^T runs on the side stream (for multi-round GEMMs), launched
+    # before G so that the two GEMMs share the CUs (each alone leaves its last
+    # round half empty) and U also overlaps the selection over G; the
+    # 16-byte-row copy of W_down (when its rows need one), which the backward
+    # reuses, follows U there
+    side = _side_for(x.device, rows, inter)
     g = K.padded_empty(rows, inter, x.dtype, x.device)
     u = K.padded_empty(rows, inter, x.dtype, x.device)
     wd = (K.padded_empty(down_w.shape[0], down_w.shape[1], down_w.dtype, x.device)
@@ -139,7 +155,8 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     else:
         raise ValueError(selection)
     del g
-    torch.cuda.current_stream(x.device).wait_stream(side)
+    if side is not None:
+        torch.cuda.current_stream(x.device).wait_stream(side)
     u_s, s_s, z_s, z_full = K.sparse_forward_aux(vals, idx, u, inter, want_s=save_s, want_z=save_s)
     del u
     out = K.gemm(z_full, wd.t())
@@ -158,17 +175,17 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     dWd = go^T Z, gZ = go Wd, (gG, gU) = sparse_backward_aux, dWg = gG^T x,
     dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products).
 
-    dWd (176 tiles of 256x256 at the 1b shape: two thirds of the CUs) runs on
-    the side stream beside gZ and the aux kernel.  dWg and dWu overlap dX
-    only when together they fill at most the CUs once; larger ones run in
-    order with dX (overlapping them measured slower at the 1b shape: the
-    concurrent GEMMs split each XCD's L2 between their tile groups)."""
+    When gZ takes several rounds of tiles, dWd (176 tiles of 256x256 at the
+    1b shape: two thirds of the CUs) runs on the side stream beside gZ and
+    the aux kernel.  dWg, dWu and dX run in order (overlapping them measured
+    slower at the 1b shape: the concurrent GEMMs split each XCD's L2 between
+    their tile groups; small ones split K instead)."""
     d = x.shape[-1]
     inter = gate_w.shape[0]
     dev = x.device
     main = torch.cuda.current_stream(dev)
-    side = _side_stream(dev)
     x2 = K.aligned_rows(x.reshape(-1, d))
+    side = _side_for(dev, x2.shape[0], inter)
     go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
     if gcp and x.dtype == torch.bfloat16 and K.row_pitch(inter, torch.bfloat16) <= 8192:
         s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter)
@@ -185,20 +202,11 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     K.gemm(go, wd, out=gz)
     grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
     del gz
-    grad_gate_w = torch.empty(inter, d, dtype=gate_w.dtype, device=dev)
-    grad_up_w = torch.empty(inter, d, dtype=up_w.dtype, device=dev)
-
-    def weight_grads():
-        K.gemm(grad_g.t(), x2, out=grad_gate_w, out_dtype=grad_gate_w.dtype)
-        K.gemm(grad_u.t(), x2, out=grad_up_w, out_dtype=grad_up_w.dtype)
-
-    if 2 * K.gemm_tiles(inter, d) <= K.cu_count(x.get_device()):
-        # small weight gradients leave most CUs idle: overlap them with dX
-        _on_side(side, (grad_g, grad_u, x2, grad_gate_w, grad_up_w), weight_grads)
-    else:
-        weight_grads()
+    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=gate_w.dtype)
+    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=up_w.dtype)
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
-    main.wait_stream(side)
+    if side is not None:
+        main.wait_stream(side)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
 
 
