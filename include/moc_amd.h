@@ -142,13 +142,21 @@ int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t 
              int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn, void* C,
              int64_t ldc, int c_dtype, void* stream);
 
-/* moc_gemm with a caller-provided device workspace (16-byte aligned).  A bf16
- * product whose 256x256 output tiles fill at most half the CUs (the weight
- * gradients of small models) then splits its K range over several
- * workgroups per tile, writes f32 partial tiles into the workspace and sums
- * them in a fixed order (results do not depend on timing).  With a null or
- * too small workspace it is moc_gemm.  Same reference call sites as
- * moc_gemm. */
+/* moc_gemm with a caller-provided device workspace (256-byte aligned).  A
+ * bf16 product with fewer 256x256 output tiles than CUs then splits its K
+ * range over several workgroups per tile:
+ *  - at most half the CUs (weight gradients of small models): each tile as
+ *    `ks` workgroups writing f32 partial tiles, summed in a fixed order by a
+ *    second kernel;
+ *  - more than half (weight gradients at the 1b shape, 176 tiles on 256
+ *    CUs): each tile as two workgroups over an uneven K split; the one that
+ *    finishes second adds the other's f32 partial and writes C (a + b = b + a:
+ *    the result does not depend on timing).
+ * The first 4 KB of the workspace hold the arrival counters of the second
+ * form: they must be zero when a call starts and every call leaves them
+ * zero, so a workspace zeroed once can be reused; calls that share a
+ * workspace must not run concurrently.  With a null or too small workspace
+ * it is moc_gemm.  Same reference call sites as moc_gemm. */
 int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
                 int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2, const void* A2,
                 int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn,
@@ -156,7 +164,8 @@ int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64
                 void* stream);
 
 /* Workspace bytes moc_gemm_ws uses for this shape on the current device (0:
- * the product does not split).  No counterpart in the reference (its GEMMs
+ * the product does not split; otherwise 4 KB of counters plus the f32
+ * partial tiles).  No counterpart in the reference (its GEMMs
  * are library calls). */
 int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2);
 

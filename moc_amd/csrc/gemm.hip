@@ -91,6 +91,15 @@ struct GemmArgs {
   int ksplit;     // workgroups per C tile (split-K; 512-thread kernel only)
   int kper;       // K tiles per split
   int64_t ws_stride;  // f32 elements between the partial C matrices of two splits
+  // Tail fix-up (512-thread kernel, fix_tail > 0): workgroups [0, fix_full)
+  // run whole tiles; each of the fix_tail tiles after them runs as two
+  // workgroups, over K tiles [0, fix_split) and [fix_split, nk), and the
+  // second to finish adds the other's partial (fix_part, [fix_tail][2]
+  // partial tiles) and writes C.  fix_cnt: arrival counters [fix_tail],
+  // zero at launch and left zero.
+  int fix_full, fix_tail, fix_split;
+  char* fix_part;
+  int* fix_cnt;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -612,6 +621,71 @@ struct LoadMap {
   }
 };
 
+// ------------------------------------------------------------ tail fix-up
+// A tile of the last, partial round of a launch (every tile when a launch
+// has fewer tiles than CUs) runs as two workgroups: part 0 over K tiles
+// [0, fix_kper), part 1 over the rest.  The one that finishes first stores
+// its f32 partial tile in accumulator order (16-byte word (b, q, tid) =
+// acc[b / 2][b % 2][4q .. 4q+3] of thread tid: one wave instruction covers
+// 1 KB) with device-coherent stores, waits for them and bumps the tile's
+// arrival counter; the one that finishes second (it finds the counter at 1,
+// or its own increment returns 1) reads that partial back with
+// device-coherent loads, adds it to its registers (a + b = b + a, so the
+// result does not depend on which part came second), writes C and resets
+// the counter.  Nothing waits on another workgroup.
+constexpr int kPartBytes = 8 * 4 * kPpThreads * 16;  // one partial tile (256 KB)
+constexpr int kFixCounterBytes = 4096;                // arrival counters at the workspace start
+constexpr int kCoherent = 16;                         // buffer op cache policy: sc1
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Returns true in the second workgroup of the tile; acc then holds the sum
+// of both parts.  flag: one LDS word.
+__device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4][2], int slot, int part,
+                                           int tid, int* flag) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      g.fix_part + static_cast<int64_t>(slot) * 2 * kPartBytes, (short)0, 2 * kPartBytes, kBufferFlags);
+  int* cnt = g.fix_cnt + slot;
+  if (tid == 0) *flag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*flag == 0) {
+    // first so far: publish the partial, then arrive
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x16_t& a = acc[b >> 1][b & 1];
+        const u32x4_t v = {__float_as_uint(a[4 * q]), __float_as_uint(a[4 * q + 1]),
+                           __float_as_uint(a[4 * q + 2]), __float_as_uint(a[4 * q + 3])};
+        __builtin_amdgcn_raw_buffer_store_b128(
+            v, rsrc, static_cast<uint32_t>(part * kPartBytes + ((b * 4 + q) * kPpThreads + tid) * 16), 0,
+            kCoherent);
+      }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is stored
+    __syncthreads();
+    if (tid == 0) *flag = atomicAdd(cnt, 1);
+    __syncthreads();
+    if (*flag == 0) return false;
+  }
+  // second: the other part's partial plus ours
+  const uint32_t other = static_cast<uint32_t>((1 - part) * kPartBytes);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    f32x16_t& a = acc[b >> 1][b & 1];
+    u32x4_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      w[q] = __builtin_amdgcn_raw_buffer_load_b128(
+          rsrc, other + static_cast<uint32_t>(((b * 4 + q) * kPpThreads + tid) * 16), 0, kCoherent);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) a[4 * q + c] += __uint_as_float(w[q][c]);
+  }
+  if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+  return true;
+}
+
 // SPLIT: split-K launch (f32 partial tiles into the workspace slices).
 template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT>
 __global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -626,7 +700,16 @@ void gemm_pp_kernel(GemmArgs g) {
   // split-K: workgroup bid runs K tiles [split * kper, +kper) of its tile
   // and writes an f32 partial tile into slice `split` of the workspace
   const int split = SPLIT ? static_cast<int>(blockIdx.x % g.ksplit) : 0;
-  const int tbid = SPLIT ? static_cast<int>(blockIdx.x / g.ksplit) : static_cast<int>(blockIdx.x);
+  int tbid = SPLIT ? static_cast<int>(blockIdx.x / g.ksplit) : static_cast<int>(blockIdx.x);
+  // tail fix-up: workgroup fix_full + part * fix_tail + slot runs part
+  // `part` of the K range of tile fix_full + slot
+  int part = -1, slot = 0;
+  if (!SPLIT && g.fix_tail > 0 && tbid >= g.fix_full) {
+    const int j = tbid - g.fix_full;
+    part = j / g.fix_tail;
+    slot = j - part * g.fix_tail;
+    tbid = g.fix_full + slot;
+  }
   int tm, tn;
   tile_coords(tbid, g.tiles_m, g.tiles_n, tm, tn);
   const int row0 = tm * kBM;
@@ -637,8 +720,9 @@ void gemm_pp_kernel(GemmArgs g) {
 
   const int nk0 = g.nk[0];
   const int nk_all = nk0 + (DUAL ? g.nk[1] : 0);
-  const int kt0 = SPLIT ? split * g.kper : 0;           // first K tile of this workgroup
-  const int nk = SPLIT ? min(nk_all, kt0 + g.kper) : nk_all;  // one past its last
+  // first K tile of this workgroup and one past its last
+  const int kt0 = SPLIT ? split * g.kper : (part == 1 ? g.fix_split : 0);
+  const int nk = SPLIT ? min(nk_all, kt0 + g.kper) : (part == 0 ? g.fix_split : nk_all);
 
   FragMap<A_KC> fa_map;
   FragMap<B_KC> fb_map;
@@ -800,6 +884,8 @@ void gemm_pp_kernel(GemmArgs g) {
     gs.C = static_cast<float*>(g.C) + split * g.ws_stride;
     store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
   } else {
+    if (part >= 0 && !fix_arrive(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kSinkOffset)))
+      return;
     store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
   }
 }
@@ -905,7 +991,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgsF32 g) {
 
 template <bool A_KC, bool B_KC>
 void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(a.tiles_m * a.tiles_n * a.ksplit)), block(kThreads);
+  const int64_t units = a.fix_tail > 0 ? a.fix_full + 2 * static_cast<int64_t>(a.fix_tail)
+                                       : static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.ksplit;
+  const dim3 grid(static_cast<unsigned>(units)), block(kThreads);
   const bool dual = a.nk[1] > 0;
   if (a.pp) {
     const dim3 pblock(kPpThreads);
@@ -989,8 +1077,48 @@ SplitPlan plan_split(int64_t M, int64_t N, int nk) {
   p.ksplit = ks;
   p.kper = kper;
   p.ldw = (N + 3) & ~3LL;
-  p.bytes = static_cast<int64_t>(ks) * M * p.ldw * 4;
+  p.bytes = kFixCounterBytes + static_cast<int64_t>(ks) * M * p.ldw * 4;  // partials after the counters
   return p;
+}
+
+// Fix-up plan of a bf16 GEMM whose n tiles fill more than half the CUs but
+// not all of them (the weight gradients at the 1b shape: 176 tiles on 256
+// CUs, K = 16384).  Each tile runs as two workgroups: part 0 over K tiles
+// [0, s) on n CUs, part 1 over [s, nk) on the h = CUs - n others, which take
+// w = ceil(n / h) of them in turn.  s balances the two sides,
+// s + kFix ~ w (nk - s + kStore), in K-tile times (kUnit of prologue and
+// epilogue per workgroup, kFix for reading and adding the other partial,
+// kStore for storing one); the plan is kept if it beats whole tiles.
+// Launches with more tiles than CUs run whole tiles only: splitting the
+// tiles of their last, partial round measured no faster (the half-empty
+// last round already runs its K tiles faster, with less contention for L2
+// and HBM, and the partial stores of a whole round at once are HBM-bound).
+struct FixPlan {
+  int full = 0, tail = 0, split = 0;
+  int64_t bytes = 0;
+};
+
+FixPlan plan_fix(int64_t M, int64_t N, int nk) {
+  constexpr int64_t kUnit = 5, kFix = 4, kStore = 3;
+  FixPlan f;
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const int64_t cus = cu_count();
+  if (tiles <= 0 || 2 * tiles <= cus || tiles >= cus || nk < 8 || tiles * 4 > kFixCounterBytes) return f;
+  const int64_t w = (tiles + (cus - tiles) - 1) / (cus - tiles);
+  int64_t best = nk + kUnit, best_s = 0;
+  for (int64_t r = 4; 2 * r <= nk; ++r) {
+    const int64_t s = nk - r;
+    const int64_t cost = std::max(s + kUnit + kFix, w * (r + kUnit + kStore));
+    if (cost < best) {
+      best = cost;
+      best_s = s;
+    }
+  }
+  if (best_s == 0) return f;
+  f.tail = static_cast<int>(tiles);
+  f.split = static_cast<int>(best_s);
+  f.bytes = kFixCounterBytes + tiles * 2 * kPartBytes;
+  return f;
 }
 
 }  // namespace
@@ -1001,7 +1129,7 @@ using namespace moc;
 extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2) {
   if (dtype != MOC_BF16 || M <= 0 || N <= 0 || K < 0 || K2 < 0) return 0;
   const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
-  return plan_split(M, N, nk).bytes;
+  return std::max(plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes);
 }
 
 extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
@@ -1105,9 +1233,19 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     run.ksplit = sp.ksplit;
     run.kper = sp.kper;
     run.ws_stride = M * sp.ldw;
-    run.C = workspace;
+    run.C = static_cast<char*>(workspace) + kFixCounterBytes;
     run.ldc = sp.ldw;
     run.vec_store = 1;
+  }
+  const FixPlan fp = split ? FixPlan() : plan_fix(M, N, a.nk[0] + a.nk[1]);
+  const bool fix = a.pp && fp.tail > 0 && workspace != nullptr && workspace_bytes >= fp.bytes &&
+                   reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
+  if (fix) {
+    run.fix_full = fp.full;
+    run.fix_tail = fp.tail;
+    run.fix_split = fp.split;
+    run.fix_cnt = static_cast<int*>(workspace);
+    run.fix_part = static_cast<char*>(workspace) + kFixCounterBytes;
   }
   const bool of_run = split ? true : of;
   if (la && lb) launch_bf16<true, true>(run, of_run, st);
@@ -1120,12 +1258,13 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     if (rc != MOC_OK) return rc;
     const int64_t quads = M * ((N + 3) / 4);
     const dim3 grid(static_cast<unsigned>((quads + 255) / 256));
+    const float* parts = static_cast<const float*>(run.C);
     if (of)
-      splitk_reduce_kernel<true><<<grid, 256, 0, st>>>(static_cast<const float*>(workspace), run.ws_stride,
-                                                       sp.ksplit, (int)M, (int)N, sp.ldw, C, ldc, a.vec_store);
+      splitk_reduce_kernel<true><<<grid, 256, 0, st>>>(parts, run.ws_stride, sp.ksplit, (int)M, (int)N, sp.ldw,
+                                                       C, ldc, a.vec_store);
     else
-      splitk_reduce_kernel<false><<<grid, 256, 0, st>>>(static_cast<const float*>(workspace), run.ws_stride,
-                                                        sp.ksplit, (int)M, (int)N, sp.ldw, C, ldc, a.vec_store);
+      splitk_reduce_kernel<false><<<grid, 256, 0, st>>>(parts, run.ws_stride, sp.ksplit, (int)M, (int)N, sp.ldw,
+                                                        C, ldc, a.vec_store);
     return check_launch("splitk_reduce_kernel");
   }
 }

@@ -261,6 +261,24 @@ def _operand(t: torch.Tensor, bf16: bool) -> tuple[torch.Tensor, int, int]:
     return tt, (tt.stride(0) if r > 1 else round_up(max(c, 1), 8)), 1
 
 
+_GEMM_WS: dict = {}
+
+
+def _gemm_workspace(device, nbytes: int) -> torch.Tensor:
+    """The GEMM workspace of the current stream on `device`, grown on demand.
+    Its first 4 KB hold arrival counters that must be zero when a GEMM starts
+    and that every GEMM leaves zero, so the buffer is created zeroed and then
+    reused without clearing; one buffer per stream keeps GEMMs that run
+    concurrently on different streams apart."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _GEMM_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        _GEMM_WS.pop(key, None)
+        ws = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
+        _GEMM_WS[key] = ws
+    return ws
+
+
 def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
          b2: torch.Tensor | None = None, out: torch.Tensor | None = None,
          out_dtype: torch.dtype | None = None) -> torch.Tensor:
@@ -293,11 +311,12 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
         b2p, b2s0, b2s1 = _operand(b2, bf16)
     ldc = out.stride(0) if M > 1 else max(Nn, 1)
     code = N.dtype_code(a.dtype)
-    # products with few output tiles split K over a workspace of f32 partials
+    # products with fewer tiles than CUs split K over a workspace of f32
+    # partial tiles
     ws_bytes = 0
-    if bf16 and 2 * gemm_tiles(M, Nn) <= cu_count(a.get_device()):
+    if bf16 and gemm_tiles(M, Nn) < cu_count(a.get_device()):
         ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2)
-    ws = _empty((ws_bytes,), torch.uint8, a.device) if ws_bytes > 0 else None
+    ws = _gemm_workspace(a.device, ws_bytes) if ws_bytes > 0 else None
     N.call("moc_gemm_ws", code, M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
            bs0, bs1, K2, N.ptr(a2p), a2s0, a2s1, N.ptr(b2p), b2s0, b2s1, out.data_ptr(), ldc,
            N.dtype_code(out_dtype), N.ptr(ws), ws_bytes, N.stream_of(a))

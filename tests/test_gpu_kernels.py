@@ -155,6 +155,82 @@ def test_gemm_split_k_dual():
     close(out, ref, rtol=1e-4, atol=1e-3)
 
 
+def _unsplit(ad, bd, M, Nn, Kk, a2=None, b2=None, K2=0):
+    """The GEMM without a workspace (moc_gemm: whole tiles only), f32 out."""
+    flat = torch.empty(M, Nn, device=DEV, dtype=torch.float32)
+    a_, as0, as1 = K()._operand(ad, True)
+    b_, bs0, bs1 = K()._operand(bd, True)
+    p2 = [None, 0, 0, None, 0, 0]
+    if a2 is not None:
+        a2_, a2s0, a2s1 = K()._operand(a2, True)
+        b2_, b2s0, b2s1 = K()._operand(b2, True)
+        p2 = [a2_.data_ptr(), a2s0, a2s1, b2_.data_ptr(), b2s0, b2s1]
+    N().call("moc_gemm", N().MOC_BF16, M, Nn, Kk, a_.data_ptr(), as0, as1, b_.data_ptr(), bs0, bs1,
+             K2, *p2, flat.data_ptr(), Nn, N().MOC_F32, N().stream_of(ad))
+    return flat
+
+
+@pytest.mark.parametrize("layout,mnk", [
+    ("mnmn", (5461, 2048, 16384)),   # 1b dW_gate / dW_up: 176 tiles, each in two K ranges
+    ("mnmn", (2048, 5461, 16384)),   # 1b dW_down
+    ("kckc", (5461, 2000, 16001)),   # ragged M, N and K (K % 64 != 0)
+    ("kcmn", (1000, 3000, 9000)),    # 48 tiles: split-K plan, not the fix-up
+])
+def test_gemm_tail_fixup(layout, mnk):
+    """Products with more tiles than half the CUs but fewer than all of them
+    run each tile as two K ranges on two workgroups; the one that finishes
+    second adds the other's f32 partial.  Results match the fp32 reference,
+    repeat bit for bit (the arrival counters are left zero for the next
+    call), and agree with the whole-tile kernel to f32 rounding."""
+    M, Nn, Kk = mnk
+    g = torch.Generator(device=DEV).manual_seed(13)
+    a = torch.randn(M, Kk, device=DEV, generator=g).to(torch.bfloat16)
+    b = torch.randn(Kk, Nn, device=DEV, generator=g).to(torch.bfloat16)
+    ad = K().aligned_rows(a) if layout in ("kcmn", "kckc") else K().aligned_rows(a.t().contiguous()).t()
+    bd = K().aligned_rows(b.t().contiguous()).t() if layout == "kckc" else K().aligned_rows(b)
+    assert N().query("moc_gemm_workspace_size", N().MOC_BF16, M, Nn, Kk, 0) > 0
+    first = K().gemm(ad, bd, out_dtype=torch.float32)
+    ref = a.float() @ b.float()
+    close(first, ref, rtol=1e-4, atol=2e-2)
+    assert torch.equal(first, K().gemm(ad, bd, out_dtype=torch.float32))
+    bf16_close(K().gemm(ad, bd), ref, ulps=1, atol=2e-2)
+    close(first, _unsplit(ad, bd, M, Nn, Kk), rtol=1e-5, atol=1e-2)
+
+
+def test_gemm_tail_fixup_dual():
+    """A dual product (dX form) with 160 tiles, each in two K ranges that
+    split the second product."""
+    g = torch.Generator(device=DEV).manual_seed(14)
+    T, I, d = 5000, 1000, 2048
+    gg = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    gu = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    gg, gu = K().aligned_rows(gg), K().aligned_rows(gu)
+    assert N().query("moc_gemm_workspace_size", N().MOC_BF16, T, d, I, I) > 0
+    out = K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32)
+    ref = gg.float() @ wg.float() + gu.float() @ wu.float()
+    close(out, ref, rtol=1e-4, atol=1e-3)
+    assert torch.equal(out, K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32))
+    close(out, _unsplit(gg, wg, T, d, I, gu, wu, I), rtol=1e-5, atol=1e-3)
+
+
+def test_gemm_workspace_shared_by_split_and_fixup():
+    """Split-K and fix-up launches take turns on the stream's one workspace:
+    the split-K partials leave the fix-up's arrival counters untouched."""
+    g = torch.Generator(device=DEV).manual_seed(15)
+    a = K().aligned_rows(torch.randn(5461, 4096, device=DEV, generator=g).to(torch.bfloat16))
+    b = K().aligned_rows(torch.randn(4096, 2048, device=DEV, generator=g).to(torch.bfloat16))
+    c = K().aligned_rows(torch.randn(1000, 4096, device=DEV, generator=g).to(torch.bfloat16))
+    fix0 = K().gemm(a, b, out_dtype=torch.float32)
+    split0 = K().gemm(c, b, out_dtype=torch.float32)
+    for _ in range(2):
+        assert torch.equal(K().gemm(a, b, out_dtype=torch.float32), fix0)
+        assert torch.equal(K().gemm(c, b, out_dtype=torch.float32), split0)
+    close(fix0, a.float() @ b.float(), rtol=1e-4, atol=1e-2)
+    close(split0, c.float() @ b.float(), rtol=1e-4, atol=1e-2)
+
+
 def test_gemm_dual_product_and_f32():
     g = gen(2)
     a, a2 = torch.randn(200, 72, generator=g), torch.randn(200, 40, generator=g)
