@@ -40,6 +40,10 @@ extern "C" {
 #define MOC_I32 1
 #define MOC_I64 2
 
+/* moc_gemm_ws: bytes of arrival counters at the start of its workspace (zero
+ * when a call starts; every call leaves them zero). */
+#define MOC_GEMM_WS_COUNTER_BYTES 4096
+
 /* ------------------------------------------------------------------ misc */
 const char* moc_last_error(void);
 int moc_abi_version(void);

@@ -634,7 +634,7 @@ struct LoadMap {
 // result does not depend on which part came second), writes C and resets
 // the counter.  Nothing waits on another workgroup.
 constexpr int kPartBytes = 8 * 4 * kPpThreads * 16;  // one partial tile (256 KB)
-constexpr int kFixCounterBytes = 4096;                // arrival counters at the workspace start
+constexpr int kFixCounterBytes = MOC_GEMM_WS_COUNTER_BYTES;  // arrival counters at the workspace start
 constexpr int kCoherent = 16;                         // buffer op cache policy: sc1
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -1053,9 +1053,10 @@ int cu_count() {
   return cached[dev];
 }
 
-// Split-K plan of a bf16 GEMM: a product whose 256x256 tiles fill at most
-// half the CUs runs each tile as `ksplit` workgroups over consecutive ranges
-// of at least 4 K tiles.  ldw: row pitch of the f32 partials.
+// Split-K plan of a bf16 GEMM: a product whose 256x256 tiles fill at most a
+// third of the CUs runs each tile as `ksplit` (>= 3) workgroups over
+// consecutive ranges of at least 4 K tiles.  ldw: row pitch of the f32
+// partials.
 struct SplitPlan {
   int ksplit = 1;
   int kper = 0;
@@ -1068,7 +1069,7 @@ SplitPlan plan_split(int64_t M, int64_t N, int nk) {
   p.kper = nk;
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const int cus = cu_count();
-  if (tiles <= 0 || 2 * tiles > cus) return p;
+  if (tiles <= 0 || 3 * tiles > cus) return p;
   int ks = static_cast<int>(std::min<int64_t>(cus / tiles, nk / 4));
   if (ks < 2) return p;
   const int kper = (nk + ks - 1) / ks;
@@ -1081,11 +1082,12 @@ SplitPlan plan_split(int64_t M, int64_t N, int nk) {
   return p;
 }
 
-// Fix-up plan of a bf16 GEMM whose n tiles fill more than half the CUs but
-// not all of them (the weight gradients at the 1b shape: 176 tiles on 256
-// CUs, K = 16384).  Each tile runs as two workgroups: part 0 over K tiles
-// [0, s) on n CUs, part 1 over [s, nk) on the h = CUs - n others, which take
-// w = ceil(n / h) of them in turn.  s balances the two sides,
+// Fix-up plan of a bf16 GEMM whose n tiles fill more than a third of the
+// CUs but not all of them (the weight gradients at the 1b shape: 176 tiles
+// on 256 CUs, K = 16384; the 2:8 down projection: 128 tiles).  Each tile
+// runs as two workgroups: part 0 over K tiles [0, s) on n CUs, part 1 over
+// [s, nk) on the h = CUs - n others, which take w = ceil(n / h) of them in
+// turn (w = 1 up to half the CUs).  s balances the two sides,
 // s + kFix ~ w (nk - s + kStore), in K-tile times (kUnit of prologue and
 // epilogue per workgroup, kFix for reading and adding the other partial,
 // kStore for storing one); the plan is kept if it beats whole tiles.
@@ -1103,7 +1105,7 @@ FixPlan plan_fix(int64_t M, int64_t N, int nk) {
   FixPlan f;
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const int64_t cus = cu_count();
-  if (tiles <= 0 || 2 * tiles <= cus || tiles >= cus || nk < 8 || tiles * 4 > kFixCounterBytes) return f;
+  if (tiles <= 0 || 3 * tiles <= cus || tiles >= cus || nk < 8 || tiles * 4 > kFixCounterBytes) return f;
   const int64_t w = (tiles + (cus - tiles) - 1) / (cus - tiles);
   int64_t best = nk + kUnit, best_s = 0;
   for (int64_t r = 4; 2 * r <= nk; ++r) {

@@ -32,11 +32,12 @@ extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64
 extern "C" int moc_scatter_sparse_to_dense(int dtype, const void* sparse, const void* idx,
                                            int idx_dtype, int64_t rows, int64_t k, int64_t inter,
                                            void* dense, int64_t ld, void* stream);
-extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
-                        int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
-                        const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
-                        int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
-                        void* stream);
+extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+                           int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
+                           const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
+                           int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2);
 
 namespace moc {
 namespace {
@@ -309,7 +310,8 @@ extern "C" int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t 
                                                             int64_t hidden) {
   if (nb <= 0 || k <= 0 || inter <= 0 || hidden <= 0) return 0;
   if (nb <= 64) return moc_selected_down_workspace_size(nb, k, hidden);
-  return align256(nb * inter * 2);
+  // dense z, then the down GEMM's own workspace
+  return align256(nb * inter * 2) + moc_gemm_workspace_size(MOC_BF16, nb, hidden, inter, 0);
 }
 
 extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb,
@@ -329,7 +331,17 @@ extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, i
   int rc = moc_scatter_sparse_to_dense(MOC_BF16, sz, idx, MOC_I64, nb, k, inter, workspace, inter,
                                        stream);
   if (rc != MOC_OK) return rc;
+  // The GEMM's workspace starts with arrival counters that must be zero;
+  // this entry point's workspace carries nothing between calls, so they are
+  // cleared here.
+  char* gws = static_cast<char*>(workspace) + align256(nb * inter * 2);
+  const int64_t gbytes = moc_gemm_workspace_size(MOC_BF16, nb, hidden, inter, 0);
+  if (gbytes > 0) {
+    rc = moc_fill_zero(gws, MOC_GEMM_WS_COUNTER_BYTES, stream);
+    if (rc != MOC_OK) return rc;
+  }
   // y[nb, hidden] = z[nb, inter] (K-contiguous) x W_down^T[inter, hidden] (N-contiguous)
-  return moc_gemm(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, hidden, 1, 0,
-                  nullptr, 0, 0, nullptr, 0, 0, y, hidden, MOC_BF16, stream);
+  return moc_gemm_ws(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, hidden, 1, 0,
+                     nullptr, 0, 0, nullptr, 0, 0, y, hidden, MOC_BF16, gbytes > 0 ? gws : nullptr,
+                     gbytes, stream);
 }
