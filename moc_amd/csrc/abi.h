@@ -20,6 +20,11 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// MoC 2:8 gate/up + top-2-of-8 for nb tokens on the MFMA GEMM kernel
+// (gemm.hip); 1: shape not supported there (nothing launched).
+int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* wg, const void* wu,
+                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st);
+
 }  // namespace moc
 
 #define MOC_REQUIRE(cond, ...)        \

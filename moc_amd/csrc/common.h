@@ -87,6 +87,33 @@ __device__ __forceinline__ uint32_t f32_order_key(uint32_t u) {
 // SiLU and its derivative, in f32.  expf is the accurate device exp.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+// MoC 2:8: top-2 of one group of 8 channels from bf16-rounded g[8], u[8]
+// (values as f32), emitted as (idx, sz) pairs: top-1 is the largest gate
+// value with the lowest index among equal maxima, top-2 the largest of the
+// other seven under the same rule, sz = bf16((g * sigmoid(g)) * u) in f32
+// (moc/inference/triton_fused_ffn_kernels.py:103-114,126-129).
+__device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
+                                                  int64_t* __restrict__ idx_out,
+                                                  uint16_t* __restrict__ sz_out) {
+  uint32_t key[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) key[j] = bf16_order_key(f32_to_bf16(g[j]));
+  int b1 = 0;
+#pragma unroll
+  for (int j = 1; j < 8; ++j)
+    if (key[j] > key[b1]) b1 = j;
+  int b2 = (b1 == 0) ? 1 : 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if (j != b1 && key[j] > key[b2]) b2 = j;
+  const float g1 = g[b1], g2 = g[b2];
+  idx_out[0] = c0 + b1;
+  idx_out[1] = c0 + b2;
+  sz_out[0] = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
+  sz_out[1] = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------

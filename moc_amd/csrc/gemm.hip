@@ -100,6 +100,12 @@ struct GemmArgs {
   int fix_full, fix_tail, fix_split;
   char* fix_part;
   int* fix_cnt;
+  // MoC 2:8 gate/up launch (gemm_pp_kernel<..., GU = true>): B rows [0, 128)
+  // of a tile are W_gate rows (b[0]), rows [128, 256) the same W_up rows
+  // (b[1]); the epilogue writes top-2-of-8 indices and SiLU(g) u values.
+  int64_t* gu_idx;
+  uint16_t* gu_sz;
+  int gu_inter;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -686,8 +692,61 @@ __device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4]
   return true;
 }
 
+// ------------------------------------------------------ MoC 2:8 epilogue
+// The C tile of a gate/up launch holds, for 256 tokens, the gate values of
+// 128 channels (columns 0-127) and their up values (columns 128-255).  They
+// are rounded to bf16 and staged in LDS (G then U, 256 B rows whose 16-byte
+// chunks are XOR-swizzled by row), then each thread selects the top 2 of a
+// (token, group of 8 channels) item and writes its two indices (int64) and
+// two SiLU(g) u values (bf16) in the reference's compacted layout
+// [token][group][top-1, top-2].
+__device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][2],
+                                              int row0, int col0, int wm, int wn, int tid, int lane) {
+  constexpr int kU = 256 * 256;  // byte offset of the U rows
+  __syncthreads();               // every wave is done with the LDS stages
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = wm + 32 * i + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = wn + 32 * j;
+      char* base = lds + (col < 128 ? 0 : kU) + row * 256;
+      const f32x16_t& a = acc[i][j];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int cc = (col & 127) + 8 * q + 4 * (lane >> 5);
+        *reinterpret_cast<uint2*>(base + (((cc >> 3) ^ (row & 15)) << 4) + (cc & 7) * 2) =
+            make_uint2(pack_bf16x2(a[4 * q], a[4 * q + 1]), pack_bf16x2(a[4 * q + 2], a[4 * q + 3]));
+      }
+    }
+  }
+  __syncthreads();
+  const int kout = g.gu_inter / 4;
+#pragma unroll 2
+  for (int item = tid; item < 256 * 16; item += kPpThreads) {
+    const int tr = item >> 4, grp8 = item & 15;
+    const int tok = row0 + tr, cg = col0 + grp8 * 8;
+    if (tok >= g.M || cg >= g.gu_inter) continue;
+    const int off = tr * 256 + ((grp8 ^ (tr & 15)) << 4);
+    const uint4 gv = *reinterpret_cast<const uint4*>(lds + off);
+    const uint4 uv = *reinterpret_cast<const uint4*>(lds + kU + off);
+    const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+    float gf[8], uf[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gf[2 * e] = __uint_as_float(gw[e] << 16);
+      gf[2 * e + 1] = __uint_as_float(gw[e] & 0xFFFF0000u);
+      uf[2 * e] = __uint_as_float(uw[e] << 16);
+      uf[2 * e + 1] = __uint_as_float(uw[e] & 0xFFFF0000u);
+    }
+    const int64_t o = static_cast<int64_t>(tok) * kout + (cg / 8) * 2;
+    select_group_emit(gf, uf, cg, g.gu_idx + o, g.gu_sz + o);
+  }
+}
+
 // SPLIT: split-K launch (f32 partial tiles into the workspace slices).
-template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT>
+// GU: MoC 2:8 gate/up launch (see GemmArgs::gu_idx).
+template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT, bool GU = false>
 __global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
@@ -713,7 +772,7 @@ void gemm_pp_kernel(GemmArgs g) {
   int tm, tn;
   tile_coords(tbid, g.tiles_m, g.tiles_n, tm, tn);
   const int row0 = tm * kBM;
-  const int col0 = tn * kBN;
+  const int col0 = GU ? tn * 128 : tn * kBN;  // GU: channel base of the gate and up halves
   const int wm = (sw >> 1) * 128;
   const int wn = (sw & 1) * 128 + grp * 64;
   const uint32_t lds0 = lds_addr(lds);
@@ -782,6 +841,12 @@ void gemm_pp_kernel(GemmArgs g) {
     ra1 = make_rsrc(g.a[1]);
     rb1 = make_rsrc(g.b[1]);
   }
+  if (GU) {
+    // loads 4-7 fill tile rows 128-255 from the W_up rows col0.. (the
+    // offsets of the loads < 4 of this map, never issued, may wrap)
+    mb1.init(g.b[1], col0 - 128, sw, lane);
+    rb1 = make_rsrc(g.b[1]);
+  }
   // Loads [j0, j1) of A and of B of K tile t into its stage.
   auto load_tile = [&](int t, int j0, int j1) {
     const int st = t % kStages;
@@ -792,12 +857,16 @@ void gemm_pp_kernel(GemmArgs g) {
     const Operand& ob = p1 ? g.b[1] : g.b[0];
     const LoadMap<A_KC>& la = p1 ? ma1 : ma0;
     const LoadMap<B_KC>& lb = p1 ? mb1 : mb0;
-    const uint32_t ba = la.tile_base(oa, k0), bb = lb.tile_base(ob, k0);
+    constexpr int kHalf = kLoads / 2;  // GU: loads [kHalf, kLoads) read W_up
+    const uint32_t ba = la.tile_base(oa, k0);
+    const uint32_t bb = GU && j0 >= kHalf ? 0u : lb.tile_base(ob, k0);
+    const uint32_t bu = GU && j1 > kHalf ? mb1.tile_base(g.b[1], k0) : 0u;
 #pragma unroll
     for (int j = 0; j < kLoads; ++j)
       if (j >= j0 && j < j1) {
         la.issue(p1 ? ra1 : ra0, oa, ba, at, sw, j);
-        lb.issue(p1 ? rb1 : rb0, ob, bb, bt, sw, j);
+        if (GU && j >= kHalf) mb1.issue(rb1, g.b[1], bu, bt, sw, j);
+        else lb.issue(p1 ? rb1 : rb0, ob, bb, bt, sw, j);
       }
   };
   // After loads [j0, j1) of tile t have landed: zero KC elements beyond a K
@@ -853,7 +922,10 @@ void gemm_pp_kernel(GemmArgs g) {
         prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, k0, row0, sink, lane, tn & 7, 8);
       } else if (sw == 1) {
         const Operand& o = p1 ? g.b[1] : g.b[0];
-        prefetch_slice<B_KC>(p1 ? rb1 : rb0, o, k0, col0, sink, lane, tm & 3, 4);
+        if (GU && (tm & 3) >= 2)  // quarters 2-3 of the B tile are W_up rows
+          prefetch_slice<B_KC>(rb1, g.b[1], k0, col0 - 128, sink, lane, tm & 3, 4);
+        else
+          prefetch_slice<B_KC>(p1 ? rb1 : rb0, o, k0, col0, sink, lane, tm & 3, 4);
       }
     };
 #pragma unroll
@@ -879,7 +951,9 @@ void gemm_pp_kernel(GemmArgs g) {
     compute();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  if (SPLIT) {
+  if (GU) {
+    gu28_epilogue(g, lds, acc, row0, col0, wm, wn, tid, lane);
+  } else if (SPLIT) {
     GemmArgs gs = g;
     gs.C = static_cast<float*>(g.C) + split * g.ws_stride;
     store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
@@ -1124,6 +1198,38 @@ FixPlan plan_fix(int64_t M, int64_t N, int nk) {
 }
 
 }  // namespace
+
+// MoC 2:8 gate/up projection + top-2-of-8 on the 512-thread GEMM kernel
+// (256 tokens x 128 channels of gate and of up per workgroup).  Returns 1
+// without launching when an operand is too large for its 32-bit buffer
+// offsets (the caller then uses its own kernel).
+int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* wg, const void* wu,
+                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st) {
+  GemmArgs a{};
+  const bool ok = make_operand(x, hidden, true, nb, hidden, a.a[0]) &&
+                  make_operand(wg, hidden, true, inter, hidden, a.b[0]) &&
+                  make_operand(wu, hidden, true, inter, hidden, a.b[1]);
+  auto no_wrap = [](const Operand& o) {
+    return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
+  };
+  if (!ok || !no_wrap(a.a[0]) || !no_wrap(a.b[0]) || !no_wrap(a.b[1])) return 1;
+  a.a[1] = a.a[0];
+  a.nk[0] = static_cast<int>((hidden + kBK - 1) / kBK);
+  a.nk[1] = 0;
+  a.M = static_cast<int>(nb);
+  a.N = static_cast<int>(2 * inter);
+  a.tiles_m = static_cast<int>((nb + kBM - 1) / kBM);
+  a.tiles_n = static_cast<int>((inter + 127) / 128);
+  a.pp = 1;
+  a.ksplit = 1;
+  a.gu_idx = idx;
+  a.gu_sz = sz;
+  a.gu_inter = static_cast<int>(inter);
+  const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tiles_m) * a.tiles_n));
+  gemm_pp_kernel<true, true, false, false, false, true><<<grid, dim3(kPpThreads), 0, st>>>(a);
+  return check_launch("gemm_pp_kernel (2:8 gate/up)");
+}
+
 }  // namespace moc
 
 using namespace moc;

@@ -46,29 +46,6 @@ using namespace tile;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// Select top-2 of one group from bf16-rounded g[8], u[8] (values as f32) and
-// emit (idx, sz) pairs.
-__device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
-                                                  int64_t* __restrict__ idx_out,
-                                                  uint16_t* __restrict__ sz_out) {
-  uint32_t key[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) key[j] = bf16_order_key(f32_to_bf16(g[j]));
-  int b1 = 0;
-#pragma unroll
-  for (int j = 1; j < 8; ++j)
-    if (key[j] > key[b1]) b1 = j;
-  int b2 = (b1 == 0) ? 1 : 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j != b1 && key[j] > key[b2]) b2 = j;
-  const float g1 = g[b1], g2 = g[b2];
-  idx_out[0] = c0 + b1;
-  idx_out[1] = c0 + b2;
-  sz_out[0] = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
-  sz_out[1] = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
-}
-
 // ---------------------------------------------------------------------------
 // nb <= 16 path.
 // ---------------------------------------------------------------------------
@@ -297,6 +274,11 @@ extern "C" int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t 
         (const uint16_t*)x, (int)nb, (int)hidden, (const uint16_t*)w_gate, (const uint16_t*)w_up,
         (int)inter, (int64_t*)idx, (uint16_t*)sz);
     return check_launch("grouped_decode_kernel");
+  }
+  {
+    const int rc = launch_gate_up_2of8(x, nb, hidden, w_gate, w_up, inter, static_cast<int64_t*>(idx),
+                                       static_cast<uint16_t*>(sz), st);
+    if (rc != 1) return rc;
   }
   MOC_REQUIRE((nb + kBM - 1) / kBM <= 65535, "moc_grouped_top2_up_silu_bf16: too many tokens");
   const dim3 grid(static_cast<unsigned>((inter + 63) / 64), static_cast<unsigned>((nb + kBM - 1) / kBM));

@@ -400,8 +400,7 @@ def test_grouped_2of8_integer_inputs_bitexact():
     """Integer-valued bf16 inputs make G and U exact, so the fused kernel's
     selection can be compared bit-exactly with the oracle."""
     rng = np.random.default_rng(9)
-    for nb in (3, 40):
-        d, inter = 64, 96
+    for nb, d, inter in ((3, 64, 96), (40, 64, 96), (600, 256, 400)):
         x = torch.tensor(rng.integers(-3, 4, (nb, d)), dtype=torch.bfloat16)
         wg = torch.tensor(rng.integers(-2, 3, (inter, d)), dtype=torch.bfloat16)
         wu = torch.tensor(rng.integers(-2, 3, (inter, d)), dtype=torch.bfloat16)
