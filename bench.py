@@ -68,6 +68,9 @@ def parse_args():
                    help="only the 350m-model training step (config 5): tokens/s and peak "
                         "memory, moc_gcp vs dense, one JSON line")
     p.add_argument("--cfg5-steps", type=int, default=10)
+    p.add_argument("--roofline-only", action="store_true",
+                   help="only the eight GEMM launches of the roofline (for rocprofv3 kernel "
+                        "traces whose per-kernel averages match roofline.per_launch)")
     p.add_argument("--pmc-target", choices=["gemm", "copy", "decode"], default=None,
                    help="only launch one workload a few times (for rocprofv3 --pmc runs): the G "
                         "GEMM of the 1b layer, a plain 256 MiB copy kernel (counter scale), or "
@@ -468,6 +471,15 @@ def main():
         sys.exit(1)
     if args.pmc_target:
         pmc_target(args.pmc_target)
+        return
+    if args.roofline_only:
+        from moc_amd import _native
+        _native.load()
+        t = BATCH1B * SEQ1B
+        x, wg, wu, wd, go = seeded_inputs(t, D1B, I1B)
+        xd = x.reshape(BATCH1B, SEQ1B, D1B).cuda()
+        god = go.reshape(BATCH1B, SEQ1B, D1B).cuda()
+        print(json.dumps({"roofline": gemm_roofline(t, D1B, I1B, K1B, (wg, wu, wd), xd, god)}), flush=True)
         return
     if args.cfg5:
         print(json.dumps({"config": "350m LLaMA training step (config 5), 16x256 tokens, bf16",
