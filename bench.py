@@ -68,6 +68,9 @@ def parse_args():
                    help="only the 350m-model training step (config 5): tokens/s and peak "
                         "memory, moc_gcp vs dense, one JSON line")
     p.add_argument("--cfg5-steps", type=int, default=10)
+    p.add_argument("--decode-e2e", action="store_true",
+                   help="only end-to-end greedy decode of a 24-layer 1b-shape decoder (dense, "
+                        "global MoC, MoC 2:8; eager and whole-step graph): ms/token, one JSON line")
     p.add_argument("--roofline-only", action="store_true",
                    help="only the eight GEMM launches of the roofline (for rocprofv3 kernel "
                         "traces whose per-kernel averages match roofline.per_launch)")
@@ -471,6 +474,25 @@ def main():
         sys.exit(1)
     if args.pmc_target:
         pmc_target(args.pmc_target)
+        return
+    if args.decode_e2e:
+        from moc_amd import _native
+        from moc_amd.inference.decode_model import measure_decode
+        _native.load()
+        rows = []
+        for row, scope, fuse in (("dense", "whole_graph", False), ("global_moc", "whole_graph", True),
+                                 ("global_moc", "whole_graph", False), ("moc_2_8", "whole_graph", False),
+                                 ("dense", "eager", False), ("global_moc", "eager", True),
+                                 ("moc_2_8", "eager", False)):
+            log(f"decode e2e {row} {scope} fuse={fuse}")
+            rows.append(measure_decode(row, scope=scope, fuse=fuse))
+            torch.cuda.empty_cache()
+        print(json.dumps({"workload": "greedy decode, 24 layers, d=2048, I=5464, 16 heads, prompt "
+                                      "128 + 128 generated tokens, batch 1, bf16, random weights "
+                                      "and prompt (seed 1234)",
+                          "reference_a800_ms_per_token": {"dense": 4.310, "global_moc": 4.003,
+                                                          "moc_2_8": 3.586},
+                          "rows": rows}), flush=True)
         return
     if args.roofline_only:
         from moc_amd import _native

@@ -182,6 +182,15 @@ int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int6
 int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void* W, int64_t ldw,
                   int64_t rows, int64_t hidden, void* y, int64_t ldy, void* stream);
 
+/* moc_gemv_bf16 of the RMSNorm'd tokens, for nb <= 4 and hidden <= 4096:
+ * xn[b] = bf16(bf16(x[b] * r_b) * norm_w) with r_b = 1 / sqrt(mean(x[b]^2) +
+ * eps) in f32 (the FFN's pre-norm, benchmark_decode.py:101-109,303:
+ * ffn_norm fused into the gate projection), y[b] = bf16(W . xn[b]); xn is
+ * also written out (the up projection's input).  bf16 only. */
+int moc_gemv_rmsnorm_bf16(const void* x, int64_t ldx, int64_t nb, const void* norm_w, float eps,
+                          void* xn, int64_t ldxn, const void* W, int64_t ldw, int64_t rows,
+                          int64_t hidden, void* y, int64_t ldy, void* stream);
+
 /* z[b,k] = bf16(bf16(SiLU(vals[b,k])) * bf16(x[b] . W_up[idx[b,k]]))
  * (moc_native::optimized_global_selected_up_silu_bf16,
  * optimized_global_moc_ext.cu:127-162,400-427; rounding points of
@@ -216,6 +225,15 @@ int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t 
 int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
                                int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
                                void* y, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* moc_global_after_gate_bf16 with the layer's residual added in its last
+ * step: y = bf16(residual + bf16(FFN)), the decoder's x + ffn(norm(x))
+ * (benchmark_decode.py:303) without a separate add.  Same workspace rules. */
+int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
+                                        int64_t inter, int64_t hidden, const void* w_up,
+                                        const void* w_down_t, int64_t k, const void* residual,
+                                        void* y, void* workspace, int64_t workspace_bytes,
+                                        void* stream);
 
 /* ------------------------------------------------------------------- 2:8 */
 /* Fused gate+up projection with top-2-of-8 selection for nb tokens:

@@ -236,11 +236,30 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
 // products and a wave reduction.  With ~one row per wave every byte of W is
 // in flight within one memory latency.
 // ---------------------------------------------------------------------------
-template <int NB, int CHN>
+// NORM: the tokens go through RMSNorm first (the FFN's pre-norm,
+// benchmark_decode.py:101-109,303): xn = bf16(bf16(x * r) * w) with
+// r = 1 / sqrt(mean(x^2) + eps) in f32; every wave normalises its own copy
+// of x, and wave 0 of workgroup 0 also writes xn for the kernels after it.
+__device__ __forceinline__ uint4 rmsnorm8(uint4 xv, uint4 wv, float r) {
+  const uint32_t a[4] = {xv.x, xv.y, xv.z, xv.w}, w[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = round_bf16(round_bf16(__uint_as_float(a[i] << 16) * r) * __uint_as_float(w[i] << 16));
+    const float hi = round_bf16(round_bf16(__uint_as_float(a[i] & 0xFFFF0000u) * r) *
+                                __uint_as_float(w[i] & 0xFFFF0000u));
+    o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <int NB, int CHN, bool NORM>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                         const uint16_t* __restrict__ W, int64_t ldw,
                                                         int rows, int hidden,
-                                                        uint16_t* __restrict__ y, int64_t ldy) {
+                                                        uint16_t* __restrict__ y, int64_t ldy,
+                                                        const uint16_t* __restrict__ norm_w, float eps,
+                                                        uint16_t* __restrict__ xn, int64_t ldxn) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -256,12 +275,36 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
 #pragma unroll
   for (int t = 0; t < NB; ++t) {
     acc[t] = 0.f;
+    uint4 xv[CHN];
 #pragma unroll
     for (int i = 0; i < CHN; ++i) {
       const int c = lane + 64 * i;
-      const uint4 xv = c < nch ? *reinterpret_cast<const uint4*>(x + t * ldx + c * 8) : make_uint4(0, 0, 0, 0);
-      acc[t] = dot8(wv[i], xv, acc[t]);
+      xv[i] = c < nch ? *reinterpret_cast<const uint4*>(x + t * ldx + c * 8) : make_uint4(0, 0, 0, 0);
     }
+    if (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < CHN; ++i) {
+        const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = __uint_as_float(a[j] << 16), hi = __uint_as_float(a[j] & 0xFFFF0000u);
+          ss = fmaf(lo, lo, ss);
+          ss = fmaf(hi, hi, ss);
+        }
+      }
+      const float r = rsqrtf(wave_sum(ss) / static_cast<float>(hidden) + eps);
+#pragma unroll
+      for (int i = 0; i < CHN; ++i) {
+        const int c = lane + 64 * i;
+        const uint4 nw = c < nch ? *reinterpret_cast<const uint4*>(norm_w + c * 8) : make_uint4(0, 0, 0, 0);
+        xv[i] = rmsnorm8(xv[i], nw, r);
+        if (blockIdx.x == 0 && threadIdx.x < 64 && c < nch)
+          *reinterpret_cast<uint4*>(xn + t * ldxn + c * 8) = xv[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) acc[t] = dot8(wv[i], xv[i], acc[t]);
   }
 #pragma unroll
   for (int t = 0; t < NB; ++t) {
@@ -270,14 +313,16 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
   }
 }
 
-template <int NB>
+template <int NB, bool NORM = false>
 void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, int rows, int hidden,
-                      void* y, int64_t ldy, hipStream_t st) {
+                      void* y, int64_t ldy, hipStream_t st, const void* norm_w = nullptr,
+                      float eps = 0.f, void* xn = nullptr, int64_t ldxn = 0) {
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
   const int chn = (hidden / 8 + 63) / 64;
-#define MOC_GR(C)                                                                                 \
-  gemv_rows_kernel<NB, C><<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (const uint16_t*)W, ldw, \
-                                                   rows, hidden, (uint16_t*)y, ldy)
+#define MOC_GR(C)                                                                                  \
+  gemv_rows_kernel<NB, C, NORM><<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (const uint16_t*)W, \
+                                                         ldw, rows, hidden, (uint16_t*)y, ldy,       \
+                                                         (const uint16_t*)norm_w, eps, (uint16_t*)xn, ldxn)
   if (chn <= 1) MOC_GR(1);
   else if (chn <= 2) MOC_GR(2);
   else if (chn <= 4) MOC_GR(4);
@@ -317,7 +362,8 @@ template <int L, int CW>
 __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
     int k, int P, int CB, const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ wdt,
-    float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y) {
+    float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ res) {
   constexpr int QN = CW / 8;            // 16-byte chunks per row segment
   constexpr int S = kUdThreads / QN;    // row segments summed in parallel
   static_assert(S * QN == kUdThreads, "CW / 8 must divide the workgroup");
@@ -475,7 +521,10 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     float t = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) t += flat[g * CW + tid];
-    y[static_cast<int64_t>(b) * hidden + cb * CW + tid] = f32_to_bf16(t);
+    const int64_t o = static_cast<int64_t>(b) * hidden + cb * CW + tid;
+    // with a residual: the layer's x + FFN(x), both bf16 as in the reference
+    // (benchmark_decode.py:303)
+    y[o] = res ? f32_to_bf16(bf16_to_f32(res[o]) + round_bf16(t)) : f32_to_bf16(t);
   }
   if (tid == 0) cnt[b * CB + cb] = 0;  // ready for the next call
 }
@@ -661,14 +710,14 @@ inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
 template <int CW>
 void launch_fused(const void* x, int hidden, const void* gate, int inter, int k, int nb,
                   const FusedShape& f, const void* w_up, const void* wdt, float* part, int* cnt,
-                  void* y, hipStream_t st) {
+                  void* y, const void* res, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
   const int per = (inter + kUdThreads - 1) / kUdThreads;
 #define MOC_FU(N)                                                                               \
   select_up_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)x, hidden,               \
                                                        (const uint16_t*)gate, inter, k, f.P, f.CB, \
                                                        (const uint16_t*)w_up, (const uint16_t*)wdt, \
-                                                       part, cnt, (uint16_t*)y)
+                                                       part, cnt, (uint16_t*)y, (const uint16_t*)res)
   if (per <= 8) MOC_FU(8);
   else if (per <= 16) MOC_FU(16);
   else if (per <= 24) MOC_FU(24);
@@ -719,6 +768,31 @@ extern "C" int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void*
   gemv16_kernel<<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw,
                                         (int)rows, (int)hidden, (uint16_t*)y, ldy);
   return check_launch("gemv16_kernel");
+}
+
+extern "C" int moc_gemv_rmsnorm_bf16(const void* x, int64_t ldx, int64_t nb, const void* norm_w,
+                                     float eps, void* xn, int64_t ldxn, const void* W, int64_t ldw,
+                                     int64_t rows, int64_t hidden, void* y, int64_t ldy, void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 4, "moc_gemv_rmsnorm_bf16: 0 <= nb <= 4 tokens (got %lld)", (long long)nb);
+  MOC_REQUIRE(rows >= 0 && rows < (1LL << 31) && hidden >= 8 && hidden <= 4096 && hidden % 8 == 0,
+              "moc_gemv_rmsnorm_bf16: hidden must be a multiple of 8 in [8, 4096]");
+  MOC_REQUIRE(ldx >= hidden && ldw >= hidden && ldy >= rows && ldxn >= hidden,
+              "moc_gemv_rmsnorm_bf16: bad leading dimension");
+  MOC_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ldxn % 8 == 0,
+              "moc_gemv_rmsnorm_bf16: ldx/ldw/ldxn must be multiples of 8");
+  MOC_REQUIRE(eps >= 0.f, "moc_gemv_rmsnorm_bf16: eps must be >= 0");
+  if (nb == 0 || rows == 0) return MOC_OK;
+  MOC_REQUIRE(x && norm_w && xn && W && y, "moc_gemv_rmsnorm_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(W) && aligned16(norm_w) && aligned16(xn),
+              "moc_gemv_rmsnorm_bf16: x, norm_w, xn and W must be 16-byte aligned");
+  hipStream_t st = as_stream(stream);
+  switch (nb) {
+    case 1: launch_gemv_rows<1, true>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, norm_w, eps, xn, ldxn); break;
+    case 2: launch_gemv_rows<2, true>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, norm_w, eps, xn, ldxn); break;
+    case 3: launch_gemv_rows<3, true>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, norm_w, eps, xn, ldxn); break;
+    default: launch_gemv_rows<4, true>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, norm_w, eps, xn, ldxn); break;
+  }
+  return check_launch("gemv_rows_kernel (rmsnorm)");
 }
 
 extern "C" int moc_selected_up_silu_bf16(const void* x, int64_t nb, int64_t hidden,
@@ -786,11 +860,11 @@ extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inte
   return kFusedCounterBytes + nb * f.P * hidden * 4;
 }
 
-extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
-                                          int64_t inter, int64_t hidden, const void* w_up,
-                                          const void* w_down_t, int64_t k, void* y,
-                                          void* workspace, int64_t workspace_bytes,
-                                          void* stream) {
+namespace moc {
+namespace {
+int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter, int64_t hidden,
+                      const void* w_up, const void* w_down_t, int64_t k, const void* res, void* y,
+                      void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64, "moc_global_after_gate_bf16: bad shape");
   MOC_REQUIRE(hidden % 64 == 0, "moc_global_after_gate_bf16: hidden must be a multiple of 64");
@@ -810,9 +884,30 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
   hipStream_t st = as_stream(stream);
   if (f.CW == 256)
     launch_fused<256>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, w_up, w_down_t, part,
-                      cnt, y, st);
+                      cnt, y, res, st);
   else
     launch_fused<64>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, w_up, w_down_t, part,
-                     cnt, y, st);
+                     cnt, y, res, st);
   return check_launch("select_up_down_kernel");
+}
+}  // namespace
+}  // namespace moc
+
+extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
+                                          int64_t inter, int64_t hidden, const void* w_up,
+                                          const void* w_down_t, int64_t k, void* y,
+                                          void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, workspace,
+                           workspace_bytes, stream);
+}
+
+extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
+                                                   int64_t inter, int64_t hidden, const void* w_up,
+                                                   const void* w_down_t, int64_t k, const void* residual,
+                                                   void* y, void* workspace, int64_t workspace_bytes,
+                                                   void* stream) {
+  MOC_REQUIRE(nb == 0 || residual != nullptr, "moc_global_after_gate_residual_bf16: null residual");
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, residual, y,
+                           workspace, workspace_bytes, stream);
 }

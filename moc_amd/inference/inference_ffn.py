@@ -164,6 +164,26 @@ class InferenceMoCSwiGLUFFN(nn.Module):
             x_2d, gate_full, self.up_proj.weight, self._down_weight_t, self.config.k)
         return self._restore_output_shape(y, shp)
 
+    def fused_decode_residual(self, x: torch.Tensor, norm_weight: torch.Tensor,
+                              eps: float) -> torch.Tensor:
+        """x + FFN(RMSNorm(x)) for a decoder layer's FFN half, global MoC,
+        <= 4 tokens: the pre-norm runs inside the gate GEMV and the residual
+        add inside the after-gate kernel's last step, two launches in all
+        (the layer of benchmark_decode.py:303 with RMSNorm of :101-109).
+        Other shapes: the same result unfused."""
+        x_2d, shp = self._flatten_decode_input(x)
+        if self.config.grouped or x_2d.shape[0] > 4 or x_2d.dtype != torch.bfloat16:
+            xf = x_2d.float()
+            xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x_2d.dtype) * norm_weight
+            return self._restore_output_shape(x_2d + self.forward(xn), shp)
+        ensure_native_ops_ready()
+        self._ensure_down_weight_t()
+        x_2d = x_2d.contiguous()
+        gate_full, xn = K.gemv_rmsnorm(x_2d, norm_weight, eps, self.gate_proj.weight)
+        y = K.global_after_gate(xn, gate_full, self.up_proj.weight, self._down_weight_t,
+                                self.config.k, residual=x_2d)
+        return self._restore_output_shape(y, shp)
+
     def make_moc2_8_graph_runner(self, batch_size: int, gate_up_BLOCK_B: int | None = None,
                                  gate_up_BLOCK_G: int | None = None,
                                  gate_up_BLOCK_H: int | None = None,

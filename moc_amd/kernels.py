@@ -347,6 +347,29 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = No
     return y
 
 
+def gemv_rmsnorm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: torch.Tensor, *,
+                 out: torch.Tensor | None = None, xn_out: torch.Tensor | None = None):
+    """(y, xn): xn = RMSNorm(x) (f32 statistics, bf16 rounding as torch's
+    (x.float() * r).to(bf16) * w), y = xn @ weight.T, for <= 4 tokens."""
+    N.require_device(x, norm_weight, weight)
+    xx = aligned_rows(x)
+    w = aligned_rows(weight)
+    nw = norm_weight.contiguous()
+    nb, hidden = xx.shape
+    rows = w.shape[0]
+    if w.shape[1] != hidden or nw.shape != (hidden,):
+        raise ValueError("gemv_rmsnorm shape mismatch")
+    for t in (xx, w, nw):
+        if t.dtype != torch.bfloat16:
+            raise ValueError("gemv_rmsnorm is bf16 only")
+    y = _empty((nb, rows), torch.bfloat16, x.device) if out is None else out
+    xn = _empty((nb, hidden), torch.bfloat16, x.device) if xn_out is None else xn_out
+    N.call("moc_gemv_rmsnorm_bf16", xx.data_ptr(), xx.stride(0) if nb > 1 else round_up(hidden, 8), nb,
+           nw.data_ptr(), float(eps), xn.data_ptr(), xn.stride(0) if nb > 1 else round_up(hidden, 8),
+           w.data_ptr(), w.stride(0), rows, hidden, y.data_ptr(), rows, N.stream_of(x))
+    return y, xn
+
+
 def _bf16_contig(*ts):
     for t in ts:
         if t.dtype != torch.bfloat16:
@@ -407,22 +430,45 @@ def global_after_gate_workspace(nb: int, inter: int, k: int, hidden: int, device
 
 
 def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, workspace=None,
-                      out=None) -> torch.Tensor:
+                      out=None, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-K + selected Up * SiLU + selected Down after the gate; with
+    `residual`, returns residual + that (bf16 add) from the same launch."""
     N.require_device(x, gate_scores, up_weight, down_weight_t)
     x, g, wu, wdt = _bf16_contig(x, gate_scores, up_weight, down_weight_t)
     nb, hidden = x.shape
     inter = g.shape[1]
     if wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
         raise ValueError("up_weight and down_weight_t must be [intermediate, hidden]")
+    if nb > 16:
+        # more tokens than the fused kernel takes: the same steps as separate
+        # launches (row Top-K, selected Up * SiLU, selected Down), like the
+        # reference's op, which accepts any batch (optimized_global_moc_ext.cu:457-540)
+        vals, idx, _ = topk_rows(g, int(k), idx_dtype=torch.int32)
+        z = selected_up_silu(x, vals, idx, wu)
+        yy = selected_down(z, idx, wdt)
+        if residual is not None:
+            yy = residual.reshape(yy.shape) + yy
+        if out is None:
+            return yy
+        out.copy_(yy)
+        return out
     y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
     ws_bytes = N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
     if workspace is None:
         workspace = _decode_workspace(x.device, ws_bytes)
     elif workspace.numel() < ws_bytes:
         raise ValueError(f"global_after_gate: workspace of {ws_bytes} bytes required")
-    N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
-           wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), workspace.data_ptr(), ws_bytes,
-           N.stream_of(x))
+    if residual is None:
+        N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
+               wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), workspace.data_ptr(), ws_bytes,
+               N.stream_of(x))
+        return y
+    r = residual.reshape(nb, hidden)
+    if r.dtype != torch.bfloat16 or not r.is_contiguous():
+        raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
+    N.call("moc_global_after_gate_residual_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
+           wu.data_ptr(), wdt.data_ptr(), int(k), r.data_ptr(), y.data_ptr(), workspace.data_ptr(),
+           ws_bytes, N.stream_of(x))
     return y
 
 

@@ -396,6 +396,41 @@ def test_global_decode_path_1b(nb):
     close(y2, y, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("nb", [1, 2, 3, 4])
+def test_gemv_rmsnorm_fused_prologue(nb):
+    """The gate GEMV with the FFN's RMSNorm in front: xn matches the
+    reference formula (x.float() * rsqrt(mean(x^2) + eps)).to(bf16) * w to
+    one bf16 ulp (the f32 mean is summed in another order), and y equals the
+    plain GEMV of that xn bit for bit (same dot products)."""
+    d, inter, eps = 2048, 5461, 1e-6
+    g = gen(300 + nb)
+    x = (torch.randn(nb, d, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    y, xn = K().gemv_rmsnorm(x, nw, eps, wg)
+    xf = x.float()
+    want = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16) * nw
+    bf16_close(xn, want.float().cpu(), ulps=1, atol=0)
+    assert torch.equal(y, K().gemv(xn, wg))
+
+
+@pytest.mark.parametrize("nb", [1, 4])
+def test_global_after_gate_residual(nb):
+    """The residual add in the after-gate kernel's last step equals the
+    bf16 add of the residual and the plain result, bit for bit."""
+    d, inter, k = 2048, 5461, 1024
+    g = gen(320 + nb)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    res = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    G = K().gemv(x, wg)
+    y = K().global_after_gate(x, G, wu, wdt, k)
+    yr = K().global_after_gate(x, G, wu, wdt, k, residual=res)
+    assert torch.equal(yr, res + y)
+
+
 def test_grouped_2of8_integer_inputs_bitexact():
     """Integer-valued bf16 inputs make G and U exact, so the fused kernel's
     selection can be compared bit-exactly with the oracle."""
