@@ -481,9 +481,9 @@ def main():
         _native.load()
         rows = []
         for row, scope, fuse in (("dense", "whole_graph", False), ("global_moc", "whole_graph", True),
-                                 ("global_moc", "whole_graph", False), ("moc_2_8", "whole_graph", False),
-                                 ("dense", "eager", False), ("global_moc", "eager", True),
-                                 ("moc_2_8", "eager", False)):
+                                 ("global_moc", "whole_graph", False), ("moc_2_8", "whole_graph", True),
+                                 ("moc_2_8", "whole_graph", False), ("dense", "eager", False),
+                                 ("global_moc", "eager", True), ("moc_2_8", "eager", True)):
             log(f"decode e2e {row} {scope} fuse={fuse}")
             rows.append(measure_decode(row, scope=scope, fuse=fuse))
             torch.cuda.empty_cache()

@@ -245,6 +245,14 @@ int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t hidden, con
                                   const void* w_up, int64_t inter, void* idx, void* sz,
                                   void* stream);
 
+/* moc_grouped_top2_up_silu_bf16 of the RMSNorm'd tokens (rounding as in
+ * moc_gemv_rmsnorm_bf16: the FFN's pre-norm fused into the gate/up
+ * projection, benchmark_decode.py:101-109,303), nb <= 4, hidden <= 4096. */
+int moc_grouped_top2_up_silu_rmsnorm_bf16(const void* x, int64_t nb, int64_t hidden,
+                                          const void* norm_w, float eps, const void* w_gate,
+                                          const void* w_up, int64_t inter, void* idx, void* sz,
+                                          void* stream);
+
 /* Workspace bytes moc_selected_grouped_down_bf16 needs. */
 int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t inter,
                                                  int64_t hidden);
@@ -255,6 +263,14 @@ int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t 
 int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb, int64_t k,
                                    const void* w_down_t, int64_t inter, int64_t hidden, void* y,
                                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* moc_selected_grouped_down_bf16 for nb <= 64 tokens with the layer's
+ * residual added in its last step: y = bf16(residual + bf16(FFN)), the
+ * decoder's x + ffn(norm(x)) (benchmark_decode.py:303).  Same workspace. */
+int moc_selected_grouped_down_residual_bf16(const void* sz, const void* idx, int64_t nb, int64_t k,
+                                            const void* w_down_t, int64_t inter, int64_t hidden,
+                                            const void* residual, void* y, void* workspace,
+                                            int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

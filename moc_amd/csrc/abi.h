@@ -20,6 +20,12 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// moc_selected_down_bf16 with an optional residual added in the last step
+// (y = bf16(res + bf16(sum)); res may be null) (decode.hip).
+int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
+                       const void* w_down_t, int64_t inter, int64_t hidden, const void* res, void* y,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
 // MoC 2:8 gate/up + top-2-of-8 for nb tokens on the MFMA GEMM kernel
 // (gemm.hip); 1: shape not supported there (nothing launched).
 int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* wg, const void* wu,

@@ -114,6 +114,34 @@ __device__ __forceinline__ void select_group_emit(const float* g, const float* u
   sz_out[1] = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
 }
 
+// Dot product of 8 bf16 pairs (two 16-byte chunks) accumulated in f32.
+__device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = fmaf(__uint_as_float(aw[i] << 16), __uint_as_float(bw[i] << 16), acc);
+    acc = fmaf(__uint_as_float(aw[i] & 0xFFFF0000u), __uint_as_float(bw[i] & 0xFFFF0000u), acc);
+  }
+  return acc;
+}
+
+// RMSNorm of 8 bf16 values with the row's factor r = 1 / sqrt(mean(x^2) +
+// eps) and the norm weights w: bf16(bf16(x * r) * w), the rounding points of
+// (x.float() * r).to(bf16) * w (benchmark_decode.py:101-109).
+__device__ __forceinline__ uint4 rmsnorm8(uint4 xv, uint4 wv, float r) {
+  const uint32_t a[4] = {xv.x, xv.y, xv.z, xv.w}, w[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = round_bf16(round_bf16(__uint_as_float(a[i] << 16) * r) * __uint_as_float(w[i] << 16));
+    const float hi = round_bf16(round_bf16(__uint_as_float(a[i] & 0xFFFF0000u) * r) *
+                                __uint_as_float(w[i] & 0xFFFF0000u));
+    o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------

@@ -41,17 +41,6 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr uint32_t kOob = 0x80000000u;  // buffer offset that reads as zero
 
-__device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
-  const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc = fmaf(__uint_as_float(aw[i] << 16), __uint_as_float(bw[i] << 16), acc);
-    acc = fmaf(__uint_as_float(aw[i] & 0xFFFF0000u), __uint_as_float(bw[i] & 0xFFFF0000u), acc);
-  }
-  return acc;
-}
-
 template <typename IdxT>
 __device__ __forceinline__ int64_t load_idx(const void* p, int64_t e) {
   return static_cast<int64_t>(static_cast<const IdxT*>(p)[e]);
@@ -240,19 +229,6 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
 // benchmark_decode.py:101-109,303): xn = bf16(bf16(x * r) * w) with
 // r = 1 / sqrt(mean(x^2) + eps) in f32; every wave normalises its own copy
 // of x, and wave 0 of workgroup 0 also writes xn for the kernels after it.
-__device__ __forceinline__ uint4 rmsnorm8(uint4 xv, uint4 wv, float r) {
-  const uint32_t a[4] = {xv.x, xv.y, xv.z, xv.w}, w[4] = {wv.x, wv.y, wv.z, wv.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lo = round_bf16(round_bf16(__uint_as_float(a[i] << 16) * r) * __uint_as_float(w[i] << 16));
-    const float hi = round_bf16(round_bf16(__uint_as_float(a[i] & 0xFFFF0000u) * r) *
-                                __uint_as_float(w[i] & 0xFFFF0000u));
-    o[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
-  }
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
-
 template <int NB, int CHN, bool NORM>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                         const uint16_t* __restrict__ W, int64_t ldw,
@@ -270,6 +246,14 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
     const int c = lane + 64 * i;
     wv[i] = c < nch ? *reinterpret_cast<const uint4*>(W + static_cast<int64_t>(row) * ldw + c * 8)
                     : make_uint4(0, 0, 0, 0);
+  }
+  uint4 nwv[NORM ? CHN : 1];  // norm weight chunks, requested with the row
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      nwv[i] = c < nch ? *reinterpret_cast<const uint4*>(norm_w + c * 8) : make_uint4(0, 0, 0, 0);
+    }
   }
   float acc[NB];
 #pragma unroll
@@ -297,8 +281,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
 #pragma unroll
       for (int i = 0; i < CHN; ++i) {
         const int c = lane + 64 * i;
-        const uint4 nw = c < nch ? *reinterpret_cast<const uint4*>(norm_w + c * 8) : make_uint4(0, 0, 0, 0);
-        xv[i] = rmsnorm8(xv[i], nw, r);
+        xv[i] = rmsnorm8(xv[i], nwv[NORM ? i : 0], r);
         if (blockIdx.x == 0 && threadIdx.x < 64 && c < nch)
           *reinterpret_cast<uint4*>(xn + t * ldxn + c * 8) = xv[i];
       }
@@ -542,7 +525,7 @@ template <typename IdxT>
 __global__ __launch_bounds__(256) void selected_down_kernel(
     const uint16_t* __restrict__ z, const void* __restrict__ idx, int k, int hidden,
     const uint16_t* __restrict__ wdt, int inter, int G, float* __restrict__ part,
-    int* __restrict__ cnt, uint16_t* __restrict__ y) {
+    int* __restrict__ cnt, uint16_t* __restrict__ y, const uint16_t* __restrict__ res) {
   __shared__ float red[32][65];
   __shared__ int last;
   const int tid = threadIdx.x;
@@ -604,7 +587,9 @@ __global__ __launch_bounds__(256) void selected_down_kernel(
     for (int gi = 0; gi < G; ++gi)
       s += __hip_atomic_load(p0 + static_cast<int64_t>(gi) * hidden, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-    y[static_cast<int64_t>(b) * hidden + cb * 64 + tid] = f32_to_bf16(s);
+    const int64_t o = static_cast<int64_t>(b) * hidden + cb * 64 + tid;
+    // with a residual: the layer's x + FFN(x), both bf16 as in the reference
+    y[o] = res ? f32_to_bf16(bf16_to_f32(res[o]) + round_bf16(s)) : f32_to_bf16(s);
   }
   if (tid == 0) cnt[b * (hidden / 64) + cb] = 0;  // ready for the next call
 }
@@ -670,7 +655,7 @@ inline DownWs down_ws(int64_t nb, int64_t k, int64_t hidden) {
 
 int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
                          const void* wdt, int64_t inter, int64_t hidden, void* y, void* ws,
-                         hipStream_t st) {
+                         hipStream_t st, const void* res = nullptr) {
   const DownWs w = down_ws(nb, k, hidden);
   float* part = static_cast<float*>(ws);
   int* cnt = reinterpret_cast<int*>(static_cast<char*>(ws) + w.part_bytes);
@@ -678,7 +663,7 @@ int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t 
 #define MOC_DOWN(T)                                                                         \
   selected_down_kernel<T><<<grid, block, 0, st>>>((const uint16_t*)z, idx, (int)k, (int)hidden, \
                                                   (const uint16_t*)wdt, (int)inter, w.G, part, \
-                                                  cnt, (uint16_t*)y)
+                                                  cnt, (uint16_t*)y, (const uint16_t*)res)
   if (idx_dtype == MOC_I16) MOC_DOWN(int16_t);
   else if (idx_dtype == MOC_I32) MOC_DOWN(int32_t);
   else MOC_DOWN(int64_t);
@@ -827,10 +812,10 @@ extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64
   return w.part_bytes + w.cnt_bytes;
 }
 
-extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
-                                      int64_t k, const void* w_down_t, int64_t inter,
-                                      int64_t hidden, void* y, void* workspace,
-                                      int64_t workspace_bytes, void* stream) {
+namespace moc {
+int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
+                       const void* w_down_t, int64_t inter, int64_t hidden, const void* res, void* y,
+                       void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(idx_ok(idx_dtype), "moc_selected_down_bf16: bad index dtype");
   MOC_REQUIRE(nb >= 0 && k >= 1 && inter >= 1 && hidden >= 1, "moc_selected_down_bf16: bad shape");
   MOC_REQUIRE(hidden % 64 == 0, "moc_selected_down_bf16: hidden must be a multiple of 64");
@@ -845,7 +830,16 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
   int rc = moc_fill_zero(static_cast<char*>(workspace) + w.part_bytes, w.cnt_bytes, stream);
   if (rc != MOC_OK) return rc;
   return launch_selected_down(z, idx, idx_dtype, nb, k, w_down_t, inter, hidden, y, workspace,
-                              as_stream(stream));
+                              as_stream(stream), res);
+}
+}  // namespace moc
+
+extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
+                                      int64_t k, const void* w_down_t, int64_t inter,
+                                      int64_t hidden, void* y, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  return selected_down_impl(z, idx, idx_dtype, nb, k, w_down_t, inter, hidden, nullptr, y, workspace,
+                            workspace_bytes, stream);
 }
 
 // Workspace: a fixed 64 KB block of arrival counters (so the counters of one

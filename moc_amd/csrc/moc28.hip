@@ -121,6 +121,122 @@ __global__ __launch_bounds__(256) void grouped_decode_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// nb <= 4 path, row streaming: a workgroup of 8 waves covers 16 channels (two
+// groups of 8); wave w owns channels c0 + 2w and c0 + 2w + 1 and requests
+// their W_gate and W_up rows whole (lane l: 16-byte chunks l + 64 i), so
+// every byte of the four rows is in flight within one memory latency (the
+// gate GEMV's scheme).  NORM: the tokens go through the FFN's RMSNorm first
+// (rmsnorm8; every wave normalises its own copy of x).  G and U are rounded
+// to bf16 and the two groups selected from LDS.
+// ---------------------------------------------------------------------------
+template <int NB, int CHN, bool NORM>
+__global__ __launch_bounds__(512) void grouped_rows_kernel(
+    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ wg,
+    const uint16_t* __restrict__ wu, int inter, int64_t* __restrict__ idx, uint16_t* __restrict__ sz,
+    const uint16_t* __restrict__ norm_w, float eps) {
+  __shared__ float gu[2][16][NB];  // [g | u][channel][token]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c0 = blockIdx.x * 16;
+  const int nch = hidden / 8;
+  uint4 w[4][CHN];  // gate ch0, gate ch1, up ch0, up ch1
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int ch = c0 + 2 * wave + (r & 1);
+    const uint16_t* row = (r < 2 ? wg : wu) + static_cast<int64_t>(ch < inter ? ch : 0) * hidden;
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      w[r][i] = (ch < inter && c < nch) ? *reinterpret_cast<const uint4*>(row + c * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  uint4 nwv[NORM ? CHN : 1];
+  if (NORM) {
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      nwv[i] = c < nch ? *reinterpret_cast<const uint4*>(norm_w + c * 8) : make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    uint4 xv[CHN];
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      xv[i] = c < nch ? *reinterpret_cast<const uint4*>(x + static_cast<int64_t>(t) * hidden + c * 8)
+                      : make_uint4(0, 0, 0, 0);
+    }
+    if (NORM) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < CHN; ++i) {
+        const uint32_t a[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = __uint_as_float(a[j] << 16), hi = __uint_as_float(a[j] & 0xFFFF0000u);
+          ss = fmaf(lo, lo, ss);
+          ss = fmaf(hi, hi, ss);
+        }
+      }
+      const float rr = rsqrtf(wave_sum(ss) / static_cast<float>(hidden) + eps);
+#pragma unroll
+      for (int i = 0; i < CHN; ++i) xv[i] = rmsnorm8(xv[i], nwv[NORM ? i : 0], rr);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < CHN; ++i) a = dot8(w[r][i], xv[i], a);
+      a = wave_sum(a);
+      if (lane == 0) gu[r >> 1][2 * wave + (r & 1)][t] = round_bf16(a);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * NB) {
+    const int t = threadIdx.x % NB, grp = threadIdx.x / NB;
+    const int cg = c0 + grp * 8;
+    if (cg < inter) {
+      float g[8], u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        g[j] = gu[0][grp * 8 + j][t];
+        u[j] = gu[1][grp * 8 + j][t];
+      }
+      const int64_t o = static_cast<int64_t>(t) * (inter / 4) + (cg / 8) * 2;
+      select_group_emit(g, u, cg, idx + o, sz + o);
+    }
+  }
+}
+
+template <int NB, bool NORM>
+void launch_grouped_rows(const void* x, int hidden, const void* wg, const void* wu, int inter, void* idx,
+                         void* sz, const void* norm_w, float eps, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((inter + 15) / 16)), block(512);
+  const int chn = (hidden / 8 + 63) / 64;
+#define MOC_GRW(C)                                                                                    \
+  grouped_rows_kernel<NB, C, NORM><<<grid, block, 0, st>>>((const uint16_t*)x, hidden,                \
+                                                            (const uint16_t*)wg, (const uint16_t*)wu, \
+                                                            inter, (int64_t*)idx, (uint16_t*)sz,      \
+                                                            (const uint16_t*)norm_w, eps)
+  if (chn <= 1) MOC_GRW(1);
+  else if (chn <= 2) MOC_GRW(2);
+  else if (chn <= 4) MOC_GRW(4);
+  else MOC_GRW(8);
+#undef MOC_GRW
+}
+
+template <bool NORM>
+void launch_grouped_rows_nb(int nb, const void* x, int hidden, const void* wg, const void* wu, int inter,
+                            void* idx, void* sz, const void* norm_w, float eps, hipStream_t st) {
+  switch (nb) {
+    case 1: launch_grouped_rows<1, NORM>(x, hidden, wg, wu, inter, idx, sz, norm_w, eps, st); break;
+    case 2: launch_grouped_rows<2, NORM>(x, hidden, wg, wu, inter, idx, sz, norm_w, eps, st); break;
+    case 3: launch_grouped_rows<3, NORM>(x, hidden, wg, wu, inter, idx, sz, norm_w, eps, st); break;
+    default: launch_grouped_rows<4, NORM>(x, hidden, wg, wu, inter, idx, sz, norm_w, eps, st); break;
+  }
+}
+
 // B tile of the fused gate/up GEMM: rows [0, 64) are W_gate rows c0.., rows
 // [64, 128) the same W_up rows; same thread mapping and LDS layout as the
 // K-contiguous TileLoader.
@@ -269,6 +385,10 @@ extern "C" int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t 
   MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up),
               "moc_grouped_top2_up_silu_bf16: x and weights must be 16-byte aligned");
   hipStream_t st = as_stream(stream);
+  if (nb <= 4 && hidden <= 4096) {
+    launch_grouped_rows_nb<false>((int)nb, x, (int)hidden, w_gate, w_up, (int)inter, idx, sz, nullptr, 0.f, st);
+    return check_launch("grouped_rows_kernel");
+  }
   if (nb <= 16) {
     grouped_decode_kernel<<<dim3(static_cast<unsigned>((inter + 15) / 16)), 256, 0, st>>>(
         (const uint16_t*)x, (int)nb, (int)hidden, (const uint16_t*)w_gate, (const uint16_t*)w_up,
@@ -326,4 +446,37 @@ extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, i
   return moc_gemm_ws(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, hidden, 1, 0,
                      nullptr, 0, 0, nullptr, 0, 0, y, hidden, MOC_BF16, gbytes > 0 ? gws : nullptr,
                      gbytes, stream);
+}
+
+extern "C" int moc_grouped_top2_up_silu_rmsnorm_bf16(const void* x, int64_t nb, int64_t hidden,
+                                                     const void* norm_w, float eps, const void* w_gate,
+                                                     const void* w_up, int64_t inter, void* idx, void* sz,
+                                                     void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 4, "moc_grouped_top2_up_silu_rmsnorm_bf16: 0 <= nb <= 4 tokens");
+  MOC_REQUIRE(hidden >= 8 && hidden <= 4096 && hidden % 8 == 0,
+              "moc_grouped_top2_up_silu_rmsnorm_bf16: hidden must be a multiple of 8 in [8, 4096]");
+  MOC_REQUIRE(inter >= 8 && inter % 8 == 0 && inter < (1LL << 30),
+              "intermediate=%lld must be divisible by 8", (long long)inter);
+  MOC_REQUIRE(eps >= 0.f, "moc_grouped_top2_up_silu_rmsnorm_bf16: eps must be >= 0");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && norm_w && w_gate && w_up && idx && sz, "moc_grouped_top2_up_silu_rmsnorm_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(norm_w) && aligned16(w_gate) && aligned16(w_up),
+              "moc_grouped_top2_up_silu_rmsnorm_bf16: x, norm_w and weights must be 16-byte aligned");
+  launch_grouped_rows_nb<true>((int)nb, x, (int)hidden, w_gate, w_up, (int)inter, idx, sz, norm_w, eps,
+                               as_stream(stream));
+  return check_launch("grouped_rows_kernel (rmsnorm)");
+}
+
+extern "C" int moc_selected_grouped_down_residual_bf16(const void* sz, const void* idx, int64_t nb,
+                                                       int64_t k, const void* w_down_t, int64_t inter,
+                                                       int64_t hidden, const void* residual, void* y,
+                                                       void* workspace, int64_t workspace_bytes,
+                                                       void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 64, "moc_selected_grouped_down_residual_bf16: 0 <= nb <= 64 tokens");
+  MOC_REQUIRE(k >= 1 && inter >= k && hidden >= 1 && hidden % 64 == 0,
+              "moc_selected_grouped_down_residual_bf16: bad shape");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(residual != nullptr, "moc_selected_grouped_down_residual_bf16: null residual");
+  return selected_down_impl(sz, idx, MOC_I64, nb, k, w_down_t, inter, hidden, residual, y, workspace,
+                            workspace_bytes, stream);
 }

@@ -148,9 +148,9 @@ class DecoderLayer(nn.Module):
     def __init__(self, row: str, cfg: DecodeConfig, fuse: bool = True):
         super().__init__()
         self.mode = ROWS[row]
-        # global MoC decode: ffn_norm and the residual add run inside the FFN's
-        # two kernels (InferenceMoCSwiGLUFFN.fused_decode_residual)
-        self.fuse = fuse and row == "global_moc"
+        # MoC decode: ffn_norm and the residual add run inside the FFN's two
+        # kernels (InferenceMoCSwiGLUFFN.fused_decode_residual)
+        self.fuse = fuse and row in ("global_moc", "moc_2_8")
         grouped = row == "moc_2_8"
         k = cfg.intermediate * 2 // 8 if grouped else cfg.k
         self.attn_norm = RMSNorm(cfg.hidden)

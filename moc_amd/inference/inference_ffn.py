@@ -166,12 +166,22 @@ class InferenceMoCSwiGLUFFN(nn.Module):
 
     def fused_decode_residual(self, x: torch.Tensor, norm_weight: torch.Tensor,
                               eps: float) -> torch.Tensor:
-        """x + FFN(RMSNorm(x)) for a decoder layer's FFN half, global MoC,
-        <= 4 tokens: the pre-norm runs inside the gate GEMV and the residual
-        add inside the after-gate kernel's last step, two launches in all
-        (the layer of benchmark_decode.py:303 with RMSNorm of :101-109).
-        Other shapes: the same result unfused."""
+        """x + FFN(RMSNorm(x)) for a decoder layer's FFN half, <= 4 tokens,
+        in two launches: the pre-norm runs inside the gate GEMV (global MoC)
+        or the fused gate/up + top-2-of-8 kernel (MoC 2:8), the residual add
+        inside the last step of the after-gate kernel or of the selected
+        Down (the layer of benchmark_decode.py:303 with RMSNorm of
+        :101-109).  Other shapes: the same result unfused."""
         x_2d, shp = self._flatten_decode_input(x)
+        grouped28 = self.config.grouped and self.config.grouped_a == 2 and self.config.grouped_b == 8
+        if grouped28 and x_2d.shape[0] <= 4 and x_2d.dtype == torch.bfloat16:
+            ensure_native_ops_ready()
+            self._ensure_down_weight_t()
+            x_2d = x_2d.contiguous()
+            idx, sz = K.grouped_top2_up_silu(x_2d, self.gate_proj.weight, self.up_proj.weight,
+                                             norm_weight=norm_weight, eps=eps)
+            y = K.selected_grouped_down(sz, idx, self._down_weight_t, residual=x_2d)
+            return self._restore_output_shape(y, shp)
         if self.config.grouped or x_2d.shape[0] > 4 or x_2d.dtype != torch.bfloat16:
             xf = x_2d.float()
             xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x_2d.dtype) * norm_weight

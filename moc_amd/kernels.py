@@ -473,9 +473,11 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
 
 
 # ----------------------------------------------------------------------- 2:8
-def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None):
-    """-> (idx int64 [nb, inter/4], sparse_z bf16 [nb, inter/4])."""
-    N.require_device(x, gate_weight, up_weight)
+def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None,
+                         norm_weight: torch.Tensor | None = None, eps: float = 1e-6):
+    """-> (idx int64 [nb, inter/4], sparse_z bf16 [nb, inter/4]).  With
+    norm_weight (<= 4 tokens): of RMSNorm(x) (the FFN's pre-norm) instead."""
+    N.require_device(x, gate_weight, up_weight, norm_weight)
     x, wg, wu = _bf16_contig(x, gate_weight, up_weight)
     nb, hidden = x.shape
     inter = wg.shape[0]
@@ -488,8 +490,16 @@ def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None
     sz = _empty((nb, k), torch.bfloat16, x.device) if sz_out is None else sz_out
     if idx.shape != (nb, k) or sz.shape != (nb, k) or not (idx.is_contiguous() and sz.is_contiguous()):
         raise ValueError(f"out shapes must be ({nb},{k})")
-    N.call("moc_grouped_top2_up_silu_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(), wu.data_ptr(),
-           inter, idx.data_ptr(), sz.data_ptr(), N.stream_of(x))
+    if norm_weight is None:
+        N.call("moc_grouped_top2_up_silu_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(), wu.data_ptr(),
+               inter, idx.data_ptr(), sz.data_ptr(), N.stream_of(x))
+    else:
+        nw = norm_weight.contiguous()
+        if nw.dtype != torch.bfloat16 or nw.shape != (hidden,):
+            raise ValueError("norm_weight must be a bf16 [hidden] tensor")
+        N.call("moc_grouped_top2_up_silu_rmsnorm_bf16", x.data_ptr(), nb, hidden, nw.data_ptr(),
+               float(eps), wg.data_ptr(), wu.data_ptr(), inter, idx.data_ptr(), sz.data_ptr(),
+               N.stream_of(x))
     return idx, sz
 
 
@@ -497,8 +507,11 @@ def selected_grouped_down_workspace_bytes(nb: int, k: int, inter: int, hidden: i
     return N.query("moc_selected_grouped_down_workspace_size", nb, k, inter, hidden)
 
 
-def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=None) -> torch.Tensor:
-    N.require_device(sparse_z, idx, down_weight_t)
+def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=None,
+                          residual: torch.Tensor | None = None) -> torch.Tensor:
+    """y = sparse_z * W_down^T[idx]; with `residual` (<= 64 tokens),
+    residual + y (bf16 add) from the same launches."""
+    N.require_device(sparse_z, idx, down_weight_t, residual)
     sz, wdt = _bf16_contig(sparse_z, down_weight_t)
     ii = idx.contiguous()
     if ii.dtype != torch.int64:
@@ -511,6 +524,19 @@ def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=N
     ws_bytes = selected_grouped_down_workspace_bytes(nb, k, inter, hidden)
     ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else \
         _empty((max(ws_bytes, 1),), torch.uint8, sz.device)
-    N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
-           inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
+    if residual is None:
+        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
+               inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
+        return y
+    r = residual.reshape(nb, hidden)
+    if r.dtype != torch.bfloat16 or not r.is_contiguous():
+        raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
+    if nb > 64:
+        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
+               inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
+        y.copy_(r + y)
+        return y
+    N.call("moc_selected_grouped_down_residual_bf16", sz.data_ptr(), ii.data_ptr(), nb, k,
+           wdt.data_ptr(), inter, hidden, r.data_ptr(), y.data_ptr(), ws.data_ptr(), ws_bytes,
+           N.stream_of(sz))
     return y

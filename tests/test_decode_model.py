@@ -87,14 +87,15 @@ def test_decode_graph_matches_eager(row):
 
 
 @pytest.mark.gpu
-def test_decode_fused_ffn_neighbours_match_unfused():
-    """Global MoC decode with ffn_norm fused into the gate GEMV and the
-    residual add into the after-gate kernel gives the unfused layer's
-    logits (the RMSNorm statistics are summed in another order: bf16
-    tolerance) and the same greedy tokens."""
+@pytest.mark.parametrize("row", ["global_moc", "moc_2_8"])
+def test_decode_fused_ffn_neighbours_match_unfused(row):
+    """MoC decode with ffn_norm fused into the gate (or gate/up) kernel and
+    the residual add into the down kernel gives the unfused layer's logits
+    (the RMSNorm statistics are summed in another order: bf16 tolerance)
+    and the same greedy tokens."""
     cfg = DecodeConfig(layers=2, max_seq=40)
-    fused = DecoderModel("global_moc", cfg, fuse=True).to(DEV, torch.bfloat16).init_weights(9)
-    plain = DecoderModel("global_moc", cfg, fuse=False).to(DEV, torch.bfloat16)
+    fused = DecoderModel(row, cfg, fuse=True).to(DEV, torch.bfloat16).init_weights(9)
+    plain = DecoderModel(row, cfg, fuse=False).to(DEV, torch.bfloat16)
     plain.load_state_dict(fused.state_dict())
     for m in (fused, plain):
         m.allocate_cache()

@@ -431,6 +431,28 @@ def test_global_after_gate_residual(nb):
     assert torch.equal(yr, res + y)
 
 
+@pytest.mark.parametrize("nb", [1, 3, 4])
+def test_grouped_2of8_rmsnorm_and_residual(nb):
+    """The 2:8 decode kernels with the FFN's neighbours inside: gate/up of
+    RMSNorm(x) equals gate/up of the kernel-side norm (gemv_rmsnorm's xn,
+    same rounding) bit for bit, and the residual form of the selected Down
+    equals residual + Down."""
+    d, inter, eps = 2048, 5464, 1e-6
+    g = gen(340 + nb)
+    x = (torch.randn(nb, d, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    _, xn = K().gemv_rmsnorm(x, nw, eps, wg)
+    idx_f, sz_f = K().grouped_top2_up_silu(x, wg, wu, norm_weight=nw, eps=eps)
+    idx, sz = K().grouped_top2_up_silu(xn, wg, wu)
+    assert torch.equal(idx_f, idx) and torch.equal(sz_f, sz)
+    y = K().selected_grouped_down(sz, idx, wdt)
+    yr = K().selected_grouped_down(sz, idx, wdt, residual=x)
+    assert torch.equal(yr, x + y)
+
+
 def test_grouped_2of8_integer_inputs_bitexact():
     """Integer-valued bf16 inputs make G and U exact, so the fused kernel's
     selection can be compared bit-exactly with the oracle."""
