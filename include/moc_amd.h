@@ -76,6 +76,16 @@ int moc_topk_rows(int dtype, const void* scores, int64_t rows, int64_t inter, in
                   int64_t k, int score_transform, void* vals_out, void* idx_out, int idx_dtype,
                   uint32_t* mask_out, int64_t mask_ld, void* stream);
 
+/* Channel indices of a selection bit mask (mask[rows, ld_words] of uint32
+ * words, bit c%32 of word c/32 = channel c): idx[r, :] = the first k set
+ * bits of row r in ascending channel order (a moc_topk_rows mask has exactly
+ * k; slots a shorter row leaves empty get channel 0).  The backward's side
+ * of the compact saved-mask format (a bitmask of
+ * I bits per token instead of K int16 indices, moc/ffn.py:147,395,417); no
+ * counterpart in the reference. */
+int moc_mask_to_idx(const void* mask, int64_t rows, int64_t inter, int64_t ld_words, int64_t k,
+                    void* idx, int idx_dtype, void* stream);
+
 /* K' of the 2:8 structure: 2*floor(inter/8) + min(2, inter%8)
  * (moc/ffn.py:62-65). */
 int64_t moc_moc28_effective_k(int64_t inter);

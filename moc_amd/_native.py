@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "moc_fill_zero": (_int, [_vp, _i64, _vp]),
     "moc_copy_pad_2d": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp]),
     "moc_topk_rows": (_int, [_int, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _int, _vp, _i64, _vp]),
+    "moc_mask_to_idx": (_int, [_vp, _i64, _i64, _i64, _i64, _vp, _int, _vp]),
     "moc_moc28_effective_k": (_i64, [_i64]),
     "moc_select_2of8": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "moc_sparse_forward_aux": (_int, [_int, _vp, _vp, _int, _vp, _i64, _i64, _i64, _i64,

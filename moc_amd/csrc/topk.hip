@@ -243,10 +243,73 @@ __global__ __launch_bounds__(256) void select_2of8_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Bit mask -> channel indices: row r's set bits in ascending channel order,
+// the first k of them (a mask from moc_topk_rows has exactly k).  One
+// workgroup of 256 threads per row; thread t owns the W consecutive mask
+// words [t W, t W + W), counts their bits, and a block scan gives the
+// thread's first output slot.  Slots a short row leaves empty get channel 0
+// (always in range).
+// ---------------------------------------------------------------------------
+template <typename IdxT>
+__global__ __launch_bounds__(256) void mask_to_idx_kernel(const uint32_t* __restrict__ mask, int words,
+                                                          int64_t ldw, int k, int W,
+                                                          IdxT* __restrict__ idx) {
+  __shared__ uint32_t tot_w[4];
+  __shared__ uint32_t total;
+  const int64_t r = blockIdx.x;
+  const uint32_t* m = mask + r * ldw;
+  IdxT* out = idx + r * static_cast<int64_t>(k);
+  const int w0 = static_cast<int>(threadIdx.x) * W;
+  uint32_t cnt = 0;
+  for (int i = 0; i < W; ++i)
+    if (w0 + i < words) cnt += __popc(m[w0 + i]);
+  uint32_t t;
+  uint32_t pos = block_exclusive_scan(cnt, tot_w, &t);
+  for (int i = 0; i < W; ++i) {
+    if (w0 + i >= words) break;
+    uint32_t bits = m[w0 + i];
+    while (bits) {
+      const int b = __ffs(bits) - 1;
+      if (pos < static_cast<uint32_t>(k)) out[pos] = static_cast<IdxT>(32 * (w0 + i) + b);
+      ++pos;
+      bits &= bits - 1u;
+    }
+  }
+  for (uint32_t j = t + threadIdx.x; j < static_cast<uint32_t>(k); j += 256) out[j] = static_cast<IdxT>(0);
+  (void)total;
+}
+
 }  // namespace
 }  // namespace moc
 
 using namespace moc;
+
+extern "C" int moc_mask_to_idx(const void* mask, int64_t rows, int64_t inter, int64_t ld_words,
+                               int64_t k, void* idx, int idx_dtype, void* stream) {
+  MOC_REQUIRE(rows >= 0 && inter >= 1 && k >= 1 && k <= inter && inter < (1LL << 30),
+              "moc_mask_to_idx: bad shape");
+  const int64_t words = (inter + 31) / 32;
+  MOC_REQUIRE(ld_words >= words, "moc_mask_to_idx: ld_words < ceil(inter / 32)");
+  MOC_REQUIRE(idx_dtype == MOC_I16 || idx_dtype == MOC_I32 || idx_dtype == MOC_I64,
+              "moc_mask_to_idx: bad index dtype");
+  MOC_REQUIRE(idx_dtype != MOC_I16 || inter - 1 <= 32767,
+              "topk_idx range [0, %lld] cannot be stored as torch.int16", (long long)(inter - 1));
+  MOC_REQUIRE(rows < (1LL << 31), "moc_mask_to_idx: too many rows");
+  if (rows == 0) return MOC_OK;
+  MOC_REQUIRE(mask && idx, "moc_mask_to_idx: null pointer");
+  const int W = static_cast<int>((words + 255) / 256);
+  const dim3 grid(static_cast<unsigned>(rows)), block(256);
+  hipStream_t st = as_stream(stream);
+  const uint32_t* m = static_cast<const uint32_t*>(mask);
+  if (idx_dtype == MOC_I16)
+    mask_to_idx_kernel<int16_t><<<grid, block, 0, st>>>(m, (int)words, ld_words, (int)k, W, (int16_t*)idx);
+  else if (idx_dtype == MOC_I32)
+    mask_to_idx_kernel<int32_t><<<grid, block, 0, st>>>(m, (int)words, ld_words, (int)k, W, (int32_t*)idx);
+  else
+    mask_to_idx_kernel<int64_t><<<grid, block, 0, st>>>(m, (int)words, ld_words, (int)k, W, (int64_t*)idx);
+  return check_launch("mask_to_idx_kernel");
+}
 
 extern "C" int moc_topk_rows(int dtype, const void* scores, int64_t rows, int64_t inter,
                              int64_t ld, int64_t k, int score_transform, void* vals_out,

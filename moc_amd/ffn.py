@@ -38,11 +38,20 @@ _MODES = (
 )
 
 
+# index_save_dtype that saves the selection as a bit mask (ceil(I / 32)
+# int32 words per token instead of K indices: the compact saved-mask format,
+# an extension of moc/ffn.py:147,395,417); the backward expands it back to
+# indices (moc_mask_to_idx).  Top-K selections only.
+INDEX_SAVE_BITMASK = "bitmask"
+
+
 def _pack_topk_idx_dtype(dtype, inter: int):
     """Index dtype check of _pack_topk_idx (moc/ffn.py:27-41) with the static
     bound max_allowed_idx = inter - 1 the reference always passes."""
     if dtype is None:
         return torch.int64
+    if isinstance(dtype, str) and dtype == INDEX_SAVE_BITMASK:
+        return torch.int16 if inter - 1 <= torch.iinfo(torch.int16).max else torch.int32
     info = torch.iinfo(dtype)
     if inter - 1 > info.max:
         raise ValueError(f"topk_idx range [0, {inter - 1}] cannot be stored as {dtype}")
@@ -69,7 +78,7 @@ class StandardSwiGLUFFN(nn.Module):
 
 
 def _check_inputs(x, gate_w, up_w, down_w, strict_aux: bool, index_save_dtype):
-    if strict_aux and index_save_dtype != torch.int16:
+    if strict_aux and not (index_save_dtype == torch.int16 or index_save_dtype == INDEX_SAVE_BITMASK):
         raise ValueError("MoC fused helper kernels require compact saved indices.")
     for t in (x, gate_w, up_w, down_w):
         if not t.is_cuda:
@@ -120,7 +129,8 @@ def _side_for(device, rows: int, inter: int):
     return None
 
 
-def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool):
+def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool,
+                    want_mask: bool = False):
     """Shared MoC forward: G -> select -> U -> sparse aux -> D.
 
     Follows _MoCFunction.forward (moc/ffn.py:130-173) and the variants at
@@ -146,11 +156,14 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
 
     _on_side(side, (x2, up_w, u, down_w, wd), side_work)
     K.linear(x2, gate_w, out=g)
+    mask = None
     if selection == "topk":
-        vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype)
+        vals, idx, mask = K.topk_rows(g, k, idx_dtype=idx_dtype, want_mask=want_mask)
     elif selection == "post_silu_abs":
-        vals, idx, _ = K.topk_rows(g, k, idx_dtype=idx_dtype, score_transform=1)
+        vals, idx, mask = K.topk_rows(g, k, idx_dtype=idx_dtype, score_transform=1, want_mask=want_mask)
     elif selection == "2of8":
+        if want_mask:
+            raise ValueError("the bit-mask index format is for Top-K selections, not MoC 2:8")
         vals, idx = K.select_2of8(g, idx_dtype=idx_dtype)
     else:
         raise ValueError(selection)
@@ -163,9 +176,27 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     del z_full
     kk = idx.shape[-1]
     shp = (*x.shape[:-1], kk)
-    return (out.reshape(*x.shape[:-1], down_w.shape[0]), idx.reshape(shp), vals.reshape(shp),
-            u_s.reshape(shp), None if s_s is None else s_s.reshape(shp),
-            None if z_s is None else z_s.reshape(shp), wd)
+    res = (out.reshape(*x.shape[:-1], down_w.shape[0]), idx.reshape(shp), vals.reshape(shp),
+           u_s.reshape(shp), None if s_s is None else s_s.reshape(shp),
+           None if z_s is None else z_s.reshape(shp), wd)
+    if not want_mask:
+        return res
+    return res + (mask.reshape(*x.shape[:-1], mask.shape[-1]),)
+
+
+def _saved_index(idx, mask, bitmask: bool):
+    """What the forward saves for the selection: the indices, or the mask."""
+    return mask if bitmask else idx
+
+
+def _restore_index(ctx, saved):
+    """The backward's indices: the saved ones, or the saved mask expanded."""
+    if not ctx.bitmask:
+        return saved
+    rows_shape = saved.shape[:-1]
+    idx = K.mask_to_idx(saved.reshape(-1, saved.shape[-1]), ctx.inter, ctx.k,
+                        idx_dtype=_pack_topk_idx_dtype(INDEX_SAVE_BITMASK, ctx.inter))
+    return idx.reshape(*rows_shape, ctx.k)
 
 
 def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool):
@@ -226,16 +257,20 @@ class _MoCFunction(torch.autograd.Function):
         _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
         inter = gate_w.shape[0]
         idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        out, idx, vals, u_s, s_s, z_s, wd = _forward_common(
-            x, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=True)
-        ctx.save_for_backward(x, idx, vals, u_s, s_s, z_s, gate_w, up_w, wd)
+        bitmask = index_save_dtype == INDEX_SAVE_BITMASK
+        out, idx, vals, u_s, s_s, z_s, wd, *mask = _forward_common(
+            x, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=True, want_mask=bitmask)
+        ctx.save_for_backward(x, _saved_index(idx, mask[0] if mask else None, bitmask), vals, u_s,
+                              s_s, z_s, gate_w, up_w, wd)
         ctx.k = idx.shape[-1]
         ctx.inter = inter
+        ctx.bitmask = bitmask
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w = ctx.saved_tensors
+        x, saved, g_s, u_s, s_s, z_s, gate_w, up_w, down_w = ctx.saved_tensors
+        idx = _restore_index(ctx, saved)
         dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w,
                                              down_w, gcp=False)
         return dx, dwg, dwu, dwd, None, None, None
@@ -274,16 +309,20 @@ class _MoCGCPFunction(torch.autograd.Function):
         _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
         inter = gate_w.shape[0]
         idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        out, idx, vals, u_s, _, _, wd = _forward_common(
-            x, gate_w, up_w, down_w, k, "topk", idx_dtype, save_s=False)
-        ctx.save_for_backward(x, idx, vals, u_s, gate_w, up_w, wd)
+        bitmask = index_save_dtype == INDEX_SAVE_BITMASK
+        out, idx, vals, u_s, _, _, wd, *mask = _forward_common(
+            x, gate_w, up_w, down_w, k, "topk", idx_dtype, save_s=False, want_mask=bitmask)
+        ctx.save_for_backward(x, _saved_index(idx, mask[0] if mask else None, bitmask), vals, u_s,
+                              gate_w, up_w, wd)
         ctx.k = k
         ctx.inter = inter
+        ctx.bitmask = bitmask
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        x, idx, g_s, u_s, gate_w, up_w, down_w = ctx.saved_tensors
+        x, saved, g_s, u_s, gate_w, up_w, down_w = ctx.saved_tensors
+        idx = _restore_index(ctx, saved)
         dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, None, None, gate_w,
                                              up_w, down_w, gcp=True)
         return dx, dwg, dwu, dwd, None, None, None

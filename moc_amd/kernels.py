@@ -111,6 +111,20 @@ def topk_rows(scores: torch.Tensor, k: int, *, idx_dtype=torch.int64, want_vals:
     return vals, idx, mask
 
 
+def mask_to_idx(mask: torch.Tensor, inter: int, k: int, *, idx_dtype=torch.int16) -> torch.Tensor:
+    """[rows, ceil(inter/32)] int32 selection mask -> [rows, k] channel
+    indices in ascending order (the first k set bits of each row)."""
+    N.require_device(mask)
+    m, ld = _rows_view(mask)
+    if m.dtype != torch.int32:
+        raise ValueError("mask must be int32 words")
+    rows = m.shape[0]
+    idx = _empty((rows, k), idx_dtype, m.device)
+    N.call("moc_mask_to_idx", m.data_ptr(), rows, int(inter), ld, int(k), idx.data_ptr(),
+           N.idx_code(idx_dtype), N.stream_of(m))
+    return idx
+
+
 def moc28_effective_k(inter: int) -> int:
     full, tail = divmod(int(inter), 8)
     return full * 2 + min(2, tail)

@@ -171,6 +171,54 @@ def test_gcp_saved_activation_bytes_config2():
     assert torch.isfinite(x.grad.float()).all()
 
 
+@pytest.mark.parametrize("mode", ["moc_gcp", "moc"])
+def test_bitmask_saved_selection(mode):
+    """index_save_dtype=INDEX_SAVE_BITMASK saves the selection as ceil(I/32)
+    int32 words per token (config 2: 256 B instead of 768 B of int16 idx)
+    and gives the int16 path's outputs and gradients bit for bit (the
+    backward expands the mask to the same indices)."""
+    from moc_amd.ffn import INDEX_SAVE_BITMASK, MoCSwiGLUFFN
+    t, d, inter, k = 8 * 1024, 768, 2048, 384
+    ref = MoCSwiGLUFFN(d, inter, k, mode=mode, index_save_dtype=torch.int16).to(DEV, torch.bfloat16)
+    bm = MoCSwiGLUFFN(d, inter, k, mode=mode, index_save_dtype=INDEX_SAVE_BITMASK).to(DEV, torch.bfloat16)
+    bm.load_state_dict(ref.state_dict())
+    g = torch.Generator(device=DEV).manual_seed(21)
+    x0 = torch.randn(8, 1024, d, device=DEV, generator=g).to(torch.bfloat16)
+    go = torch.randn(8, 1024, d, device=DEV, generator=g).to(torch.bfloat16)
+    res = []
+    for m in (ref, bm):
+        x = x0.clone().requires_grad_(True)
+        saved = []
+
+        def pack(tns):
+            saved.append(tns)
+            return tns
+
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda z: z):
+            out = m(x)
+        sel = [s for s in saved if s.dtype in (torch.int16, torch.int32)]
+        assert len(sel) == 1
+        out.backward(go)
+        res.append((out, x.grad, m.gate_proj.weight.grad, m.up_proj.weight.grad,
+                    m.down_proj.weight.grad, sel[0]))
+    assert res[0][5].dtype == torch.int16 and res[0][5].numel() * 2 == t * k * 2
+    assert res[1][5].dtype == torch.int32 and res[1][5].numel() * 4 == t * (inter // 32) * 4
+    for a, b in zip(res[0][:5], res[1][:5]):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("inter,k", [(5461, 1024), (2048, 384), (10000, 3000), (96, 96)])
+def test_mask_to_idx_matches_topk(inter, k):
+    """moc_mask_to_idx of a Top-K mask gives the Top-K indices (ties and
+    all; int16, int32, int64)."""
+    from moc_amd import kernels as K
+    g = torch.Generator(device=DEV).manual_seed(inter)
+    s = (torch.randn(300, inter, device=DEV, generator=g) * 4).round().to(torch.bfloat16)  # many ties
+    for dt in ((torch.int16,) if inter <= 32768 else ()) + (torch.int32, torch.int64):
+        _, idx, mask = K.topk_rows(s, k, idx_dtype=dt, want_mask=True)
+        assert torch.equal(K.mask_to_idx(mask, inter, k, idx_dtype=dt), idx)
+
+
 # ---------------------------------------------------------------- inference
 @pytest.mark.parametrize("nb", [1, 4, 16])
 def test_inference_global_modes(nb):
