@@ -12,8 +12,8 @@ each step as the reference harness does (:55-57).
 
 The same line carries:
   roofline      the MFMA GEMM engine (the dominant kernel of the step):
-                algorithmic FLOP of the nine FFN GEMMs (8 launches, the dX
-                launch fuses two products) / their summed HIP-event time,
+                algorithmic FLOP of the nine FFN GEMMs (7 launches: G and U
+                share one, dX sums two products) / their summed HIP-event time,
                 against the 2.5 PFLOP/s dense bf16 peak;
   roofline_decode  global-MoC decode (config 3, B=1): union-of-selected-rows
                 bytes / layer time against 8 TB/s, cold weights (rotation
@@ -72,7 +72,7 @@ def parse_args():
                    help="only end-to-end greedy decode of a 24-layer 1b-shape decoder (dense, "
                         "global MoC, MoC 2:8; eager and whole-step graph): ms/token, one JSON line")
     p.add_argument("--roofline-only", action="store_true",
-                   help="only the eight GEMM launches of the roofline (for rocprofv3 kernel "
+                   help="only the seven GEMM launches of the roofline (for rocprofv3 kernel "
                         "traces whose per-kernel averages match roofline.per_launch)")
     p.add_argument("--pmc-target", choices=["gemm", "copy", "decode"], default=None,
                    help="only launch one workload a few times (for rocprofv3 --pmc runs): the G "
@@ -135,9 +135,12 @@ def pmc_target(which: str) -> None:
     if which == "gemm":
         x, wg, _, _, _ = seeded_inputs(BATCH1B * SEQ1B, D1B, I1B)
         x, wg = x.cuda(), wg.cuda()
+        wu = (torch.randn(I1B, D1B, generator=torch.Generator().manual_seed(5)) * 0.02)
+        wu = wu.to(torch.bfloat16).cuda()
         g = K.padded_empty(x.shape[0], I1B, torch.bfloat16, x.device)
+        u = K.padded_empty(x.shape[0], I1B, torch.bfloat16, x.device)
         for _ in range(5):
-            K.linear(x, wg, out=g)
+            K.linear_pair(x, wg, wu, out1=g, out2=u)
     elif which == "decode":
         gen = torch.Generator(device="cuda").manual_seed(1234)
         layers = []
@@ -236,7 +239,7 @@ DECODE_B1_TRAFFIC_BYTES = 22.48e6 + 9.33e6
 
 
 def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
-    """HIP-event time of the eight GEMM launches of one MoC FFN fwd+bwd step at
+    """HIP-event time of the seven GEMM launches of one MoC FFN fwd+bwd step at
     the layer's real shapes (the kernels and operand layouts the layer uses)."""
     import torch
     from moc_amd import kernels as K
@@ -258,8 +261,7 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
     wg_a, wu_a = K.aligned_rows(wg), K.aligned_rows(wu)
     unit = 2.0 * t * d * inter
     launches = [
-        ("G = X Wg^T", lambda: K.linear(x2, wg, out=g), 1),
-        ("U = X Wu^T", lambda: K.linear(x2, wu, out=u), 1),
+        ("G, U = X Wg^T, X Wu^T (one launch)", lambda: K.linear_pair(x2, wg, wu, out1=g, out2=u), 2),
         ("D = Z Wd^T", lambda: K.gemm(z_full, wd_a.t()), 1),
         ("dWd = dD^T Z", lambda: K.gemm(go2.t(), z_full), 1),
         ("gZ = dD Wd", lambda: K.gemm(go2, wd_a, out=gz), 1),
@@ -271,17 +273,20 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
         for _, fn, _ in launches:
             fn()
     torch.cuda.synchronize()
+    # interleaved: rep r times every launch once, so no launch is always the
+    # first after a switch of workload (that one runs several % slower)
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(reps)] for _ in launches]
+    for r in range(reps):
+        for (_, fn, _), ev in zip(launches, evs):
+            ev[r][0].record()
+            fn()
+            ev[r][1].record()
+    torch.cuda.synchronize()
     per = []
     tot_ms, tot_flop = 0.0, 0.0
-    for name, fn, mult in launches:
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(reps)]
-        for a, b in evs:
-            a.record()
-            fn()
-            b.record()
-        torch.cuda.synchronize()
-        ms = statistics.median(a.elapsed_time(b) for a, b in evs)
+    for (name, fn, mult), ev in zip(launches, evs):
+        ms = statistics.median(a.elapsed_time(b) for a, b in ev)
         flop = unit * mult
         tot_ms += ms
         tot_flop += flop
@@ -294,7 +299,7 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
         "traffic": GEMM_G_TRAFFIC_BYTES if (t, d, inter) == (BATCH1B * SEQ1B, D1B, I1B) else None,
         "traffic_note": "bytes per G launch (L2 misses to MALL/HBM; counter runs scaled by a copy "
                         "kernel, profiles/gemm_G_traffic.md)",
-        "kernel": "gemm_pp_kernel (v_mfma_f32_32x32x16_bf16), 8 launches/step",
+        "kernel": "gemm_pp_kernel (v_mfma_f32_32x32x16_bf16), 7 launches/step",
         "algorithmic_flop_per_step": tot_flop, "gemm_ms_per_step": round(tot_ms, 4),
         "per_launch": per,
     }

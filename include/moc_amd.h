@@ -177,6 +177,17 @@ int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64
                 void* C, int64_t ldc, int c_dtype, void* workspace, int64_t workspace_bytes,
                 void* stream);
 
+/* C1[M,N1] = A W1^T and C2[M,N2] = A W2^T (bf16) in one launch: A [M,K]
+ * row-major (lda), W1 [N1,K] and W2 [N2,K] nn.Linear weights (ldw1, ldw2),
+ * C1/C2 row-major (ldc1, ldc2).  The gate and up projections of the MoC FFN
+ * input, G = x W_gate^T and U = x W_up^T (moc/ffn.py:141,146 for `moc`,
+ * :389,394 for `moc_gcp`), which the reference runs as two library GEMMs.
+ * Results equal two moc_gemm_ws calls bit for bit; pairs too small to fill
+ * the CUs run as exactly those two calls (with the given workspace). */
+int moc_gemm_pair(int64_t M, int64_t K, const void* A, int64_t lda, const void* W1, int64_t ldw1,
+                  int64_t N1, void* C1, int64_t ldc1, const void* W2, int64_t ldw2, int64_t N2,
+                  void* C2, int64_t ldc2, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes moc_gemm_ws uses for this shape on the current device (0:
  * the product does not split; otherwise 4 KB of counters plus the f32
  * partial tiles).  No counterpart in the reference (its GEMMs

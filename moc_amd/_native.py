@@ -59,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "moc_gemm_ws": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                            _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp]),
     "moc_gemm_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64]),
+    "moc_gemm_pair": (_int, [_i64, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
+                             _vp, _i64, _vp, _i64, _vp]),
     "moc_gemv_bf16": (_int, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "moc_gemv_rmsnorm_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _i64, _vp, _i64, _i64,
                                      _i64, _vp, _i64, _vp]),

@@ -106,6 +106,13 @@ struct GemmArgs {
   int64_t* gu_idx;
   uint16_t* gu_sz;
   int gu_inter;
+  // Column-concatenated pair (512-thread kernel, ncat_tn > 0, single
+  // product, no split): tile columns [0, ncat_tn) compute C = A b[0], tile
+  // columns ncat_tn.. compute C2 = A b[1] (extent N2, row pitch ldc2), so two
+  // products that share A fill the CUs as one launch.
+  int ncat_tn, N2, vec_store2;
+  void* C2;
+  int64_t ldc2;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -771,6 +778,15 @@ void gemm_pp_kernel(GemmArgs g) {
   }
   int tm, tn;
   tile_coords(tbid, g.tiles_m, g.tiles_n, tm, tn);
+  const int tn_all = tn;  // column of the concatenated tile grid (L2 prefetch slices)
+  if (!GU && !DUAL && !SPLIT && g.ncat_tn > 0 && tn >= g.ncat_tn) {
+    tn -= g.ncat_tn;
+    g.b[0] = g.b[1];
+    g.C = g.C2;
+    g.N = g.N2;
+    g.ldc = g.ldc2;
+    g.vec_store = g.vec_store2;
+  }
   const int row0 = tm * kBM;
   const int col0 = GU ? tn * 128 : tn * kBN;  // GU: channel base of the gate and up halves
   const int wm = (sw >> 1) * 128;
@@ -919,7 +935,7 @@ void gemm_pp_kernel(GemmArgs g) {
       const int k0 = (p1 ? t - nk0 : t) * kBK;
       if (sw == 0) {
         const Operand& o = p1 ? g.a[1] : g.a[0];
-        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, k0, row0, sink, lane, tn & 7, 8);
+        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, k0, row0, sink, lane, tn_all & 7, 8);
       } else if (sw == 1) {
         const Operand& o = p1 ? g.b[1] : g.b[0];
         if (GU && (tm & 3) >= 2)  // quarters 2-3 of the B tile are W_up rows
@@ -1238,6 +1254,66 @@ extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int6
   if (dtype != MOC_BF16 || M <= 0 || N <= 0 || K < 0 || K2 < 0) return 0;
   const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
   return std::max(plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes);
+}
+
+// Two products of one A in one launch: C1 = A W1^T, C2 = A W2^T (the gate
+// and up projections of the FFN input).  The tile grid is the two products'
+// grids side by side (gemm_pp_kernel's ncat_tn), so a pair whose grids each
+// end in a partial round of the CUs runs as one launch with fewer partial
+// rounds.  Pairs whose tiles do not fill the CUs, or whose operands the
+// 512-thread kernel cannot address, run as two moc_gemm_ws calls.
+extern "C" int moc_gemm_pair(int64_t M, int64_t K, const void* A, int64_t lda, const void* W1,
+                             int64_t ldw1, int64_t N1, void* C1, int64_t ldc1, const void* W2,
+                             int64_t ldw2, int64_t N2, void* C2, int64_t ldc2, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(M >= 0 && K >= 0 && N1 >= 0 && N2 >= 0, "moc_gemm_pair: negative extent");
+  MOC_REQUIRE(M < (1LL << 31) && K < (1LL << 31) && N1 < (1LL << 31) && N2 < (1LL << 31),
+              "moc_gemm_pair: extent too large");
+  MOC_REQUIRE(ldc1 >= N1 && ldc2 >= N2, "moc_gemm_pair: ldc < N");
+  if (M == 0) return MOC_OK;
+  const int64_t tm = (M + kBM - 1) / kBM, tn1 = (N1 + kBN - 1) / kBN, tn2 = (N2 + kBN - 1) / kBN;
+  GemmArgs a{};
+  bool pair = K > 0 && N1 > 0 && N2 > 0 && tm * (tn1 + tn2) >= cu_count() &&
+              tm * (tn1 + tn2) < (1LL << 31) && C1 != nullptr && C2 != nullptr && A != nullptr &&
+              W1 != nullptr && W2 != nullptr && aligned16(A) && aligned16(W1) && aligned16(W2) &&
+              lda % 8 == 0 && ldw1 % 8 == 0 && ldw2 % 8 == 0 && lda >= K && ldw1 >= K && ldw2 >= K;
+  if (pair) {
+    pair = make_operand(A, lda, true, M, K, a.a[0]) && make_operand(W1, ldw1, true, N1, K, a.b[0]) &&
+           make_operand(W2, ldw2, true, N2, K, a.b[1]);
+    auto no_wrap = [](const Operand& o) {
+      return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
+    };
+    pair = pair && no_wrap(a.a[0]) && no_wrap(a.b[0]) && no_wrap(a.b[1]);
+  }
+  if (!pair) {
+    int rc = moc_gemm_ws(MOC_BF16, M, N1, K, A, lda, 1, W1, 1, ldw1, 0, nullptr, 0, 0, nullptr, 0, 0,
+                         C1, ldc1, MOC_BF16, workspace, workspace_bytes, stream);
+    if (rc == MOC_OK)
+      rc = moc_gemm_ws(MOC_BF16, M, N2, K, A, lda, 1, W2, 1, ldw2, 0, nullptr, 0, 0, nullptr, 0, 0,
+                       C2, ldc2, MOC_BF16, workspace, workspace_bytes, stream);
+    return rc;
+  }
+  a.a[1] = a.a[0];
+  a.nk[0] = static_cast<int>((K + kBK - 1) / kBK);
+  a.nk[1] = 0;
+  a.M = static_cast<int>(M);
+  a.N = static_cast<int>(N1);
+  a.C = C1;
+  a.ldc = ldc1;
+  a.vec_store = (reinterpret_cast<uintptr_t>(C1) % 16 == 0 && (ldc1 * 2) % 16 == 0) ? 1 : 0;
+  a.tiles_m = static_cast<int>(tm);
+  a.tiles_n = static_cast<int>(tn1 + tn2);
+  a.pp = 1;
+  a.ksplit = 1;
+  a.kper = a.nk[0];
+  a.ncat_tn = static_cast<int>(tn1);
+  a.N2 = static_cast<int>(N2);
+  a.C2 = C2;
+  a.ldc2 = ldc2;
+  a.vec_store2 = (reinterpret_cast<uintptr_t>(C2) % 16 == 0 && (ldc2 * 2) % 16 == 0) ? 1 : 0;
+  const dim3 grid(static_cast<unsigned>(tm * (tn1 + tn2)));
+  gemm_pp_kernel<true, true, false, false, false><<<grid, dim3(kPpThreads), 0, as_stream(stream)>>>(a);
+  return check_launch("gemm_pp_kernel (pair)");
 }
 
 extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,

@@ -139,23 +139,27 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     inter = gate_w.shape[0]
     x2 = K.aligned_rows(x.reshape(-1, d))
     rows = x2.shape[0]
-    # U = x Wu^T runs on the side stream (for multi-round GEMMs), launched
-    # before G so that the two GEMMs share the CUs (each alone leaves its last
-    # round half empty) and U also overlaps the selection over G; the
-    # 16-byte-row copy of W_down (when its rows need one), which the backward
-    # reuses, follows U there
+    # bf16: G = x Wg^T and U = x Wu^T as one MFMA launch (their tile grids
+    # side by side: two products that each end in a half-empty round of the
+    # CUs share it); the 16-byte-row copy of W_down (when its rows need one),
+    # which the backward reuses, then runs on the side stream beside the
+    # selection.  f32: U on the side stream beside G and the selection.
     side = _side_for(x.device, rows, inter)
     g = K.padded_empty(rows, inter, x.dtype, x.device)
     u = K.padded_empty(rows, inter, x.dtype, x.device)
     wd = (K.padded_empty(down_w.shape[0], down_w.shape[1], down_w.dtype, x.device)
           if K.needs_alignment(down_w) else down_w)
+    if x.dtype == torch.bfloat16:
+        K.linear_pair(x2, gate_w, up_w, out1=g, out2=u)
+        if wd is not down_w:
+            _on_side(side, (down_w, wd), lambda: K.aligned_rows(down_w, out=wd))
+    else:
+        def side_work():
+            K.linear(x2, up_w, out=u)
+            K.aligned_rows(down_w, out=wd)
 
-    def side_work():
-        K.linear(x2, up_w, out=u)
-        K.aligned_rows(down_w, out=wd)
-
-    _on_side(side, (x2, up_w, u, down_w, wd), side_work)
-    K.linear(x2, gate_w, out=g)
+        _on_side(side, (x2, up_w, u, down_w, wd), side_work)
+        K.linear(x2, gate_w, out=g)
     mask = None
     if selection == "topk":
         vals, idx, mask = K.topk_rows(g, k, idx_dtype=idx_dtype, want_mask=want_mask)

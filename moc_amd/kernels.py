@@ -343,6 +343,43 @@ def linear(x2d: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None 
     return gemm(x2d, weight.t(), out=out, out_dtype=out_dtype)
 
 
+def linear_pair(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, *,
+                out1: torch.Tensor | None = None,
+                out2: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(x2d @ w1.T, x2d @ w2.T) for two nn.Linear weights of one input, bf16,
+    in one MFMA launch when the pair fills the CUs (moc_gemm_pair)."""
+    N.require_device(x2d, w1, w2, out1, out2)
+    if not (x2d.dtype == w1.dtype == w2.dtype == torch.bfloat16):
+        raise ValueError("linear_pair takes bf16 operands")
+    M, Kd = x2d.shape
+    if w1.shape[1] != Kd or w2.shape[1] != Kd:
+        raise ValueError(f"linear_pair shape mismatch {tuple(x2d.shape)} x {tuple(w1.shape)}, "
+                         f"{tuple(w2.shape)}")
+    n1, n2 = w1.shape[0], w2.shape[0]
+    xa, wa, wb = aligned_rows(x2d), aligned_rows(w1), aligned_rows(w2)
+    outs = []
+    for o, n in ((out1, n1), (out2, n2)):
+        if o is None:
+            o = _empty((M, n), torch.bfloat16, x2d.device)
+        if o.shape != (M, n) or (o.stride(1) != 1 and n > 1) or o.dtype != torch.bfloat16:
+            raise ValueError("linear_pair outputs must be bf16 [M, N] with unit column stride")
+        outs.append(o)
+    lda = xa.stride(0) if M > 1 else round_up(max(Kd, 1), 8)
+    ld1 = wa.stride(0) if n1 > 1 else round_up(max(Kd, 1), 8)
+    ld2 = wb.stride(0) if n2 > 1 else round_up(max(Kd, 1), 8)
+    ldc = [o.stride(0) if M > 1 else max(o.shape[1], 1) for o in outs]
+    ws_bytes = 0
+    for n in (n1, n2):
+        if gemm_tiles(M, n) < cu_count(x2d.get_device()):
+            ws_bytes = max(ws_bytes, N.query("moc_gemm_workspace_size", N.dtype_code(torch.bfloat16),
+                                             M, n, Kd, 0))
+    ws = _gemm_workspace(x2d.device, ws_bytes) if ws_bytes > 0 else None
+    N.call("moc_gemm_pair", M, Kd, xa.data_ptr(), lda, wa.data_ptr(), ld1, n1, outs[0].data_ptr(),
+           ldc[0], wb.data_ptr(), ld2, n2, outs[1].data_ptr(), ldc[1], N.ptr(ws), ws_bytes,
+           N.stream_of(x2d))
+    return outs[0], outs[1]
+
+
 # -------------------------------------------------------------------- decode
 def gemv(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None) -> torch.Tensor:
     """[nb <= 16, hidden] @ weight[rows, hidden].T -> [nb, rows] (bf16)."""

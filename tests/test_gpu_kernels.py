@@ -155,6 +155,36 @@ def test_gemm_split_k_dual():
     close(out, ref, rtol=1e-4, atol=1e-3)
 
 
+@pytest.mark.parametrize("mkn", [
+    (16384, 2048, 5461, 5461),   # 1b gate/up: 1408 + 1408 tiles, one launch
+    (8192, 768, 2048, 2048),     # 130m: 256 + 256 tiles, one launch
+    (1000, 200, 1300, 700),      # ragged: 4 x (6 + 3) tiles -> two moc_gemm_ws calls
+    (300, 64, 50, 90),           # one tile each, split-K plans
+])
+def test_gemm_pair_equals_two_launches(mkn):
+    """moc_gemm_pair (G = x Wg^T and U = x Wu^T with the two tile grids side
+    by side in one launch) equals the two single-product launches bit for bit,
+    leaves the pad columns of padded outputs alone, and matches fp32."""
+    M, Kd, n1, n2 = mkn
+    g = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(M, Kd, device=DEV, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(n1, Kd, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(n2, Kd, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    o1 = K().padded_empty(M, n1, torch.bfloat16, DEV)
+    o2 = K().padded_empty(M, n2, torch.bfloat16, DEV)
+    for o in (o1, o2):
+        o.as_strided((M, o.stride(0)), (o.stride(0), 1)).fill_(7.0)
+    K().linear_pair(x, w1, w2, out1=o1, out2=o2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, K().linear(x, w1)) and torch.equal(o2, K().linear(x, w2))
+    for o, n in ((o1, n1), (o2, n2)):
+        pad = o.as_strided((M, o.stride(0)), (o.stride(0), 1))[:, n:]
+        assert pad.numel() == 0 or bool((pad == 7.0).all())
+    sub = slice(0, min(M, 512))
+    bf16_close(o1[sub], x[sub].float() @ w1.float().t(), ulps=1, atol=1e-3)
+    bf16_close(o2[sub], x[sub].float() @ w2.float().t(), ulps=1, atol=1e-3)
+
+
 def _unsplit(ad, bd, M, Nn, Kk, a2=None, b2=None, K2=0):
     """The GEMM without a workspace (moc_gemm: whole tiles only), f32 out."""
     flat = torch.empty(M, Nn, device=DEV, dtype=torch.float32)
