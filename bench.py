@@ -228,11 +228,11 @@ def time_train_layer(m, x, go, steps, warmup):
     return wall * 1e3 / steps, summarize(fwd), summarize(bwd)
 
 
-# L2-miss (MALL/HBM side) bytes of one G launch at the 1b shape, from the
-# FETCH_SIZE / WRITE_SIZE counter runs in profiles/gemm_G_traffic.md, each
+# L2-miss (MALL/HBM side) bytes of one G,U pair launch at the 1b shape, from the
+# FETCH_SIZE / WRITE_SIZE counter runs in profiles/gemm_GU_pair_traffic.md, each
 # scaled by what the counter reads for a copy kernel of known size
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).
-GEMM_G_TRAFFIC_BYTES = 593.6e6 + 179.3e6
+GEMM_GU_TRAFFIC_BYTES = 1133.3e6 + 358.6e6
 # the same for the B=1 decode layer (gate GEMV + fused select/up/down),
 # profiles/decode_B1_traffic.md
 DECODE_B1_TRAFFIC_BYTES = 22.48e6 + 9.33e6
@@ -273,19 +273,20 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
         for _, fn, _ in launches:
             fn()
     torch.cuda.synchronize()
-    # interleaved: rep r times every launch once, so no launch is always the
-    # first after a switch of workload (that one runs several % slower)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(reps)] for _ in launches]
-    for r in range(reps):
-        for (_, fn, _), ev in zip(launches, evs):
-            ev[r][0].record()
-            fn()
-            ev[r][1].record()
-    torch.cuda.synchronize()
     per = []
     tot_ms, tot_flop = 0.0, 0.0
-    for (name, fn, mult), ev in zip(launches, evs):
+    for name, fn, mult in launches:
+        # two untimed launches first: the first launch after a switch of
+        # workload runs several % slower than the steady state
+        fn()
+        fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
         ms = statistics.median(a.elapsed_time(b) for a, b in ev)
         flop = unit * mult
         tot_ms += ms
@@ -296,9 +297,9 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
     return {
         "bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-        "traffic": GEMM_G_TRAFFIC_BYTES if (t, d, inter) == (BATCH1B * SEQ1B, D1B, I1B) else None,
-        "traffic_note": "bytes per G launch (L2 misses to MALL/HBM; counter runs scaled by a copy "
-                        "kernel, profiles/gemm_G_traffic.md)",
+        "traffic": GEMM_GU_TRAFFIC_BYTES if (t, d, inter) == (BATCH1B * SEQ1B, D1B, I1B) else None,
+        "traffic_note": "bytes per G,U pair launch (L2 misses to MALL/HBM; counter runs scaled by a "
+                        "copy kernel, profiles/gemm_GU_pair_traffic.md)",
         "kernel": "gemm_pp_kernel (v_mfma_f32_32x32x16_bf16), 7 launches/step",
         "algorithmic_flop_per_step": tot_flop, "gemm_ms_per_step": round(tot_ms, 4),
         "per_launch": per,
