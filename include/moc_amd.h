@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define MOC_ABI_VERSION 1
+#define MOC_ABI_VERSION 2
 
 /* status codes */
 #define MOC_OK 0
@@ -239,13 +239,17 @@ int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t 
  * Up * SiLU, selected Down -> y[nb, hidden], in one kernel launch
  * (moc_native::optimized_global_after_gate_bf16, optimized_global_moc_ext.cu:
  * 457-540, optimized_global_moc_ext.cpp:61-76,92).
+ * idx_out, if not NULL, receives the selection the kernel made: int32
+ * [nb, k], ascending channel order (the reference keeps its int32 indices
+ * internal, optimized_global_moc_ext.cu:468-483).
  * The workspace starts with 64 KB of arrival counters that must be zero
  * before the first call with that workspace (e.g. hipMemset once after
  * allocation); every call, of any shape, leaves them zero again.  Calls
  * sharing a workspace must not overlap. */
 int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
                                int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
-                               void* y, void* workspace, int64_t workspace_bytes, void* stream);
+                               void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
+                               void* stream);
 
 /* moc_global_after_gate_bf16 with the layer's residual added in its last
  * step: y = bf16(residual + bf16(FFN)), the decoder's x + ffn(norm(x))
@@ -253,8 +257,8 @@ int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t n
 int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
                                         int64_t inter, int64_t hidden, const void* w_up,
                                         const void* w_down_t, int64_t k, const void* residual,
-                                        void* y, void* workspace, int64_t workspace_bytes,
-                                        void* stream);
+                                        void* y, void* idx_out, void* workspace,
+                                        int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------- 2:8 */
 /* Fused gate+up projection with top-2-of-8 selection for nb tokens:

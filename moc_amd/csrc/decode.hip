@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
     int k, int P, int CB, const uint16_t* __restrict__ w_up, int64_t up_ld, const uint16_t* __restrict__ wdt,
     float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ res) {
+    const uint16_t* __restrict__ res, int* __restrict__ idx_out) {
   constexpr int QN = CW / 8;            // 16-byte chunks per row segment
   constexpr int S = kUdThreads / QN;    // row segments summed in parallel
   static_assert(S * QN == kUdThreads, "CW / 8 must divide the workgroup");
@@ -386,6 +386,8 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
       if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) {
         sch[pos - lo] = c;
         sv[pos - lo] = round_bf16(silu_f32(bf16_to_f32(raw[c])));
+        // the selection itself, written once per token (column block 0)
+        if (idx_out != nullptr && cb == 0) idx_out[static_cast<int64_t>(b) * k + pos] = c;
       }
     });
   }
@@ -701,14 +703,15 @@ inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
 template <int CW>
 void launch_fused(const void* x, int hidden, const void* gate, int inter, int k, int nb,
                   const FusedShape& f, const void* w_up, int64_t up_ld, const void* wdt, float* part,
-                  int* cnt, void* y, const void* res, hipStream_t st) {
+                  int* cnt, void* y, const void* res, int* idx_out, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
   const int per = (inter + kUdThreads - 1) / kUdThreads;
 #define MOC_FU(N)                                                                               \
   select_up_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)x, hidden,               \
                                                        (const uint16_t*)gate, inter, k, f.P, f.CB, \
                                                        (const uint16_t*)w_up, up_ld, (const uint16_t*)wdt, \
-                                                       part, cnt, (uint16_t*)y, (const uint16_t*)res)
+                                                       part, cnt, (uint16_t*)y, (const uint16_t*)res, \
+                                                       idx_out)
   if (per <= 8) MOC_FU(8);
   else if (per <= 16) MOC_FU(16);
   else if (per <= 24) MOC_FU(24);
@@ -851,7 +854,7 @@ extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dt
 // Workspace: a fixed 64 KB block of arrival counters (so the counters of one
 // call shape never overlap other data of another shape that reuses the
 // workspace), then the partial sums.
-constexpr int64_t kFusedCounterBytes = 64 * 1024;
+constexpr int64_t kFusedCounterBytes = kAfterGateCounterBytes;
 
 // From this many tokens on, U = x W_up^T is computed densely for all
 // channels by the gate GEMV kernel before the after-gate kernel: the union of
@@ -874,10 +877,9 @@ extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inte
 }
 
 namespace moc {
-namespace {
 int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter, int64_t hidden,
                       const void* w_up, const void* w_down_t, int64_t k, const void* res, void* y,
-                      void* workspace, int64_t workspace_bytes, void* stream) {
+                      void* idx_out, void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64, "moc_global_after_gate_bf16: bad shape");
   MOC_REQUIRE(hidden % 64 == 0, "moc_global_after_gate_bf16: hidden must be a multiple of 64");
@@ -904,32 +906,32 @@ int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_
     up = u;
     up_ld = inter;
   }
+  int* io = static_cast<int*>(idx_out);
   if (f.CW == 256)
     launch_fused<256>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, up, up_ld, w_down_t,
-                      part, cnt, y, res, st);
+                      part, cnt, y, res, io, st);
   else
     launch_fused<64>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, up, up_ld, w_down_t,
-                     part, cnt, y, res, st);
+                     part, cnt, y, res, io, st);
   return check_launch("select_up_down_kernel");
 }
-}  // namespace
 }  // namespace moc
 
 extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
                                           int64_t inter, int64_t hidden, const void* w_up,
-                                          const void* w_down_t, int64_t k, void* y,
-                                          void* workspace, int64_t workspace_bytes,
-                                          void* stream) {
-  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, workspace,
-                           workspace_bytes, stream);
+                                          const void* w_down_t, int64_t k, void* y, void* idx_out,
+                                          void* workspace, int64_t workspace_bytes, void* stream) {
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out,
+                           workspace, workspace_bytes, stream);
 }
 
 extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
                                                    int64_t inter, int64_t hidden, const void* w_up,
                                                    const void* w_down_t, int64_t k, const void* residual,
-                                                   void* y, void* workspace, int64_t workspace_bytes,
-                                                   void* stream) {
+                                                   void* y, void* idx_out, void* workspace,
+                                                   int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb == 0 || residual != nullptr, "moc_global_after_gate_residual_bf16: null residual");
-  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, residual, y,
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, residual, y, idx_out,
                            workspace, workspace_bytes, stream);
 }
+

@@ -182,7 +182,7 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     shp = (*x.shape[:-1], kk)
     res = (out.reshape(*x.shape[:-1], down_w.shape[0]), idx.reshape(shp), vals.reshape(shp),
            u_s.reshape(shp), None if s_s is None else s_s.reshape(shp),
-           None if z_s is None else z_s.reshape(shp), wd)
+           None if z_s is None else z_s.reshape(shp))
     if not want_mask:
         return res
     return res + (mask.reshape(*x.shape[:-1], mask.shape[-1]),)
@@ -203,9 +203,12 @@ def _restore_index(ctx, saved):
     return idx.reshape(*rows_shape, ctx.k)
 
 
-def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool):
+def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool,
+                     grad_dtype=None):
     """Shared MoC backward (moc/ffn.py:175-259 and the GCP form :423-497).
-    down_w may be the forward's 16-byte-row copy of W_down (same values).
+    x and the weights are in the compute dtype; the weight gradients come out
+    in grad_dtype (the parameters' dtype, default the weights' dtype), dX in
+    x's dtype.
 
     dWd = go^T Z, gZ = go Wd, (gG, gU) = sparse_backward_aux, dWg = gG^T x,
     dWu = gU^T x, dX = gG Wg + gU Wu (one MFMA pass over both products).
@@ -228,7 +231,8 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
         if gcp:
             s_s, z_s = K.gcp_recompute(g_s, u_s)
         z_full = K.scatter_sparse_to_dense(z_s, idx, inter)
-    grad_down_w = torch.empty(go.shape[1], inter, dtype=down_w.dtype, device=dev)
+    grad_dtype = grad_dtype or down_w.dtype
+    grad_down_w = torch.empty(go.shape[1], inter, dtype=grad_dtype, device=dev)
     _on_side(side, (go, z_full, grad_down_w), lambda: K.gemm(go.t(), z_full, out=grad_down_w,
                                                              out_dtype=grad_down_w.dtype))
     del z_full
@@ -237,47 +241,81 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     K.gemm(go, wd, out=gz)
     grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
     del gz
-    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=gate_w.dtype)
-    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=up_w.dtype)
+    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=grad_dtype)
+    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=grad_dtype)
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
     if side is not None:
         main.wait_stream(side)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
 
 
+def _autocast_dtype(x):
+    """The autocast dtype the reference's matmuls would run in for x
+    (moc/ffn.py:50-59), or None outside torch.autocast."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return None
+
+
+def _in_compute_dtype(cdt, *ts):
+    """ts cast to the compute dtype (temporaries; None: unchanged)."""
+    if cdt is None:
+        return ts
+    return tuple(t if t.dtype == cdt else t.to(cdt) for t in ts)
+
+
+def _moc_forward(ctx, selection, x, gate_w, up_w, down_w, k, index_save_dtype, use_triton_aux,
+                 gcp: bool):
+    """Forward of every MoC Function.  Under torch.autocast x and the weights
+    are cast to the autocast dtype here, inside the Function: the casts are
+    temporaries, and what is saved for backward is the cast x plus the
+    parameters themselves (as the reference saves them, moc/ffn.py:166-169,
+    417), not copies of the weights."""
+    cdt = _autocast_dtype(x)
+    xc, wg, wu, wd = _in_compute_dtype(cdt, x, gate_w, up_w, down_w)
+    _check_inputs(xc, wg, wu, wd, use_triton_aux, index_save_dtype)
+    inter = gate_w.shape[0]
+    idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
+    bitmask = index_save_dtype == INDEX_SAVE_BITMASK
+    out, idx, vals, u_s, s_s, z_s, *mask = _forward_common(
+        xc, wg, wu, wd, k, selection, idx_dtype, save_s=not gcp, want_mask=bitmask)
+    sel = _saved_index(idx, mask[0] if mask else None, bitmask)
+    if gcp:
+        ctx.save_for_backward(xc, sel, vals, u_s, gate_w, up_w, down_w)
+    else:
+        ctx.save_for_backward(xc, sel, vals, u_s, s_s, z_s, gate_w, up_w, down_w)
+    ctx.k = idx.shape[-1]
+    ctx.inter = inter
+    ctx.bitmask = bitmask
+    ctx.compute_dtype = cdt
+    ctx.x_dtype = x.dtype
+    ctx.gcp = gcp
+    return out
+
+
+def _moc_backward(ctx, grad_out):
+    if ctx.gcp:
+        x, saved, g_s, u_s, gate_w, up_w, down_w = ctx.saved_tensors
+        s_s = z_s = None
+    else:
+        x, saved, g_s, u_s, s_s, z_s, gate_w, up_w, down_w = ctx.saved_tensors
+    idx = _restore_index(ctx, saved)
+    wg, wu, wd = _in_compute_dtype(ctx.compute_dtype, gate_w, up_w, down_w)
+    dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, wg, wu, wd,
+                                         gcp=ctx.gcp, grad_dtype=gate_w.dtype)
+    return dx.to(ctx.x_dtype), dwg, dwu, dwd, None, None, None
+
+
 class _MoCFunction(torch.autograd.Function):
     """MoC autograd path that keeps selected activations for backward
     (moc/ffn.py:124-259)."""
 
-    selection = "topk"
-
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
-        return _MoCFunction._fwd(ctx, _MoCFunction.selection, x, gate_w, up_w, down_w, k,
-                                 index_save_dtype, use_triton_aux)
+        return _moc_forward(ctx, "topk", x, gate_w, up_w, down_w, k, index_save_dtype,
+                            use_triton_aux, gcp=False)
 
-    @staticmethod
-    def _fwd(ctx, selection, x, gate_w, up_w, down_w, k, index_save_dtype, use_triton_aux):
-        _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
-        inter = gate_w.shape[0]
-        idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        bitmask = index_save_dtype == INDEX_SAVE_BITMASK
-        out, idx, vals, u_s, s_s, z_s, wd, *mask = _forward_common(
-            x, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=True, want_mask=bitmask)
-        ctx.save_for_backward(x, _saved_index(idx, mask[0] if mask else None, bitmask), vals, u_s,
-                              s_s, z_s, gate_w, up_w, wd)
-        ctx.k = idx.shape[-1]
-        ctx.inter = inter
-        ctx.bitmask = bitmask
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        x, saved, g_s, u_s, s_s, z_s, gate_w, up_w, down_w = ctx.saved_tensors
-        idx = _restore_index(ctx, saved)
-        dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w,
-                                             down_w, gcp=False)
-        return dx, dwg, dwu, dwd, None, None, None
+    backward = staticmethod(_moc_backward)
 
 
 class _MoC28Function(torch.autograd.Function):
@@ -286,10 +324,10 @@ class _MoC28Function(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
-        return _MoCFunction._fwd(ctx, "2of8", x, gate_w, up_w, down_w, k, index_save_dtype,
-                                 use_triton_aux)
+        return _moc_forward(ctx, "2of8", x, gate_w, up_w, down_w, k, index_save_dtype,
+                            use_triton_aux, gcp=False)
 
-    backward = staticmethod(_MoCFunction.backward)
+    backward = staticmethod(_moc_backward)
 
 
 class _MoCPostSiluFunction(torch.autograd.Function):
@@ -298,10 +336,10 @@ class _MoCPostSiluFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
-        return _MoCFunction._fwd(ctx, "post_silu_abs", x, gate_w, up_w, down_w, k,
-                                 index_save_dtype, use_triton_aux)
+        return _moc_forward(ctx, "post_silu_abs", x, gate_w, up_w, down_w, k, index_save_dtype,
+                            use_triton_aux, gcp=False)
 
-    backward = staticmethod(_MoCFunction.backward)
+    backward = staticmethod(_moc_backward)
 
 
 class _MoCGCPFunction(torch.autograd.Function):
@@ -310,35 +348,10 @@ class _MoCGCPFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, gate_w, up_w, down_w, k, index_save_dtype=None, use_triton_aux=False):
-        _check_inputs(x, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
-        inter = gate_w.shape[0]
-        idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
-        bitmask = index_save_dtype == INDEX_SAVE_BITMASK
-        out, idx, vals, u_s, _, _, wd, *mask = _forward_common(
-            x, gate_w, up_w, down_w, k, "topk", idx_dtype, save_s=False, want_mask=bitmask)
-        ctx.save_for_backward(x, _saved_index(idx, mask[0] if mask else None, bitmask), vals, u_s,
-                              gate_w, up_w, wd)
-        ctx.k = k
-        ctx.inter = inter
-        ctx.bitmask = bitmask
-        return out
+        return _moc_forward(ctx, "topk", x, gate_w, up_w, down_w, k, index_save_dtype,
+                            use_triton_aux, gcp=True)
 
-    @staticmethod
-    def backward(ctx, grad_out):
-        x, saved, g_s, u_s, gate_w, up_w, down_w = ctx.saved_tensors
-        idx = _restore_index(ctx, saved)
-        dx, dwg, dwu, dwd = _backward_common(grad_out, x, idx, g_s, u_s, None, None, gate_w,
-                                             up_w, down_w, gcp=True)
-        return dx, dwg, dwu, dwd, None, None, None
-
-
-def _autocast_cast(x, ws):
-    """Under torch.autocast the reference's matmuls run in the autocast dtype
-    (moc/ffn.py:50-59); cast inputs the same way for the fused path."""
-    if torch.is_autocast_enabled("cuda") and x.is_cuda:
-        dt = torch.get_autocast_dtype("cuda")
-        return x.to(dt), [w.to(dt) for w in ws]
-    return x, ws
+    backward = staticmethod(_moc_backward)
 
 
 class MoCSwiGLUFFN(nn.Module):
@@ -373,8 +386,7 @@ class MoCSwiGLUFFN(nn.Module):
         self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
 
     def forward(self, x):
-        weights = [self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight]
-        x, (wg, wu, wd) = _autocast_cast(x, weights)
+        wg, wu, wd = self.gate_proj.weight, self.up_proj.weight, self.down_proj.weight
         aux = self.mode.endswith("_triton_aux")
         if self.mode in ("moc_gcp", "moc_gcp_triton_aux"):
             fn = _MoCGCPFunction

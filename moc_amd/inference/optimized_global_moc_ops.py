@@ -1,10 +1,12 @@
 """Global-MoC operators and graph runner (moc/inference/optimized_global_moc_ops.py).
 
 load_optimized_global_moc_extension() loads libmoc_amd.so (built in-tree by
-`python -m moc_amd.build`; no JIT compile at first use) and registers the
-moc_native:: and moc:: operators.  make_optimized_global_moc_graph_runner()
-captures the decode path - gate GEMV, Top-K, selected Up * SiLU, selected
-Down - in a HIP graph, replayed per call (reference :106-162).
+`python -m moc_amd.build`; no JIT compile at first use), registers the
+moc_native:: and moc:: operators and returns the extension object whose
+methods the reference's callers use (optimized_global_moc_ext.cpp:78-86).
+make_optimized_global_moc_graph_runner() captures the decode path - gate
+GEMV, Top-K, selected Up * SiLU, selected Down - in a HIP graph, replayed
+per call (reference :106-162).
 """
 from __future__ import annotations
 
@@ -13,11 +15,82 @@ import torch
 from .. import _native, kernels as K, ops
 
 
-def load_optimized_global_moc_extension(build_dir=None):
-    """Load the gfx950 library and register the ops; returns the ctypes handle."""
-    lib = _native.load()
-    ops.register()
-    return lib
+class OptimizedGlobalMoCExtension:
+    """The methods of the reference's pybind module
+    (optimized_global_moc_ext.cpp:25-86), on the gfx950 kernels.
+
+    cub_topk_bf16_512x11 returns [values, int64 indices] ordered as the
+    reference's stable descending radix sort emits them: value descending,
+    ties to the lower channel index (-0.0 and +0.0 rank equal here).  The
+    reference's I <= 5632 limit of its one-CTA sort is lifted (I <= 16384).
+    The checks raise RuntimeError with the reference's TORCH_CHECK messages.
+    """
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    @staticmethod
+    def _require(cond: bool, msg: str) -> None:
+        if not cond:
+            raise RuntimeError(msg)
+
+    def cub_topk_bf16_512x11(self, scores: torch.Tensor, k: int):
+        r = self._require
+        r(scores.is_cuda, "scores must be CUDA")
+        r(scores.dim() == 2, "scores must be [B, I]")
+        r(scores.dtype == torch.bfloat16, "scores must be BF16")
+        r(scores.is_contiguous(), "scores must be contiguous")
+        r(0 < k <= scores.shape[1], "invalid k")
+        vals, idx, _ = K.topk_rows(scores, int(k), idx_dtype=torch.int64)
+        return list(ops.value_order(vals, idx))
+
+    def selected_up_silu_bf16(self, x, topk_vals, idx, w_up):
+        r = self._require
+        r(x.is_cuda and topk_vals.is_cuda and idx.is_cuda and w_up.is_cuda, "all tensors must be CUDA")
+        r(x.dtype == torch.bfloat16, "x must be BF16")
+        r(topk_vals.dtype == torch.bfloat16, "topk_vals must be BF16")
+        r(w_up.dtype == torch.bfloat16, "w_up must be BF16")
+        r(idx.dtype == torch.int64, "idx must be int64")
+        r(x.is_contiguous() and topk_vals.is_contiguous() and idx.is_contiguous()
+          and w_up.is_contiguous(), "inputs must be contiguous")
+        return K.selected_up_silu(x, topk_vals, idx, w_up)
+
+    def selected_down_bf16_h32_k16(self, sparse_z, idx, w_down_t):
+        r = self._require
+        r(sparse_z.is_cuda and idx.is_cuda and w_down_t.is_cuda, "all tensors must be CUDA")
+        r(sparse_z.dtype == torch.bfloat16, "sparse_z must be BF16")
+        r(w_down_t.dtype == torch.bfloat16, "w_down_t must be BF16")
+        r(idx.dtype == torch.int64, "idx must be int64")
+        r(sparse_z.is_contiguous() and idx.is_contiguous() and w_down_t.is_contiguous(),
+          "inputs must be contiguous")
+        return K.selected_down(sparse_z, idx, w_down_t)
+
+    def optimized_global_after_gate_bf16(self, x, gate_scores, up_weight, down_weight_t, k: int):
+        r = self._require
+        r(x.is_cuda and gate_scores.is_cuda and up_weight.is_cuda and down_weight_t.is_cuda,
+          "all tensors must be CUDA")
+        for t, n in ((x, "x"), (gate_scores, "gate_scores"), (up_weight, "up_weight"),
+                     (down_weight_t, "down_weight_t")):
+            r(t.dtype == torch.bfloat16, f"{n} must be BF16")
+        r(x.is_contiguous() and gate_scores.is_contiguous() and up_weight.is_contiguous()
+          and down_weight_t.is_contiguous(), "inputs must be contiguous")
+        r(0 < k <= gate_scores.shape[1], "invalid k")
+        return K.global_after_gate(x, gate_scores, up_weight, down_weight_t, int(k))
+
+
+_EXT: OptimizedGlobalMoCExtension | None = None
+
+
+def load_optimized_global_moc_extension(build_dir=None) -> OptimizedGlobalMoCExtension:
+    """Load the gfx950 library (once), register the ops and return the
+    extension object.  build_dir is accepted for the reference's signature;
+    the library is built in-tree ahead of time."""
+    global _EXT
+    if _EXT is None:
+        lib = _native.load()
+        ops.register()
+        _EXT = OptimizedGlobalMoCExtension(lib)
+    return _EXT
 
 
 def ensure_native_ops_ready() -> None:

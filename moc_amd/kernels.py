@@ -459,16 +459,21 @@ def global_after_gate_workspace_bytes(nb: int, inter: int, k: int, hidden: int) 
 
 
 _WS_CACHE: dict = {}
+_WS_RETIRED: list = []
 
 
 def _decode_workspace(device, nbytes: int) -> torch.Tensor:
-    """A zero-initialised workspace per device, grown on demand.  The decode
-    kernel's arrival counters must start at zero and every call leaves them
-    zero, so the buffer is reused without clearing (calls on one device must
-    not overlap)."""
-    key = (device.type, device.index)
+    """The after-gate workspace of the current stream on `device`, grown on
+    demand.  The kernel's arrival counters must start at zero and every call
+    leaves them zero, so a buffer is created zeroed and then reused without
+    clearing.  One buffer per stream keeps calls on different streams apart.
+    A buffer that is outgrown is kept alive, not freed: a HIP graph captured
+    with it keeps writing to it on every replay."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _WS_CACHE.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _WS_RETIRED.append(ws)
         ws = torch.zeros((max(nbytes, 256),), dtype=torch.uint8, device=device)
         _WS_CACHE[key] = ws
     return ws
@@ -481,15 +486,21 @@ def global_after_gate_workspace(nb: int, inter: int, k: int, hidden: int, device
 
 
 def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, workspace=None,
-                      out=None, residual: torch.Tensor | None = None) -> torch.Tensor:
+                      out=None, residual: torch.Tensor | None = None,
+                      idx_out: torch.Tensor | None = None) -> torch.Tensor:
     """Top-K + selected Up * SiLU + selected Down after the gate; with
-    `residual`, returns residual + that (bf16 add) from the same launch."""
-    N.require_device(x, gate_scores, up_weight, down_weight_t)
+    `residual`, returns residual + that (bf16 add) from the same launch.
+    `idx_out` (int32 [nb, k]) receives the selected channels in ascending
+    order.  Without `workspace`, the stream's shared workspace is used."""
+    N.require_device(x, gate_scores, up_weight, down_weight_t, idx_out)
     x, g, wu, wdt = _bf16_contig(x, gate_scores, up_weight, down_weight_t)
     nb, hidden = x.shape
     inter = g.shape[1]
     if wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
         raise ValueError("up_weight and down_weight_t must be [intermediate, hidden]")
+    if idx_out is not None and (idx_out.dtype != torch.int32 or idx_out.shape != (nb, int(k))
+                                or not idx_out.is_contiguous()):
+        raise ValueError(f"idx_out must be a contiguous int32 [{nb}, {int(k)}] tensor")
     if nb > 16:
         # more tokens than the fused kernel takes: the same steps as separate
         # launches (row Top-K, selected Up * SiLU, selected Down), like the
@@ -499,6 +510,8 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
         yy = selected_down(z, idx, wdt)
         if residual is not None:
             yy = residual.reshape(yy.shape) + yy
+        if idx_out is not None:
+            idx_out.copy_(idx)
         if out is None:
             return yy
         out.copy_(yy)
@@ -511,15 +524,15 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
         raise ValueError(f"global_after_gate: workspace of {ws_bytes} bytes required")
     if residual is None:
         N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
-               wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), workspace.data_ptr(), ws_bytes,
-               N.stream_of(x))
+               wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out),
+               workspace.data_ptr(), ws_bytes, N.stream_of(x))
         return y
     r = residual.reshape(nb, hidden)
     if r.dtype != torch.bfloat16 or not r.is_contiguous():
         raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
     N.call("moc_global_after_gate_residual_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
-           wu.data_ptr(), wdt.data_ptr(), int(k), r.data_ptr(), y.data_ptr(), workspace.data_ptr(),
-           ws_bytes, N.stream_of(x))
+           wu.data_ptr(), wdt.data_ptr(), int(k), r.data_ptr(), y.data_ptr(), N.ptr(idx_out),
+           workspace.data_ptr(), ws_bytes, N.stream_of(x))
     return y
 
 

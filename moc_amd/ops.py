@@ -14,10 +14,11 @@ trace under torch.compile):
   moc::selected_grouped_down(sparse_z, idx, w_down_t) -> Tensor
       (moc/inference/triton_grouped_moc_ops.py:26-143)
 
-The argument checks raise the reference's messages.  One documented
-difference: the Top-K ops return the selected channels in ascending channel
-order (the reference's CUB kernel returns them sorted by value); consumers
-only use (value, index) pairs, so results downstream are unaffected.
+The argument checks raise the reference's messages.  The Top-K ops return
+the selection in the order of the reference's stable descending radix sort
+(optimized_global_moc_ext.cu:39-83): value descending, ties to the lower
+channel index.  One documented difference: -0.0 and +0.0 rank equal here
+(the reference's key encoding puts -0.0 below +0.0).
 """
 from __future__ import annotations
 
@@ -39,10 +40,18 @@ def _check_topk(scores: torch.Tensor, k: int) -> None:
         raise RuntimeError("invalid k")
 
 
+def value_order(vals: torch.Tensor, idx: torch.Tensor):
+    """(vals, idx) of a selection in ascending channel order -> the same
+    pairs ordered by value descending, equal values by ascending channel (a
+    stable sort keeps the channel order among equal values)."""
+    order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
+    return torch.gather(vals, -1, order), torch.gather(idx, -1, order)
+
+
 def _topk_impl(scores: torch.Tensor, k: int):
     _check_topk(scores, k)
     vals, idx, _ = K.topk_rows(scores.contiguous(), int(k), idx_dtype=torch.int64)
-    return vals, idx
+    return value_order(vals, idx)
 
 
 def _up_impl(x, topk_vals, topk_idx, up_weight):

@@ -293,13 +293,14 @@ def dense_masked_autograd(x, gate_w, up_w, down_w, idx: np.ndarray, grad_out, dt
 
 
 # ---------------------------------------------------------------- inference
-def masked_reference(x, gate_w, up_w, down_w, k: int, grouped: bool = False, g_override=None):
+def masked_reference(x, gate_w, up_w, down_w, k: int, grouped: bool = False, g_override=None,
+                     u_override=None):
     """InferenceMoCSwiGLUFFN.masked_reference (moc/inference/inference_ffn.py:
     169-180): G, U in bf16, z = bf16(bf16(SiLU(g)) * u), y = z_full W_down^T."""
     dt = x.dtype
     x2 = x.reshape(-1, x.shape[-1])
     g = mm(x2, gate_w.t(), dt) if g_override is None else g_override.reshape(x2.shape[0], -1).to(dt)
-    u = mm(x2, up_w.t(), dt)
+    u = mm(x2, up_w.t(), dt) if u_override is None else u_override.reshape(x2.shape[0], -1).to(dt)
     idx = select_2of8_indices(g) if grouped else topk_indices(g, k)
     vals = gather_rows(g, idx).float()
     s = (vals / (1.0 + torch.exp(-vals))).to(dt)
@@ -327,13 +328,14 @@ def selected_down(z, idx: np.ndarray, w_down_t):
     return torch.stack(rows).to(z.dtype)
 
 
-def grouped_top2_up_silu(x, gate_w, up_w):
+def grouped_top2_up_silu(x, gate_w, up_w, g_override=None, u_override=None):
     """Kernel A of the 2:8 path (triton_fused_ffn_kernels.py:29-156): G, U
     rounded to bf16 before selection; sz = (g*sigmoid(g))*u in f32, stored
-    in x's dtype; idx int64 (top-1, top-2) per group."""
+    in x's dtype; idx int64 (top-1, top-2) per group.  g_override/u_override
+    replace the two projections (e.g. by the device's own bf16 results)."""
     dt = x.dtype
-    g = mm(x, gate_w.t(), dt)
-    u = mm(x, up_w.t(), dt)
+    g = mm(x, gate_w.t(), dt) if g_override is None else g_override.to(dt)
+    u = mm(x, up_w.t(), dt) if u_override is None else u_override.to(dt)
     idx = select_2of8_indices(g)
     gs = gather_rows(g, idx).float()
     us = gather_rows(u, idx).float()

@@ -39,7 +39,7 @@ def test_library_exports_every_header_symbol(lib):
     assert set(names) == set(N.SIGNATURES), set(names) ^ set(N.SIGNATURES)
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.moc_abi_version() == 1
+    assert lib.moc_abi_version() == 2
 
 
 def test_validation_errors_without_device_work(lib):
@@ -131,6 +131,58 @@ def test_custom_ops_registered_with_reference_names():
         assert hasattr(torch.ops.moc, name)
     with pytest.raises(Exception):
         torch.ops.moc_native.optimized_global_topk_bf16(torch.randn(2, 8).bfloat16(), 3)
+
+
+def test_reference_import_path_resolves_to_this_package():
+    """Callers written against the reference's `moc` package import unchanged
+    (examples/quickstart.py:6, benchmark_training_latency.py:17,
+    benchmark_ffn_latency.py) and get this package's objects."""
+    import importlib
+
+    import moc
+    from moc import PRESETS as P2, build_model as bm2
+    from moc.ffn import build_ffn as bf2, MoCSwiGLUFFN as M2
+    from moc.inference.inference_ffn import InferenceMoCSwiGLUFFN as I2
+    from moc.inference.optimized_global_moc_ops import load_optimized_global_moc_extension
+    import moc.inference.triton_grouped_moc_ops as tg
+    import moc.inference.triton_fused_ffn_kernels as tf
+    import moc_amd.ffn
+    assert P2 is PRESETS and bm2 is build_model and bf2 is build_ffn and M2 is MoCSwiGLUFFN
+    assert I2 is InferenceMoCSwiGLUFFN
+    assert moc.ffn is moc_amd.ffn and moc.ffn.__spec__.name == "moc_amd.ffn"
+    assert tg.__name__ == "moc_amd.inference.grouped_moc_ops"
+    assert hasattr(tf, "fused_gate_top2of8_selected_up_silu_into")
+    assert callable(load_optimized_global_moc_extension)
+    with pytest.raises(ModuleNotFoundError):
+        importlib.import_module("moc.no_such_module")
+
+
+def test_extension_object_checks_like_the_reference(lib):
+    """load_optimized_global_moc_extension() returns an object with the
+    reference pybind methods (optimized_global_moc_ext.cpp:78-86), whose
+    argument checks raise the reference's messages before any device work."""
+    from moc_amd.inference.optimized_global_moc_ops import load_optimized_global_moc_extension
+    ext = load_optimized_global_moc_extension()
+    assert ext is load_optimized_global_moc_extension()
+    for name in ("cub_topk_bf16_512x11", "selected_up_silu_bf16", "selected_down_bf16_h32_k16",
+                 "optimized_global_after_gate_bf16"):
+        assert callable(getattr(ext, name))
+    with pytest.raises(RuntimeError, match="scores must be CUDA"):
+        ext.cub_topk_bf16_512x11(torch.randn(2, 64).bfloat16(), 3)
+    with pytest.raises(RuntimeError, match="all tensors must be CUDA"):
+        ext.selected_down_bf16_h32_k16(torch.zeros(1, 4).bfloat16(), torch.zeros(1, 4, dtype=torch.long),
+                                       torch.zeros(8, 64).bfloat16())
+
+
+def test_value_order_is_stable_descending():
+    """The moc_native Top-K op's order: value descending, equal values by
+    ascending channel (the reference's stable radix sort)."""
+    from moc_amd.ops import value_order
+    vals = torch.tensor([[1.0, 3.0, 3.0, -0.0, 0.0, 2.0]]).bfloat16()
+    idx = torch.tensor([[0, 2, 5, 7, 8, 9]])
+    v, i = value_order(vals, idx)
+    assert i.tolist() == [[2, 5, 9, 0, 7, 8]]
+    assert v.float().tolist() == [[3.0, 3.0, 2.0, 1.0, -0.0, 0.0]]
 
 
 def test_product_never_imports_oracle():
