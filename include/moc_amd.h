@@ -4,8 +4,10 @@
  * libmoc_amd.so exports exactly the functions declared here.  All of them
  * take raw device pointers, element counts and element strides; `stream` is
  * a hipStream_t passed as void* (NULL = the default stream).  Nothing here
- * allocates device memory: callers own every buffer (outputs and workspaces),
- * so any sequence of calls may be recorded into a HIP graph.  No function
+ * allocates device memory: callers own every buffer (outputs and workspaces;
+ * the one exception, moc_global_after_gate_noalloc_bf16, uses a fixed device
+ * array of the library's own), so any sequence of calls may be recorded into
+ * a HIP graph.  No function
  * throws; each returns MOC_OK or a negative status, and moc_last_error()
  * describes the last failure on the calling thread.
  *
@@ -259,6 +261,23 @@ int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, 
                                         const void* w_down_t, int64_t k, const void* residual,
                                         void* y, void* idx_out, void* workspace,
                                         int64_t workspace_bytes, void* stream);
+
+/* Bytes of the library's own device scratch array (one per GPU, held until
+ * the process ends) behind moc_global_after_gate_noalloc_bf16. */
+#define MOC_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)
+
+/* moc_global_after_gate_residual_bf16 (residual may be NULL: plain
+ * moc_global_after_gate_bf16) that allocates nothing and takes no workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture without an allocator, tight
+ * serving loops).  The workspace is the library's fixed device scratch array
+ * of MOC_NOALLOC_SCRATCH_BYTES per GPU; shapes that need more are rejected
+ * (MOC_ERR_INVALID).  The stream must belong to the current device.  All
+ * calls on one GPU share its array: calls that overlap on one GPU race. */
+int moc_global_after_gate_noalloc_bf16(const void* x, const void* gate_scores, int64_t nb,
+                                       int64_t inter, int64_t hidden, const void* w_up,
+                                       const void* w_down_t, int64_t k, const void* residual,
+                                       void* y, void* idx_out, void* stream);
 
 /* ------------------------------------------------------------------- 2:8 */
 /* Fused gate+up projection with top-2-of-8 selection for nb tokens:

@@ -66,6 +66,8 @@ SIGNATURES: dict[str, tuple] = {
                                      _i64, _vp, _i64, _vp]),
     "moc_global_after_gate_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
                                                    _vp, _vp, _vp, _i64, _vp]),
+    "moc_global_after_gate_noalloc_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
+                                                  _vp, _vp, _vp]),
     "moc_selected_up_silu_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _int, _i64, _vp, _i64, _vp, _vp]),
     "moc_selected_down_workspace_size": (_i64, [_i64, _i64, _i64]),
     "moc_selected_down_bf16": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
