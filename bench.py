@@ -14,15 +14,20 @@ The same line carries:
   roofline      the MFMA GEMM engine (the dominant kernel of the step):
                 algorithmic FLOP of the nine FFN GEMMs (7 launches: G and U
                 share one, dX sums two products) / their summed HIP-event time,
-                against the 2.5 PFLOP/s dense bf16 peak;
+                against the 2.5 PFLOP/s dense bf16 peak; measured on isolated
+                back-to-back launches at the layer's shapes, and (in_step) on
+                the same launches inside real training steps;
   roofline_decode  global-MoC decode (config 3, B=1): union-of-selected-rows
                 bytes / layer time against 8 TB/s, cold weights (rotation
                 over 8 weight sets > 2x the 256 MB MALL), HIP-graph replays;
   cpu_baseline  the repo's CPU restatement (oracle/) of the reference path,
                 timed on this host on a bounded token sample and scaled to
                 the full layer;
-  extra         the other configs: decode B=1/4/16, 2:8 prefill (config 4),
-                130m MoC+GCP fwd+bwd (config 2), fwd/bwd split.
+  configs       each of the five configs: latency, throughput, roofline
+                fraction and its own CPU baseline (config 1: 60m fp32 MoC
+                forward; 2: 130m MoC+GCP fwd+bwd; 3: decode B=1/4/16; 4: MoC
+                2:8 prefill of 4096 tokens; 5: 350m model training step,
+                moc_gcp and dense, tokens/s and peak memory).
 
 Only one GPU is used; --gpus N with N > 1 exits with a message.
 """
@@ -61,8 +66,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="approximate CPU time budget of the cpu_baseline sample")
-    p.add_argument("--decode-groups", type=int, default=40)
-    p.add_argument("--decode-iters", type=int, default=50)
+    p.add_argument("--decode-groups", type=int, default=80)
+    p.add_argument("--decode-iters", type=int, default=100)
     p.add_argument("--skip-extra", action="store_true", help="headline + rooflines only")
     p.add_argument("--cfg5", action="store_true",
                    help="only the 350m-model training step (config 5): tokens/s and peak "
@@ -74,10 +79,10 @@ def parse_args():
     p.add_argument("--roofline-only", action="store_true",
                    help="only the seven GEMM launches of the roofline (for rocprofv3 kernel "
                         "traces whose per-kernel averages match roofline.per_launch)")
-    p.add_argument("--pmc-target", choices=["gemm", "copy", "decode"], default=None,
-                   help="only launch one workload a few times (for rocprofv3 --pmc runs): the G "
-                        "GEMM of the 1b layer, a plain 256 MiB copy kernel (counter scale), or "
-                        "the B=1 decode layer over 8 weight sets")
+    p.add_argument("--pmc-target", choices=["gemm", "dx", "copy", "decode"], default=None,
+                   help="only launch one workload a few times (for rocprofv3 --pmc runs): the G,U "
+                        "pair GEMM of the 1b layer, its dX GEMM (two products), a plain 256 MiB "
+                        "copy kernel (counter scale), or the B=1 decode layer over 8 weight sets")
     return p.parse_args()
 
 
@@ -141,6 +146,18 @@ def pmc_target(which: str) -> None:
         u = K.padded_empty(x.shape[0], I1B, torch.bfloat16, x.device)
         for _ in range(5):
             K.linear_pair(x, wg, wu, out1=g, out2=u)
+    elif which == "dx":
+        t, d, inter, k = BATCH1B * SEQ1B, D1B, I1B, K1B
+        x, wg, wu, _, _ = seeded_inputs(t, d, inter)
+        gen = torch.Generator(device="cuda").manual_seed(7)
+        zs = torch.randn(t, k, device="cuda", generator=gen).to(torch.bfloat16)
+        idx = torch.argsort(torch.rand(t, inter, device="cuda", generator=gen), dim=1)[:, :k]
+        idx = idx.sort(dim=1).values.to(torch.int16)
+        gg = K.scatter_sparse_to_dense(zs, idx, inter)
+        gu = K.scatter_sparse_to_dense(zs, idx, inter)
+        wg_a, wu_a = K.aligned_rows(wg.cuda()), K.aligned_rows(wu.cuda())
+        for _ in range(5):
+            K.gemm(gg, wg_a, a2=gu, b2=wu_a)
     elif which == "decode":
         gen = torch.Generator(device="cuda").manual_seed(1234)
         layers = []
@@ -200,10 +217,14 @@ def build_layer(d, inter, k, ws, mode="moc_gcp"):
     return m
 
 
-def time_train_layer(m, x, go, steps, warmup):
+def time_train_layer(m, x, go, steps, warmup, probe: list | None = None,
+                     step_starts: list | None = None):
     """Reference method: untimed warmup, then K timed fwd+bwd steps bracketed
-    by a device synchronisation; per-step events split fwd and bwd."""
+    by a device synchronisation; per-step events split fwd and bwd.  With
+    `probe` (a list), every GEMM launch of the timed steps is also bracketed
+    by timing events on its own stream and recorded there."""
     import torch
+    from moc_amd import kernels as K
     for _ in range(warmup):
         m.zero_grad(set_to_none=True)
         x.grad = None
@@ -212,17 +233,23 @@ def time_train_layer(m, x, go, steps, warmup):
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for e0, e1, e2 in ev:
-        m.zero_grad(set_to_none=True)
-        x.grad = None
-        e0.record()
-        y = m(x)
-        e1.record()
-        y.backward(go)
-        e2.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    K.set_gemm_probe(probe)
+    try:
+        t0 = time.perf_counter()
+        for e0, e1, e2 in ev:
+            m.zero_grad(set_to_none=True)
+            x.grad = None
+            e0.record()
+            y = m(x)
+            e1.record()
+            y.backward(go)
+            e2.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        K.set_gemm_probe(None)
+    if step_starts is not None:
+        step_starts.extend(e0 for e0, _, _ in ev)
     fwd = [a.elapsed_time(b) for a, b, _ in ev]
     bwd = [b.elapsed_time(c) for _, b, c in ev]
     return wall * 1e3 / steps, summarize(fwd), summarize(bwd)
@@ -437,11 +464,11 @@ def cpu_baseline(seconds: float):
     from oracle import moc_oracle as O
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    ts = 1024
+    ts = 4096
     x, wg, wu, wd, go = seeded_inputs(ts, D1B, I1B, seed=4321)
     times = []
     t_start = time.perf_counter()
-    for i in range(12):
+    for i in range(6):
         t0 = time.perf_counter()
         f = O.ffn_forward(x, wg, wu, wd, K1B, "moc_gcp")
         O.ffn_backward(x, wg, wu, wd, f, go, gcp=True)
@@ -468,6 +495,284 @@ def cpu_baseline(seconds: float):
             "cpu_model": cpu_model or platform.processor()}
 
 
+FP32_PEAK_TFLOPS = 157.3
+
+
+def in_step_gemm(records, step_starts):
+    """GEMM time inside the timed fwd+bwd steps, from the probe's records
+    (every GEMM launch bracketed by timing events on the stream it ran on).
+    Launches on the two streams can overlap, so the GEMM time of a step is
+    the length of the union of its launch intervals (relative to the step's
+    start event); per launch position, the mean bracketed duration."""
+    steps = len(step_starts)
+    per_step = len(records) // steps
+    busy, flops = [], []
+    for i, ref in enumerate(step_starts):
+        rs = records[i * per_step:(i + 1) * per_step]
+        iv = sorted((ref.elapsed_time(a), ref.elapsed_time(b)) for _, a, b, _ in rs)
+        tot, cur_s, cur_e = 0.0, None, None
+        for s0, e0 in iv:
+            if cur_e is None or s0 > cur_e:
+                if cur_e is not None:
+                    tot += cur_e - cur_s
+                cur_s, cur_e = s0, e0
+            else:
+                cur_e = max(cur_e, e0)
+        tot += cur_e - cur_s
+        busy.append(tot)
+        flops.append(sum(f for _, _, _, f in rs))
+    ms = statistics.median(busy)
+    flop = flops[0]
+    launches = []
+    for j in range(per_step):
+        rs = records[j::per_step]
+        us = statistics.mean(a.elapsed_time(b) for _, a, b, _ in rs) * 1e3
+        launches.append({"gemm": rs[0][0], "us": round(us, 1),
+                         "tflops": round(rs[0][3] / (us * 1e-6) / 1e12, 1)})
+    achieved = flop / (ms * 1e-3) / 1e12
+    return {"gemm_ms_per_step": round(ms, 4), "algorithmic_flop_per_step": flop,
+            "achieved": round(achieved, 1), "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+            "per_launch": launches}
+
+
+def gather_report(x, wg, k, tiles=(256, 64, 16)):
+    """Executed vs algorithmic FLOP of the training step's GEMMs over the
+    channel dimension, from the real selection of the bench input.  The
+    layer runs every product densely over all I channels on MFMA tiles; the
+    algorithmic count takes only each token's K selected channels; a
+    gathered-row GEMM over an M-tile of tokens would have to run over the
+    union of the tile's selections, whose share of I is measured here for
+    several tile heights (1 - (1 - K/I)^m for independent tokens)."""
+    import torch
+    from moc_amd import kernels as K
+    t, d = x.shape[0] * x.shape[1], x.shape[-1]
+    inter = wg.shape[0]
+    g = K.linear(x.reshape(-1, d).to(torch.bfloat16), wg)
+    _, _, mask = K.topk_rows(g, k, want_vals=False, want_mask=True)
+    bits = torch.zeros(t, (inter + 31) // 32 * 32, dtype=torch.bool, device=x.device)
+    words = mask.view(torch.int32)
+    for b in range(32):
+        bits[:, b::32] = ((words >> b) & 1).bool()
+    bits = bits[:, :inter]
+    union = {}
+    for m in tiles:
+        tb = bits[: (t // m) * m].view(t // m, m, inter).any(dim=1)
+        union[f"tile_{m}_tokens"] = round(tb.float().mean().item(), 4)
+    dense = 2.0 * t * d * inter
+    sparse = 2.0 * t * d * k
+    # D, dWd, gZ (needed only at selected positions), dWg, dWu, dX (2 products)
+    prods = 7
+    return {"products_over_channels": prods,
+            "executed_gflop_dense": round(prods * dense / 1e9, 1),
+            "algorithmic_gflop_selected": round(prods * sparse / 1e9, 1),
+            "gathered_gflop_at_tile_256": round(prods * dense * union["tile_256_tokens"] / 1e9, 1),
+            "union_share_of_channels": union,
+            "note": "G and U (2 products) are dense in the reference too; the other 7 products "
+                    "touch only selected channels per token, but a 256-token MFMA tile's union "
+                    "of selections covers about all channels, so gathering rows would not cut "
+                    "the executed FLOP"}
+
+
+def cfg1_bench(reps=50):
+    """Config 1: one MoC FFN layer forward at the 60m preset shape in fp32
+    (X [2, 256, 512], I 1376, K 256; `moc` mode), eager launches."""
+    import torch
+    from moc_amd.ffn import MoCSwiGLUFFN
+    d, inter, k = 512, 1376, 256
+    x, wg, wu, wd, _ = seeded_inputs(512, d, inter, dtype=torch.float32)
+    m = MoCSwiGLUFFN(d, inter, k, mode="moc").to("cuda")
+    with torch.no_grad():
+        for p_, w in zip((m.gate_proj.weight, m.up_proj.weight, m.down_proj.weight), (wg, wu, wd)):
+            p_.copy_(w)
+    xd = x.reshape(2, 256, d).cuda()
+    with torch.no_grad():
+        for _ in range(10):
+            m(xd)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            m(xd)
+            b.record()
+        torch.cuda.synchronize()
+    st = summarize([a.elapsed_time(b) * 1e3 for a, b in ev])
+    # algorithmic: gate + up GEMMs + the down projection of the K selected channels
+    flop = 2 * 2 * 512 * d * inter + 2 * 512 * k * d
+    tf = flop / (st["median"] * 1e-6) / 1e12
+    return {"us": round(st["median"], 2), "us_p10": round(st["p10"], 2), "us_p90": round(st["p90"], 2),
+            "tokens_per_s": round(512 / (st["median"] * 1e-6), 1), "dtype": "f32",
+            "roofline": {"bound": "fp32 (latency-bound at this size)", "achieved": round(tf, 2),
+                         "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / FP32_PEAK_TFLOPS, 4),
+                         "algorithmic_gflop": round(flop / 1e9, 3)}}
+
+
+def _cpu_setup():
+    import torch
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _cpu_time(fn, reps=3, budget_s=8.0):
+    """Median wall time of fn() after one untimed call, at least `reps`
+    timed calls unless the budget runs out after the first."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    return statistics.median(times), len(times)
+
+
+def cpu_cfg1():
+    import torch
+    from oracle import moc_oracle as O
+    th = _cpu_setup()
+    d, inter, k = 512, 1376, 256
+    x, wg, wu, wd, _ = seeded_inputs(512, d, inter, dtype=torch.float32)
+    med, n = _cpu_time(lambda: O.ffn_forward(x, wg, wu, wd, k, "moc"), reps=10)
+    return {"value": round(med * 1e6, 1), "unit": "us", "cores": th, "kind": "port",
+            "sample": f"oracle `moc` forward, the whole workload (512 tokens, f32), median of {n}"}
+
+
+def cpu_cfg2():
+    from oracle import moc_oracle as O
+    th = _cpu_setup()
+    t, d, inter, k = 8192, 768, 2048, 384
+    x, wg, wu, wd, go = seeded_inputs(t, d, inter)
+
+    def run():
+        f = O.ffn_forward(x, wg, wu, wd, k, "moc_gcp")
+        O.ffn_backward(x, wg, wu, wd, f, go, gcp=True)
+
+    med, n = _cpu_time(run, reps=2)
+    return {"value": round(med * 1e6, 1), "unit": "us", "cores": th, "kind": "port",
+            "sample": f"oracle moc_gcp fwd+bwd, the whole workload (8192 tokens; bf16 storage, "
+                      f"f32 matmul), median of {n}"}
+
+
+def cpu_decode(nb):
+    import torch
+    from oracle import moc_oracle as O
+    th = _cpu_setup()
+    d, inter, k = D1B, I1B, K1B
+    g = torch.Generator().manual_seed(1234)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(d, inter, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16)
+    med, n = _cpu_time(lambda: O.masked_reference(x, wg, wu, wd, k), reps=10, budget_s=3.0)
+    return {"value": round(med * 1e6, 1), "unit": "us", "cores": th, "kind": "port",
+            "sample": f"oracle masked_reference, the whole workload ({nb} token(s), bf16 storage, "
+                      f"f32 matmul), median of {n}"}
+
+
+def cpu_cfg4():
+    import torch
+    from oracle import moc_oracle as O
+    th = _cpu_setup()
+    t, d, inter = 4096, D1B, 5464
+    g = torch.Generator().manual_seed(1234)
+    x = torch.randn(t, d, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+    wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16)
+
+    def run():
+        idx, sz, _ = O.grouped_top2_up_silu(x, wg, wu)
+        O.selected_down(sz, idx, wdt)
+
+    med, n = _cpu_time(run, reps=1, budget_s=10.0)
+    return {"value": round(med * 1e6, 1), "unit": "us", "cores": th, "kind": "port",
+            "sample": f"oracle 2:8 gate/up + top-2-of-8 + compacted down, the whole workload (4096 "
+                      f"tokens; bf16 storage, f32 matmul), median of {n}"}
+
+
+def cpu_cfg5():
+    """Config 5 on the CPU: the 350m decoder's training step with the
+    oracle's moc_gcp FFN (forward and backward as an autograd Function),
+    stock PyTorch attention/norms/embeddings and AdamW, batch 16 x 256, f32.
+    A bounded sample: one transformer block's fwd+bwd and AdamW update, and
+    the rest of the step (embedding, final norm, LM head, loss, their AdamW)
+    are timed separately; the 24-layer step is rest + 24 x block."""
+    import torch
+    from dataclasses import replace
+    from oracle import moc_oracle as O
+    from moc_amd import PRESETS, build_model
+    from moc_amd.model import TransformerBlock
+    th = _cpu_setup()
+
+    class OracleGCP(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, wg, wu, wd, k):
+            x2 = x.reshape(-1, x.shape[-1])
+            f = O.ffn_forward(x2, wg, wu, wd, k, "moc_gcp")
+            ctx.f, ctx.shape = f, x.shape
+            ctx.save_for_backward(x2, wg, wu, wd)
+            return f["out"].reshape(x.shape).to(x.dtype)
+
+        @staticmethod
+        def backward(ctx, go):
+            x2, wg, wu, wd = ctx.saved_tensors
+            dx, dwg, dwu, dwd = O.ffn_backward(x2, wg, wu, wd, ctx.f, go.reshape(x2.shape), gcp=True)
+            return (dx.reshape(ctx.shape).to(x2.dtype), dwg.to(wg.dtype), dwu.to(wu.dtype),
+                    dwd.to(wd.dtype), None)
+
+    class OracleFFN(torch.nn.Module):
+        def __init__(self, ffn, k):
+            super().__init__()
+            self.gate_proj, self.up_proj, self.down_proj = ffn.gate_proj, ffn.up_proj, ffn.down_proj
+            self.k = k
+
+        def forward(self, x):
+            return OracleGCP.apply(x, self.gate_proj.weight, self.up_proj.weight,
+                                   self.down_proj.weight, self.k)
+
+    def adamw(params):
+        return torch.optim.AdamW(params, lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0, fused=False)
+
+    torch.manual_seed(1234)
+    cfg = replace(PRESETS["350m"], vocab_size=32100, max_seq_len=256)
+    # one block: fwd + bwd on a [16, 256, d] activation, then its AdamW update
+    blk = TransformerBlock(cfg, ffn_type="dense")
+    blk.ffn = OracleFFN(blk.ffn, cfg.k)
+    opt_b = adamw(blk.parameters())
+    h = torch.randn(16, 256, cfg.hidden_size, generator=torch.Generator().manual_seed(1))
+    h.requires_grad_(True)
+
+    def block_step():
+        blk(h).sum().backward()
+        opt_b.step()
+        opt_b.zero_grad(set_to_none=True)
+
+    t_block, _ = _cpu_time(block_step, reps=2, budget_s=4.0)
+    # the rest: a model with no blocks (embedding, norm, LM head, loss, AdamW)
+    rest = build_model(replace(cfg, num_hidden_layers=0), ffn_type="dense")
+    opt_r = adamw(rest.parameters())
+    tok = torch.randint(0, 32100, (16, 256), generator=torch.Generator().manual_seed(1234))
+
+    def rest_step():
+        _, loss = rest(tok, labels=tok)
+        loss.backward()
+        opt_r.step()
+        opt_r.zero_grad(set_to_none=True)
+
+    t_rest, _ = _cpu_time(rest_step, reps=2, budget_s=4.0)
+    step = t_rest + cfg.num_hidden_layers * t_block
+    return {"value": round(16 * 256 / step, 1), "unit": "tokens/s", "cores": th, "kind": "port",
+            "ms_per_step": round(step * 1e3, 1),
+            "sample": f"350m decoder step, f32, 16x256 tokens: one block (attention + oracle moc_gcp "
+                      f"FFN) fwd+bwd+AdamW {t_block * 1e3:.0f} ms and the rest (embedding, LM head, "
+                      f"loss, AdamW) {t_rest * 1e3:.0f} ms timed; step = rest + "
+                      f"{cfg.num_hidden_layers} x block"}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -488,8 +793,10 @@ def main():
         rows = []
         for row, scope, fuse in (("dense", "whole_graph", False), ("global_moc", "whole_graph", True),
                                  ("global_moc", "whole_graph", False), ("moc_2_8", "whole_graph", True),
-                                 ("moc_2_8", "whole_graph", False), ("dense", "eager", False),
-                                 ("global_moc", "eager", True), ("moc_2_8", "eager", True)):
+                                 ("moc_2_8", "whole_graph", False), ("dense", "layer_graph", False),
+                                 ("global_moc", "layer_graph", True), ("moc_2_8", "layer_graph", True),
+                                 ("dense", "eager", False), ("global_moc", "eager", True),
+                                 ("moc_2_8", "eager", True)):
             log(f"decode e2e {row} {scope} fuse={fuse}")
             rows.append(measure_decode(row, scope=scope, fuse=fuse))
             torch.cuda.empty_cache()
@@ -523,41 +830,80 @@ def main():
     m = build_layer(D1B, I1B, K1B, [w.cuda() for w in ws])
     xd = x.reshape(BATCH1B, SEQ1B, D1B).cuda().requires_grad_(True)
     god = go.reshape(BATCH1B, SEQ1B, D1B).cuda()
-    ms_step, fwd, bwd = time_train_layer(m, xd, god, args.steps, args.warmup)
+    rec, starts = [], []
+    ms_step, fwd, bwd = time_train_layer(m, xd, god, args.steps, args.warmup, probe=rec,
+                                         step_starts=starts)
     log(f"fwd+bwd {ms_step:.3f} ms/step (fwd {fwd['median']:.3f}, bwd {bwd['median']:.3f})")
-    roof = gemm_roofline(t, D1B, I1B, K1B, ws, xd.detach(), god)
-    log(f"GEMMs {roof['gemm_ms_per_step']:.3f} ms, {roof['achieved']} TFLOP/s")
+    inst = in_step_gemm(rec, starts)
+    iso = gemm_roofline(t, D1B, I1B, K1B, ws, xd.detach(), god)
+    log(f"GEMMs in the timed steps {inst['gemm_ms_per_step']:.3f} ms ({inst['achieved']} TFLOP/s), "
+        f"isolated {iso['gemm_ms_per_step']:.3f} ms ({iso['achieved']} TFLOP/s)")
+    roof = {"bound": "mfma", "achieved": inst["achieved"], "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": inst["frac"], "traffic": iso.pop("traffic"),
+            "traffic_note": iso.pop("traffic_note"), "kernel": iso.pop("kernel"),
+            "method": "algorithmic FLOP of the step's nine GEMMs (7 launches) / the time the GPU spent "
+                      "in them inside the timed steps (union of the launch intervals, timing events "
+                      "on each launch's own stream; per_launch: mean bracketed duration, which "
+                      "includes the slowdown of launches that overlap another stream's); "
+                      "`isolated`: the same launches timed back to back",
+            "algorithmic_flop_per_step": inst["algorithmic_flop_per_step"],
+            "gemm_ms_per_step": inst["gemm_ms_per_step"], "per_launch": inst["per_launch"],
+            "isolated": {k: iso[k] for k in ("achieved", "frac", "gemm_ms_per_step", "per_launch")}}
+    gath = gather_report(xd.detach(), m.gate_proj.weight.detach(), K1B)
+    log(f"gather report: union share {gath['union_share_of_channels']}")
     del m, xd, god
     torch.cuda.empty_cache()
 
-    extra = {"fwd_ms": summarize_round(fwd), "bwd_ms": summarize_round(bwd)}
+    configs = {}
     log("decode B=1")
-    dec = [decode_bench(1, groups=args.decode_groups, iters=args.decode_iters)]
-    d1 = dec[0]
+    dec = {1: decode_bench(1, groups=args.decode_groups, iters=args.decode_iters)}
+    d1 = dec[1]
     roof_dec = {"bound": "hbm", "achieved": d1["achieved_GBs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": d1["frac_hbm"], "traffic": DECODE_B1_TRAFFIC_BYTES,
                 "kernel": "decode layer (gate GEMV + Top-K + selected Up + selected Down), B=1",
                 "us": d1["us_median"], "bytes": d1["bytes"]}
+    cpu_on = not args.no_cpu_baseline
     if not args.skip_extra:
-        for nb in (4, 16):
-            log(f"decode B={nb}")
-            dec.append(decode_bench(nb, groups=args.decode_groups, iters=args.decode_iters))
-        log("2:8 prefill")
-        extra["moc28_prefill_4096"] = moc28_prefill_bench()
-        log("130m MoC+GCP fwd+bwd")
+        log("config 1: 60m fp32 MoC forward")
+        configs["1_60m_moc_fwd_f32"] = cfg1_bench()
+        log("config 2: 130m MoC+GCP fwd+bwd")
         x2, wg2, wu2, wd2, go2 = seeded_inputs(8 * 1024, 768, 2048)
         m2 = build_layer(768, 2048, 384, [w.cuda() for w in (wg2, wu2, wd2)])
         x2d = x2.reshape(8, 1024, 768).cuda().requires_grad_(True)
-        ms2, f2, b2 = time_train_layer(m2, x2d, go2.reshape(8, 1024, 768).cuda(), 20, 5)
+        go2d = go2.reshape(8, 1024, 768).cuda()
+        ms2, f2, b2 = time_train_layer(m2, x2d, go2d, 20, 5)
+        rec2, starts2 = [], []  # GEMM durations from 3 more steps (the probe costs host time here)
+        time_train_layer(m2, x2d, go2d, 3, 1, probe=rec2, step_starts=starts2)
         flop2 = 9 * 2 * 8192 * 768 * 2048
-        extra["cfg2_130m_fwd_bwd"] = {"us": round(ms2 * 1e3, 1),
-                                      "tflops_gemm_equiv": round(flop2 / (ms2 * 1e-3) / 1e12, 1)}
-        del m2, x2d
-    extra["decode"] = dec
+        tf2 = flop2 / (ms2 * 1e-3) / 1e12
+        configs["2_130m_moc_gcp_fwd_bwd"] = {
+            "us": round(ms2 * 1e3, 1), "fwd_us": round(f2["median"] * 1e3, 1),
+            "bwd_us": round(b2["median"] * 1e3, 1), "tokens_per_s": round(8192 / (ms2 * 1e-3), 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf2, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf2 / BF16_PEAK_TFLOPS, 4),
+                         "algorithmic_gflop": round(flop2 / 1e9, 1),
+                         "gemm_in_step": in_step_gemm(rec2, starts2)}}
+        del m2, x2d, go2d
+        for nb in (4, 16):
+            log(f"decode B={nb}")
+            dec[nb] = decode_bench(nb, groups=args.decode_groups, iters=args.decode_iters)
+        configs["3_decode_1b"] = {f"B{nb}": {**r, "tokens_per_s": round(nb / (r["us_median"] * 1e-6), 1)}
+                                  for nb, r in dec.items()}
+        log("config 4: 2:8 prefill")
+        configs["4_moc28_prefill_4096"] = moc28_prefill_bench()
+        log("config 5: 350m training step")
+        configs["5_350m_step"] = cfg5_bench(args.cfg5_steps)
+        if cpu_on:
+            log("cpu baselines of configs 1-5")
+            configs["1_60m_moc_fwd_f32"]["cpu_baseline"] = cpu_cfg1()
+            configs["2_130m_moc_gcp_fwd_bwd"]["cpu_baseline"] = cpu_cfg2()
+            configs["3_decode_1b"]["cpu_baseline"] = {f"B{nb}": cpu_decode(nb) for nb in (1, 4, 16)}
+            configs["4_moc28_prefill_4096"]["cpu_baseline"] = cpu_cfg4()
+            configs["5_350m_step"]["cpu_baseline"] = cpu_cfg5()
 
     cpu = None
-    if not args.no_cpu_baseline:
-        log("cpu baseline")
+    if cpu_on:
+        log("cpu baseline (headline)")
         cpu = cpu_baseline(args.cpu_seconds)
 
     out = {
@@ -570,7 +916,9 @@ def main():
                    "batch": BATCH1B, "seq_len": SEQ1B, "hidden": D1B, "intermediate": I1B,
                    "k": K1B, "parallelism": "none (one GPU)"},
         "tokens_per_s": round(t / (ms_step * 1e-3), 1),
-        "roofline": roof, "roofline_decode": roof_dec, "cpu_baseline": cpu, "extra": extra,
+        "fwd_ms": summarize_round(fwd), "bwd_ms": summarize_round(bwd),
+        "roofline": roof, "roofline_decode": roof_dec, "cpu_baseline": cpu, "configs": configs,
+        "gemm_flop_executed_vs_algorithmic": gath,
         "device": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)

@@ -57,6 +57,29 @@ __global__ void copy_pad_2d_kernel(const T* __restrict__ src, int64_t rows, int6
   }
 }
 
+// bf16 copy into 16-byte aligned destination rows (dst_ld a multiple of 8):
+// row blockIdx.y, each thread one 8-element chunk of it, written with one
+// 16-byte store; the source (any alignment) is read element by element,
+// coalesced across the threads of the row.
+__global__ __launch_bounds__(256) void copy_pad_rows16_kernel(const uint16_t* __restrict__ src,
+                                                              int64_t cols, int64_t src_ld,
+                                                              uint16_t* __restrict__ dst,
+                                                              int64_t dst_ld, int64_t dst_cols) {
+  const int64_t r = blockIdx.y;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+  if (c0 >= dst_cols) return;
+  const uint16_t* s = src + r * src_ld;
+  uint16_t v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = (c0 + j < cols) ? s[c0 + j] : uint16_t(0);
+  uint4 o;
+  o.x = v[0] | (uint32_t(v[1]) << 16);
+  o.y = v[2] | (uint32_t(v[3]) << 16);
+  o.z = v[4] | (uint32_t(v[5]) << 16);
+  o.w = v[6] | (uint32_t(v[7]) << 16);
+  *reinterpret_cast<uint4*>(dst + r * dst_ld + c0) = o;
+}
+
 }  // namespace
 }  // namespace moc
 
@@ -91,6 +114,13 @@ extern "C" int moc_copy_pad_2d(int dtype, const void* src, int64_t rows, int64_t
   if (blocks > 8192) blocks = 8192;
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
   hipStream_t st = as_stream(stream);
+  if (dtype == MOC_BF16 && dst_ld % 8 == 0 && dst_cols % 8 == 0 && aligned16(dst) && rows <= 65535) {
+    const int64_t chunks = dst_cols / 8;
+    const dim3 g2(static_cast<unsigned>((chunks + 255) / 256), static_cast<unsigned>(rows));
+    copy_pad_rows16_kernel<<<g2, 256, 0, st>>>(static_cast<const uint16_t*>(src), cols, src_ld,
+                                              static_cast<uint16_t*>(dst), dst_ld, dst_cols);
+    return check_launch("copy_pad_rows16_kernel");
+  }
   if (dtype == MOC_BF16)
     copy_pad_2d_kernel<uint16_t><<<grid, block, 0, st>>>(static_cast<const uint16_t*>(src), rows,
                                                          cols, src_ld, static_cast<uint16_t*>(dst),

@@ -8,9 +8,14 @@ gate/up + top-2-of-8 -> selected Down).  A step embeds one token, runs every
 layer (x + attn(norm(x)), x + ffn(norm(x))) against a static KV cache and
 returns the logits; the token is the argmax of the logits, outside the step.
 
-Scopes: "eager" (every kernel launched from Python) and "whole_graph" (the
-whole step captured once in a HIP graph over persistent token/position
-buffers and replayed per token: benchmark_decode.py:549-617).
+Scopes: "eager" (every kernel launched from Python), "layer_graph" (each
+decoder layer captured in its own HIP graph over persistent activation
+buffers, replayed layer by layer; embedding and LM head eager: the per-layer
+graph runners of benchmark_decode.py:461-499) and "whole_graph" (the whole
+step captured once in a HIP graph over persistent token/position buffers and
+replayed per token: benchmark_decode.py:549-617).  The reference's
+torch.compile scope (:423-459) is not offered: Inductor would generate
+Triton kernels for the host's attention, which this build does not use.
 
 Attention, RMSNorm, RoPE, the embedding and the LM head are stock PyTorch
 (the host of the FFN).  Attention keeps K transposed in its cache
@@ -236,6 +241,8 @@ def make_step(model: DecoderModel, scope: str) -> Callable[[torch.Tensor, int], 
             pos.fill_(p)
             return model.forward_step(tokens, pos)
         return step
+    if scope == "layer_graph":
+        return _layer_graph_step(model, pos)
     if scope != "whole_graph":
         raise ValueError(f"unknown scope {scope!r}")
     model.freeze_for_compile()
@@ -258,6 +265,47 @@ def make_step(model: DecoderModel, scope: str) -> Callable[[torch.Tensor, int], 
         return logits
 
     step.graph = graph
+    return step
+
+
+def _layer_graph_step(model: DecoderModel, pos: torch.Tensor) -> Callable[[torch.Tensor, int], torch.Tensor]:
+    """One HIP graph per decoder layer: layer i reads xs[i] and writes
+    xs[i + 1]; the graphs share one memory pool and replay in order."""
+    dev = model.embed.weight.device
+    model.freeze_for_compile()
+    h = model.cfg.hidden
+    xs = [torch.zeros(1, 1, h, dtype=model.embed.weight.dtype, device=dev)
+          for _ in range(len(model.layers) + 1)]
+
+    def run_layer(i, layer):
+        xs[i + 1].copy_(layer.forward_step(xs[i], pos))
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side), torch.no_grad():
+        for _ in range(3):
+            for i, layer in enumerate(model.layers):
+                run_layer(i, layer)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    pool = torch.cuda.graph_pool_handle()
+    graphs = []
+    with torch.no_grad():
+        for i, layer in enumerate(model.layers):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                run_layer(i, layer)
+            graphs.append(g)
+
+    @torch.no_grad()
+    def step(tokens: torch.Tensor, p: int) -> torch.Tensor:
+        pos.fill_(p)
+        xs[0].copy_(model.embed(tokens))
+        for g in graphs:
+            g.replay()
+        return model.lm_head(model.final_norm(xs[-1]))
+
+    step.graphs = graphs
     return step
 
 

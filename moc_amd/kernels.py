@@ -277,6 +277,34 @@ def _operand(t: torch.Tensor, bf16: bool) -> tuple[torch.Tensor, int, int]:
 
 _GEMM_WS: dict = {}
 
+# Optional timing probe: when a list is installed with set_gemm_probe(), every
+# GEMM launch made through gemm() / linear_pair() is bracketed by two timing
+# events on the stream it runs on and recorded as (events, FLOP), so a
+# harness can sum the GEMM time inside a real training step.
+_GEMM_PROBE: list | None = None
+
+
+def set_gemm_probe(records: list | None) -> None:
+    """Install (a list) or remove (None) the GEMM timing probe."""
+    global _GEMM_PROBE
+    _GEMM_PROBE = records
+
+
+def _probe_begin():
+    if _GEMM_PROBE is None:
+        return None
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record()
+    return ev
+
+
+def _probe_end(ev, name: str, flop: float) -> None:
+    if ev is None:
+        return
+    end = torch.cuda.Event(enable_timing=True)
+    end.record()
+    _GEMM_PROBE.append((name, ev, end, flop))
+
 
 def _gemm_workspace(device, nbytes: int) -> torch.Tensor:
     """The GEMM workspace of the current stream on `device`, grown on demand.
@@ -331,9 +359,11 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
     if bf16 and gemm_tiles(M, Nn) < cu_count(a.get_device()):
         ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2)
     ws = _gemm_workspace(a.device, ws_bytes) if ws_bytes > 0 else None
+    probe = _probe_begin()
     N.call("moc_gemm_ws", code, M, Nn, K, aa.data_ptr(), as0, as1, bb.data_ptr(),
            bs0, bs1, K2, N.ptr(a2p), a2s0, a2s1, N.ptr(b2p), b2s0, b2s1, out.data_ptr(), ldc,
            N.dtype_code(out_dtype), N.ptr(ws), ws_bytes, N.stream_of(a))
+    _probe_end(probe, f"gemm {M}x{Nn}x{K}" + (f"+{K2}" if K2 else ""), 2.0 * M * Nn * (K + K2))
     return out
 
 
@@ -374,9 +404,11 @@ def linear_pair(x2d: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, *,
             ws_bytes = max(ws_bytes, N.query("moc_gemm_workspace_size", N.dtype_code(torch.bfloat16),
                                              M, n, Kd, 0))
     ws = _gemm_workspace(x2d.device, ws_bytes) if ws_bytes > 0 else None
+    probe = _probe_begin()
     N.call("moc_gemm_pair", M, Kd, xa.data_ptr(), lda, wa.data_ptr(), ld1, n1, outs[0].data_ptr(),
            ldc[0], wb.data_ptr(), ld2, n2, outs[1].data_ptr(), ldc[1], N.ptr(ws), ws_bytes,
            N.stream_of(x2d))
+    _probe_end(probe, f"gemm pair {M}x({n1}+{n2})x{Kd}", 2.0 * M * Kd * (n1 + n2))
     return outs[0], outs[1]
 
 

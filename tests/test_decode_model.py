@@ -68,9 +68,12 @@ def test_decode_graph_matches_eager(row):
     prompt = torch.randint(0, cfg.vocab, (1, 24), generator=torch.Generator().manual_seed(8)).to(DEV)
     eager = make_step(m, "eager")
     graph = make_step(m, "whole_graph")
+    layer_graph = make_step(m, "layer_graph")
     _, toks_e = run_decode(m, prompt, 8, eager)
     _, toks_g = run_decode(m, prompt, 8, graph)
+    _, toks_l = run_decode(m, prompt, 8, layer_graph)
     assert torch.equal(toks_e, toks_g)
+    assert torch.equal(toks_e, toks_l)
     # one step from the same cache state: identical logits
     m.reset_cache()
     m.forward_prompt(prompt)
@@ -79,7 +82,11 @@ def test_decode_graph_matches_eager(row):
     m.reset_cache()
     m.forward_prompt(prompt)
     lg = graph(cur, 24).clone()
+    m.reset_cache()
+    m.forward_prompt(prompt)
+    ll = layer_graph(cur, 24).clone()
     torch.cuda.synchronize()
+    assert torch.allclose(le.float(), ll.float(), atol=2e-2, rtol=2e-2)
     assert bool(torch.isfinite(le.float()).all())
     # the same kernels on the same inputs; allow library GEMMs that split K
     # with atomics their last-bit differences

@@ -70,6 +70,21 @@ def close(a, b, rtol=2e-2, atol=2e-2):
     assert not bool(bad.any()), f"max err {err.max().item():.4g} at {torch.nonzero(bad)[:4].tolist()}"
 
 
+@pytest.mark.parametrize("rows,cols,off", [(2048, 5461, 0), (3, 13, 1), (17, 1000, 3), (1, 7, 5)])
+def test_aligned_rows_copy(rows, cols, off):
+    """aligned_rows() of a matrix whose rows are not 16-byte aligned (a view
+    starting `off` elements into its storage): the padded copy holds the
+    values and zero pad columns."""
+    g = gen(rows + cols)
+    base = torch.randn(rows * cols + off, generator=g).to(torch.bfloat16).to(DEV)
+    t = base[off:].view(rows, cols)
+    a = K().aligned_rows(t)
+    assert a.stride(0) % 8 == 0 and a.data_ptr() % 16 == 0
+    assert torch.equal(a, t)
+    full = a.as_strided((rows, a.stride(0)), (a.stride(0), 1))
+    assert not bool(full[:, cols:].any())
+
+
 # ----------------------------------------------------------------------- GEMM
 @pytest.mark.parametrize("a_kc", [True, False])
 @pytest.mark.parametrize("b_kc", [True, False])
@@ -613,3 +628,28 @@ def test_after_gate_selection_bitexact(nb, kind):
     vals = O.gather_rows(G, idx_ref)
     z_ref = O.selected_up_silu(x, vals, idx_ref, wu)
     close(y, O.selected_down(z_ref, idx_ref, wdt))
+
+
+@pytest.mark.parametrize("hidden,inter,k", [(512, 100, 7), (1024, 2736, 512), (4096, 16384, 4000),
+                                            (2048, 5461, 1), (2048, 5461, 5461), (1536, 777, 300),
+                                            (768, 777, 300)])
+def test_after_gate_one_token_shapes(hidden, inter, k):
+    """One token over the channel-range form (hidden a multiple of 512 up to
+    4096; ranges of up to 64 channels) and, for hidden 768, the general
+    form: selection bit-exact, y within 2e-2 of the oracle on that
+    selection, residual form equal to the bf16 add."""
+    g = gen(inter + k)
+    G = tie_heavy_rows(1, inter, "gauss", inter)
+    x = torch.randn(1, hidden, generator=g).to(torch.bfloat16)
+    wu = (torch.randn(inter, hidden, generator=g) * 0.02).to(torch.bfloat16)
+    wdt = (torch.randn(inter, hidden, generator=g) * 0.02).to(torch.bfloat16)
+    res = torch.randn(1, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    idx_ref = O.topk_indices(G, k)
+    io = torch.full((1, k), -1, dtype=torch.int32, device=DEV)
+    xd, Gd, wud, wdtd = x.to(DEV), G.to(DEV), wu.to(DEV), wdt.to(DEV)
+    y = K().global_after_gate(xd, Gd, wud, wdtd, k, idx_out=io)
+    assert np.array_equal(io.cpu().numpy(), idx_ref)
+    z_ref = O.selected_up_silu(x, O.gather_rows(G, idx_ref), idx_ref, wu)
+    close(y, O.selected_down(z_ref, idx_ref, wdt))
+    yr = K().global_after_gate(xd, Gd, wud, wdtd, k, residual=res)
+    assert torch.equal(yr, res + y)
