@@ -1079,6 +1079,140 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgsF32 g) {
     }
 }
 
+// f32 tiled path: 64x64 tile, 256 threads x (4x4) outputs, K step 32,
+// operands loaded as float4 along their contiguous dimension (K or M/N),
+// the next step's loads issued into registers before this step's FMAs,
+// two LDS stages.  The K range (both products concatenated, the first's K a
+// multiple of 32) can be split over gridDim.z workgroups: split z adds
+// [z kchunk, (z+1) kchunk) and writes its f32 partial tile to ws + z stride,
+// summed in split order by splitk_reduce_kernel.  KC: operand contiguous
+// along K; else along M (A) or N (B).
+constexpr int kF32BM = 64, kF32BK = 32, kF32Pad = 68;
+
+struct F32Step {
+  float4 a[2], b[2];
+};
+
+template <bool KC>
+__device__ __forceinline__ float4 f32_load4(const float* p, int64_t s_row, int64_t s_k, int row, int rows,
+                                           int k, int K) {
+  // four consecutive elements along the contiguous dimension, masked
+  float v[4];
+  if (KC) {
+    const float* q = p + static_cast<int64_t>(row) * s_row + k;
+    if (row < rows && k + 4 <= K) return *reinterpret_cast<const float4*>(q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (row < rows && k + e < K) ? q[e] : 0.f;
+  } else {
+    const float* q = p + static_cast<int64_t>(k) * s_k + row;
+    if (k < K && row + 4 <= rows) return *reinterpret_cast<const float4*>(q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (k < K && row + e < rows) ? q[e] : 0.f;
+  }
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <bool A_KC, bool B_KC>
+__device__ __forceinline__ void f32_load_step(F32Step& L, const GemmArgsF32& g, int k0, int m0, int n0) {
+  const int t = threadIdx.x;
+  const bool p2 = k0 >= g.K1;
+  const float* A = p2 ? g.A2 : g.A1;
+  const float* B = p2 ? g.B2 : g.B1;
+  const int K = p2 ? g.K2 : g.K1;
+  const int k = p2 ? k0 - g.K1 : k0;
+  const int64_t am = p2 ? g.a2m : g.a1m, ak = p2 ? g.a2k : g.a1k;
+  const int64_t bk = p2 ? g.b2k : g.b1k, bn = p2 ? g.b2n : g.b1n;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = t + 256 * h;  // 512 float4 per operand tile
+    if (A_KC) L.a[h] = f32_load4<true>(A, am, ak, m0 + q / 8, g.M, k + (q % 8) * 4, K);
+    else L.a[h] = f32_load4<false>(A, am, ak, m0 + (q % 16) * 4, g.M, k + q / 16, K);
+    if (B_KC) L.b[h] = f32_load4<true>(B, bn, bk, n0 + q / 8, g.N, k + (q % 8) * 4, K);
+    else L.b[h] = f32_load4<false>(B, bn, bk, n0 + (q % 16) * 4, g.N, k + q / 16, K);
+  }
+}
+
+// LDS: As[k][m], Bs[k][n] (row pitch kF32Pad floats)
+template <bool A_KC, bool B_KC>
+__device__ __forceinline__ void f32_store_step(const F32Step& L, float* As, float* Bs) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = t + 256 * h;
+    const float a[4] = {L.a[h].x, L.a[h].y, L.a[h].z, L.a[h].w};
+    const float b[4] = {L.b[h].x, L.b[h].y, L.b[h].z, L.b[h].w};
+    if (A_KC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) As[((q % 8) * 4 + e) * kF32Pad + q / 8] = a[e];
+    } else {
+      *reinterpret_cast<float4*>(As + (q / 16) * kF32Pad + (q % 16) * 4) = L.a[h];
+    }
+    if (B_KC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Bs[((q % 8) * 4 + e) * kF32Pad + q / 8] = b[e];
+    } else {
+      *reinterpret_cast<float4*>(Bs + (q / 16) * kF32Pad + (q % 16) * 4) = L.b[h];
+    }
+  }
+}
+
+template <bool A_KC, bool B_KC>
+__global__ __launch_bounds__(256) void gemm_f32_tiled_kernel(GemmArgsF32 g, int kchunk, float* ws,
+                                                             int64_t ws_stride, int64_t ldw) {
+  __shared__ __attribute__((aligned(16))) float As[2][kF32BK * kF32Pad];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kF32BK * kF32Pad];
+  const int tid = threadIdx.x;
+  const int tr = tid / 16, tc = tid % 16;
+  const int m0 = blockIdx.y * kF32BM, n0 = blockIdx.x * kF32BM;
+  const int ktot = g.K1 + g.K2;
+  const int klo = blockIdx.z * kchunk;
+  const int khi = min(ktot, klo + kchunk);
+  float acc[4][4] = {};
+  F32Step L;
+  if (klo < khi) {
+    f32_load_step<A_KC, B_KC>(L, g, klo, m0, n0);
+    f32_store_step<A_KC, B_KC>(L, As[0], Bs[0]);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = klo; k0 < khi; k0 += kF32BK) {
+    const bool more = k0 + kF32BK < khi;
+    if (more) f32_load_step<A_KC, B_KC>(L, g, k0 + kF32BK, m0, n0);
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll 8
+    for (int kk = 0; kk < kF32BK; ++kk) {
+      const float4 a4 = *reinterpret_cast<const float4*>(as + kk * kF32Pad + tr * 4);
+      const float4 b4 = *reinterpret_cast<const float4*>(bs + kk * kF32Pad + tc * 4);
+      const float a[4] = {a4.x, a4.y, a4.z, a4.w};
+      const float b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    if (more) f32_store_step<A_KC, B_KC>(L, As[buf ^ 1], Bs[buf ^ 1]);
+    __syncthreads();
+    buf ^= 1;
+  }
+  float* dst = ws ? ws + blockIdx.z * ws_stride : g.C;
+  const int64_t ld = ws ? ldw : g.ldc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = m0 + tr * 4 + i, c = n0 + tc * 4 + j;
+      if (r < g.M && c < g.N) dst[static_cast<int64_t>(r) * ld + c] = acc[i][j];
+    }
+}
+
+// Split of an f32 GEMM over K: workgroups for about two per CU when the
+// tiles alone leave CUs idle, with at least two K steps per split.
+struct F32Split {
+  int ksplit, kchunk;
+  int64_t ldw, bytes;
+};
+
 template <bool A_KC, bool B_KC>
 void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st) {
   const int64_t units = a.fix_tail > 0 ? a.fix_full + 2 * static_cast<int64_t>(a.fix_tail)
@@ -1141,6 +1275,26 @@ int cu_count() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+F32Split plan_f32(int64_t M, int64_t N, int64_t K, int64_t K2) {
+  F32Split p{1, 0, 0, 0};
+  const int64_t ktot = K + K2;
+  const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + kF32BM - 1) / kF32BM);
+  const int64_t steps = (ktot + kF32BK - 1) / kF32BK;
+  p.kchunk = static_cast<int>(steps * kF32BK);
+  const int64_t want = 2 * static_cast<int64_t>(cu_count());
+  if (tiles >= want || steps < 4) return p;
+  int64_t ks = (want + tiles - 1) / tiles;
+  if (ks > steps / 2) ks = steps / 2;
+  if (ks > 16) ks = 16;
+  if (ks < 2) return p;
+  const int64_t per = (steps + ks - 1) / ks;
+  p.kchunk = static_cast<int>(per * kF32BK);
+  p.ksplit = static_cast<int>((steps + per - 1) / per);
+  p.ldw = (N + 3) / 4 * 4;
+  p.bytes = static_cast<int64_t>(p.ksplit) * M * p.ldw * 4;
+  return p;
 }
 
 // Split-K plan of a bf16 GEMM: a product whose 256x256 tiles fill at most a
@@ -1251,7 +1405,14 @@ int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* w
 using namespace moc;
 
 extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2) {
-  if (dtype != MOC_BF16 || M <= 0 || N <= 0 || K < 0 || K2 < 0) return 0;
+  if (M <= 0 || N <= 0 || K < 0 || K2 < 0) return 0;
+  if (dtype == MOC_F32) {
+    // f32 partial tiles after the counter block the bf16 forms keep zero
+    if (K2 > 0 && K % kF32BK != 0) return 0;
+    const int64_t b = plan_f32(M, N, K, K2).bytes;
+    return b > 0 ? MOC_GEMM_WS_COUNTER_BYTES + b : 0;
+  }
+  if (dtype != MOC_BF16) return 0;
   const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
   return std::max(plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes);
 }
@@ -1350,8 +1511,51 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
                   b2_sk, b2_sn, (float*)C, ldc};
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     MOC_REQUIRE(grid.y <= 65535, "moc_gemm: M too large for the f32 grid");
-    gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
-    return check_launch("gemm_f32_kernel");
+    // tiled path: each operand contiguous along K or along M/N with 16-byte
+    // rows, both products with the same layouts, the first product's K a
+    // multiple of the K step when there is a second
+    auto f32_layout = [](const void* p, int64_t s_mn, int64_t s_k) -> int {
+      if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return -1;
+      if (s_k == 1 && s_mn % 4 == 0) return 1;  // KC
+      if (s_mn == 1 && s_k % 4 == 0) return 0;  // MN
+      return -1;
+    };
+    int la = K > 0 ? f32_layout(A, a_sm, a_sk) : 1, lb = K > 0 ? f32_layout(B, b_sn, b_sk) : 1;
+    if (second) {
+      if (f32_layout(A2, a2_sm, a2_sk) != la || f32_layout(B2, b2_sn, b2_sk) != lb || K % kF32BK != 0)
+        la = -1;
+    }
+    if (la < 0 || lb < 0 || K + (second ? K2 : 0) == 0) {
+      gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
+      return check_launch("gemm_f32_kernel");
+    }
+    F32Split sp = plan_f32(M, N, K, second ? K2 : 0);
+    float* ws = nullptr;
+    if (sp.ksplit > 1) {
+      if (workspace != nullptr && workspace_bytes >= MOC_GEMM_WS_COUNTER_BYTES + sp.bytes &&
+          reinterpret_cast<uintptr_t>(workspace) % 16 == 0) {
+        ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + MOC_GEMM_WS_COUNTER_BYTES);
+      } else {  // no room for partial tiles: one workgroup per tile
+        sp.ksplit = 1;
+        sp.kchunk = static_cast<int>((K + (second ? K2 : 0) + kF32BK - 1) / kF32BK * kF32BK);
+      }
+    }
+    const dim3 g3(grid.x, grid.y, static_cast<unsigned>(sp.ksplit));
+    const int64_t stride = M * sp.ldw;
+#define MOC_F32T(AK, BK)                                                                          \
+  gemm_f32_tiled_kernel<AK, BK><<<g3, 256, 0, st>>>(a, sp.kchunk, ws, stride, sp.ldw)
+    if (la == 1 && lb == 1) MOC_F32T(true, true);
+    else if (la == 1) MOC_F32T(true, false);
+    else if (lb == 1) MOC_F32T(false, true);
+    else MOC_F32T(false, false);
+#undef MOC_F32T
+    int rc = check_launch("gemm_f32_tiled_kernel");
+    if (rc != MOC_OK || ws == nullptr) return rc;
+    const int64_t quads = M * ((N + 3) / 4);
+    const int vec = (reinterpret_cast<uintptr_t>(C) % 16 == 0 && ldc % 4 == 0) ? 1 : 0;
+    splitk_reduce_kernel<true><<<dim3(static_cast<unsigned>((quads + 255) / 256)), 256, 0, st>>>(
+        ws, stride, sp.ksplit, (int)M, (int)N, sp.ldw, C, ldc, vec);
+    return check_launch("splitk_reduce_kernel (f32)");
   }
 
   MOC_REQUIRE(c_dtype == MOC_BF16 || c_dtype == MOC_F32, "moc_gemm: bad output dtype");

@@ -354,9 +354,9 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
     ldc = out.stride(0) if M > 1 else max(Nn, 1)
     code = N.dtype_code(a.dtype)
     # products with fewer tiles than CUs split K over a workspace of f32
-    # partial tiles
+    # partial tiles (f32 GEMMs decide inside the library)
     ws_bytes = 0
-    if bf16 and gemm_tiles(M, Nn) < cu_count(a.get_device()):
+    if not bf16 or gemm_tiles(M, Nn) < cu_count(a.get_device()):
         ws_bytes = N.query("moc_gemm_workspace_size", code, M, Nn, K, K2)
     ws = _gemm_workspace(a.device, ws_bytes) if ws_bytes > 0 else None
     probe = _probe_begin()

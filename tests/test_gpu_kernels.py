@@ -289,6 +289,36 @@ def test_gemm_dual_product_and_f32():
     close(f32, ref, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("layout", ["kckc", "kcmn", "mnkc", "mnmn"])
+@pytest.mark.parametrize("mnk", [(512, 1376, 512), (512, 512, 1376), (67, 45, 130), (1, 5, 7),
+                                 (300, 260, 64)])
+def test_gemm_f32_tiled(layout, mnk):
+    """The f32 GEMM (64x64 tiles, K split over f32 partials summed in a fixed
+    order when the tiles leave CUs idle) in all four operand layouts,
+    against float64; repeat calls are identical."""
+    M, Nn, Kk = mnk
+    g = gen(M * 7 + Nn + Kk)
+    a, b = torch.randn(M, Kk, generator=g), torch.randn(Kk, Nn, generator=g)
+    ref = (a.double() @ b.double()).float()
+    ad = a.to(DEV) if layout[:2] == "kc" else a.t().contiguous().t().to(DEV)
+    bd = b.t().contiguous().t().to(DEV) if layout[2:] == "kc" else b.to(DEV)
+    if layout[2:] == "kc":
+        bd = b.t().contiguous().to(DEV).t()
+    got = K().gemm(ad, bd)
+    close(got, ref, rtol=1e-5, atol=1e-5 * (Kk ** 0.5) * 4)
+    assert torch.equal(K().gemm(ad, bd), got)
+
+
+def test_gemm_f32_dual_product_tiled():
+    """dX-shaped f32 sum of two products (first K a multiple of the K step)."""
+    g = gen(5)
+    a, a2 = torch.randn(200, 64, generator=g), torch.randn(200, 40, generator=g)
+    b, b2 = torch.randn(64, 96, generator=g), torch.randn(40, 96, generator=g)
+    ref = (a.double() @ b.double() + a2.double() @ b2.double()).float()
+    got = K().gemm(a.to(DEV), b.to(DEV), a2=a2.to(DEV), b2=b2.to(DEV))
+    close(got, ref, rtol=1e-5, atol=1e-4)
+
+
 # ---------------------------------------------------------------------- Top-K
 @pytest.mark.parametrize("name", ["topk_bf16_ties", "topk_bf16_rand"])
 def test_topk_golden_bitexact(name):
