@@ -43,8 +43,11 @@ def _check_topk(scores: torch.Tensor, k: int) -> None:
 def value_order(vals: torch.Tensor, idx: torch.Tensor):
     """(vals, idx) of a selection in ascending channel order -> the same
     pairs ordered by value descending, equal values by ascending channel (a
-    stable sort keeps the channel order among equal values)."""
-    order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
+    stable sort keeps the channel order among equal values).  The sort key
+    is vals + 0.0 in f32, which turns -0.0 into +0.0, so the two zeros rank
+    equal whatever the sort's key encoding; NaN sorts above +inf."""
+    keys = vals.float() + 0.0
+    order = torch.sort(keys, dim=-1, descending=True, stable=True).indices
     return torch.gather(vals, -1, order), torch.gather(idx, -1, order)
 
 

@@ -247,6 +247,53 @@ def test_inference_global_modes(nb):
         close(yr, y, 0, 0, "graph replay")
 
 
+@pytest.mark.parametrize("nb", [1, 4, 16])
+def test_extension_object_runner_shape(nb):
+    """The reference benchmark's fixed-graph runner
+    (benchmark_ffn_latency.py:120-142): gate projection by the module, then
+    ext.cub_topk_bf16_512x11 -> ext.selected_up_silu_bf16 ->
+    ext.selected_down_bf16_h32_k16 on the extension object, and the one-call
+    ext.optimized_global_after_gate_bf16, against the oracle at the 1b shape.
+    The Top-K must select the oracle's channels bit for bit and return them
+    in value order (descending, ties by ascending channel)."""
+    from moc_amd.inference.inference_ffn import InferenceMoCSwiGLUFFN
+    from moc_amd.inference.optimized_global_moc_ops import load_optimized_global_moc_extension
+    ext = load_optimized_global_moc_extension()
+    d, inter, k = 2048, 5461, 1024
+    m = InferenceMoCSwiGLUFFN(d, inter, k).to(DEV, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(700 + nb)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
+    m._ensure_down_weight_t()
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    up_w, down_t = m.up_proj.weight.contiguous(), m._down_weight_t.contiguous()
+    with torch.no_grad():
+        gate = m.gate_proj(x).contiguous()
+    vals, idx = ext.cub_topk_bf16_512x11(gate, k)
+    sz = ext.selected_up_silu_bf16(x, vals.contiguous(), idx.contiguous(), up_w)
+    y = ext.selected_down_bf16_h32_k16(sz.contiguous(), idx.contiguous(), down_t)
+    G = gate.cpu()
+    idx_ref = O.topk_indices(G, k)  # ascending channel order
+    idx_c = idx.cpu()
+    assert np.array_equal(np.sort(idx_c.numpy(), axis=1), idx_ref)
+    v = vals.cpu().float()
+    assert torch.equal(v, G.float().gather(1, idx_c))
+    # value order: descending values, equal values by ascending channel
+    step_down = v[:, 1:] < v[:, :-1]
+    tie_up = (v[:, 1:] == v[:, :-1]) & (idx_c[:, 1:] > idx_c[:, :-1])
+    assert bool((step_down | tie_up).all())
+    vals_ref = O.gather_rows(G, idx_ref)
+    z_ref = O.selected_up_silu(x.cpu(), vals_ref, idx_ref, m.up_proj.weight.cpu())
+    order = np.argsort(idx_c.numpy(), axis=1, kind="stable")
+    close(torch.from_numpy(np.take_along_axis(sz.float().cpu().numpy(), order, 1)), z_ref,
+          2e-2, 2e-2, "sparse z")
+    y_ref = O.selected_down(z_ref, idx_ref, down_t.cpu())
+    close(y, y_ref, 2e-2, 2e-2, "runner y")
+    y1 = ext.optimized_global_after_gate_bf16(x, gate, up_w, down_t, k)
+    close(y1, y_ref, 2e-2, 2e-2, "after_gate y")
+
+
 @pytest.mark.parametrize("nb", [1, 64, 4096])
 def test_inference_moc28_modes(nb):
     """InferenceMoCSwiGLUFFN in MoC 2:8 mode (config 4 at nb = 4096) against

@@ -664,10 +664,10 @@ def test_after_gate_selection_bitexact(nb, kind):
                                             (2048, 5461, 1), (2048, 5461, 5461), (1536, 777, 300),
                                             (768, 777, 300)])
 def test_after_gate_one_token_shapes(hidden, inter, k):
-    """One token over the channel-range form (hidden a multiple of 512 up to
-    4096; ranges of up to 64 channels) and, for hidden 768, the general
-    form: selection bit-exact, y within 2e-2 of the oracle on that
-    selection, residual form equal to the bf16 add."""
+    """One token at shapes other than the 1b one (small and wide rows, k of
+    1 and of every channel, hidden not a multiple of the 256-column block):
+    selection bit-exact, y within 2e-2 of the oracle on that selection,
+    residual form equal to the bf16 add."""
     g = gen(inter + k)
     G = tie_heavy_rows(1, inter, "gauss", inter)
     x = torch.randn(1, hidden, generator=g).to(torch.bfloat16)

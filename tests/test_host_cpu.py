@@ -183,6 +183,10 @@ def test_value_order_is_stable_descending():
     v, i = value_order(vals, idx)
     assert i.tolist() == [[2, 5, 9, 0, 7, 8]]
     assert v.float().tolist() == [[3.0, 3.0, 2.0, 1.0, -0.0, 0.0]]
+    # the two zeros rank equal in either order; NaN ranks above +inf
+    z = torch.tensor([[0.0, -0.0, float("inf"), float("nan")], [-0.0, 0.0, 1.0, -1.0]]).bfloat16()
+    _, i = value_order(z, torch.tensor([[3, 4, 5, 6], [3, 4, 5, 6]]))
+    assert i.tolist() == [[6, 5, 3, 4], [5, 3, 4, 6]]
 
 
 def test_product_never_imports_oracle():
