@@ -13,10 +13,10 @@ each step as the reference harness does (:55-57).
 The same line carries:
   roofline      the MFMA GEMM engine (the dominant kernel of the step):
                 algorithmic FLOP of the nine FFN GEMMs (7 launches: G and U
-                share one, dX sums two products) / their summed HIP-event time,
-                against the 2.5 PFLOP/s dense bf16 peak; measured on isolated
-                back-to-back launches at the layer's shapes, and (in_step) on
-                the same launches inside real training steps;
+                share one, dX sums two products) / the time the GPU spends in
+                those launches inside the timed steps (union of their
+                event-bracketed intervals), against the 2.5 PFLOP/s dense bf16
+                peak; `isolated`: the same launches timed back to back;
   roofline_decode  global-MoC decode (config 3, B=1): union-of-selected-rows
                 bytes / layer time against 8 TB/s, cold weights (rotation
                 over 8 weight sets > 2x the 256 MB MALL), HIP-graph replays;
