@@ -92,9 +92,10 @@ def cfg5_bench(steps: int) -> dict:
     """Config 5: a 350m LLaMA training step (24 layers, d=1024, I=2736,
     K=512), bf16 parameters, AdamW (0.9/0.999, wd 0, fused=False, lr 1e-3),
     tokens [16, 256] uniform over the 32100-token vocabulary with labels =
-    tokens; 1 warmup step, then `steps` timed steps; peak memory after the
-    warmup (the method of benchmark_training_throughput.py:51-114 and
-    benchmark_memory.py:51-107).  Attention, norms and embeddings are stock
+    tokens; 5 warmup steps (the reference harness's default,
+    benchmark_training_throughput.py:135), then `steps` timed steps; peak
+    memory over the timed steps (the method of
+    benchmark_training_throughput.py:51-114 and benchmark_memory.py:51-107).  Attention, norms and embeddings are stock
     PyTorch; the FFN is this build's."""
     import torch
     from moc_amd import PRESETS, build_model
@@ -117,6 +118,8 @@ def cfg5_bench(steps: int) -> dict:
             return loss
 
         loss0 = step().detach()
+        for _ in range(4):
+            step()
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
         t0 = time.perf_counter()

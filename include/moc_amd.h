@@ -133,7 +133,10 @@ int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const void* u_spa
                               int64_t inter, void* s_sparse, void* z_full, int64_t ld,
                               void* stream);
 
-/* grad_g, grad_u dense [rows, out_ld] (zero-filled) from grad_z_full at idx:
+/* grad_g, grad_u dense [rows, inter] rows out_ld elements apart (each row
+ * written whole: inter values plus zeros up to the next multiple of 8,
+ * nothing beyond it, so out_ld may leave room for the other tensor's rows,
+ * e.g. grad_u = grad_g + pitch with out_ld = 2 pitch) from grad_z_full at idx:
  * grad_u = s*gz, grad_g = u*gz*SiLU'(g) (moc/training/triton_sparse_aux.py:
  * 363-423; bf16 follows the materialised-bf16 chain at :376-400, f32 the fused
  * kernel :139-182).  s_sparse may be NULL: s is then recomputed from g

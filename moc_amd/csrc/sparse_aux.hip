@@ -20,6 +20,8 @@
 // cleared by a fill kernel inside the same entry point (no hipMemsetAsync,
 // so the calls stay valid inside a captured HIP graph) and elementwise work
 // is one thread per selected entry.  Every kernel is bound by HBM traffic.
+#include <algorithm>
+
 #include "abi.h"
 #include "common.h"
 
@@ -165,6 +167,13 @@ __global__ __launch_bounds__(256) void sparse_backward_aux_kernel(
 constexpr int kRowThreadsBwd = 512;
 constexpr int kRowThreads = 256;
 constexpr int64_t kRowMaxLd = 8192;  // three staged rows fit the default 64 KB of LDS
+
+// Elements of an output row the row kernels write: inter rounded up to a
+// multiple of 8, at most the row pitch.
+__host__ __device__ inline int64_t out_row_width(int64_t inter, int64_t out_ld) {
+  const int64_t w = (inter + 7) / 8 * 8;
+  return w < out_ld ? w : out_ld;
+}
 
 template <int NT>
 __device__ __forceinline__ void row_zero(uint16_t* buf, int64_t ld) {
@@ -316,15 +325,18 @@ __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     const uint16_t* __restrict__ gz_full, int64_t gz_ld, int k, int64_t inter,
     uint16_t* __restrict__ grad_g, uint16_t* __restrict__ grad_u, int64_t out_ld) {
   extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
+  // an output row is inter values plus zeros up to a multiple of 8; rows
+  // are out_ld apart (out_ld may leave room for another tensor's rows)
+  const int64_t width = out_row_width(inter, out_ld);
   uint16_t* gzrow = rbuf;                  // [gz_ld]
-  uint16_t* ggrow = rbuf + gz_ld;          // [out_ld]
-  uint16_t* gurow = rbuf + gz_ld + out_ld;  // [out_ld]
+  uint16_t* ggrow = rbuf + gz_ld;          // [width]
+  uint16_t* gurow = rbuf + gz_ld + width;  // [width]
   const int64_t row = blockIdx.x;
   RowEntries<IdxT, kRowThreadsBwd> r;
   r.load(idx, g_s, u_s, s_s, row, k, 0);
   row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_ld);
-  row_zero<kRowThreadsBwd>(ggrow, out_ld);
-  row_zero<kRowThreadsBwd>(gurow, out_ld);
+  row_zero<kRowThreadsBwd>(ggrow, width);
+  row_zero<kRowThreadsBwd>(gurow, width);
   __syncthreads();
   for (int e0 = 0; e0 < k; e0 += kRowThreadsBwd * kRowPer) {
     if (e0 > 0) r.load(idx, g_s, u_s, s_s, row, k, e0);
@@ -337,8 +349,26 @@ __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     }
   }
   __syncthreads();
-  row_store<kRowThreadsBwd>(grad_g + row * out_ld, ggrow, out_ld);
-  row_store<kRowThreadsBwd>(grad_u + row * out_ld, gurow, out_ld);
+  row_store<kRowThreadsBwd>(grad_g + row * out_ld, ggrow, width);
+  row_store<kRowThreadsBwd>(grad_u + row * out_ld, gurow, width);
+}
+
+// Zeros columns [0, width) of rows x ld elements of esz bytes (16-byte
+// stores where the row start and width allow, else element stores).
+__global__ __launch_bounds__(256) void zero_rows_kernel(char* __restrict__ p, int64_t rows,
+                                                        int64_t width_bytes, int64_t ld_bytes) {
+  const int64_t row = blockIdx.y;
+  char* r = p + row * ld_bytes;
+  const bool vec = ((reinterpret_cast<uintptr_t>(r) | static_cast<uintptr_t>(width_bytes)) & 15) == 0;
+  if (vec) {
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < width_bytes / 16;
+         c += static_cast<int64_t>(gridDim.x) * 256)
+      reinterpret_cast<uint4*>(r)[c] = make_uint4(0, 0, 0, 0);
+  } else {
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; c < width_bytes;
+         c += static_cast<int64_t>(gridDim.x) * 256)
+      r[c] = 0;
+  }
 }
 
 // The row form applies to bf16 dense rows that are 16-byte aligned with a
@@ -503,7 +533,7 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
   if (dtype == MOC_BF16 && rows < (1LL << 31) && row_form_ok(gz_full, gz_ld) &&
       row_form_ok(grad_g, out_ld) && row_form_ok(grad_u, out_ld)) {
     hipStream_t st = as_stream(stream);
-    const size_t lds = static_cast<size_t>(gz_ld + 2 * out_ld) * 2;
+    const size_t lds = static_cast<size_t>(gz_ld + 2 * out_row_width(inter, out_ld)) * 2;
 #define MOC_BWDR(T)                                                                          \
   backward_aux_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
       (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                   \
@@ -513,12 +543,25 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
 #undef MOC_BWDR
     return check_launch("backward_aux_rows_kernel");
   }
-  const size_t esz = dtype == MOC_BF16 ? 2 : 4;
-  int rc = moc_fill_zero(grad_g, rows * out_ld * static_cast<int64_t>(esz), stream);
-  if (rc == MOC_OK) rc = moc_fill_zero(grad_u, rows * out_ld * static_cast<int64_t>(esz), stream);
+  const int64_t esz = dtype == MOC_BF16 ? 2 : 4;
+  MOC_REQUIRE(rows <= 65535 || out_row_width(inter, out_ld) == out_ld,
+              "moc_sparse_backward_aux: more than 65535 rows need out_ld = inter rounded to 8");
+  hipStream_t st = as_stream(stream);
+  int rc = MOC_OK;
+  if (out_row_width(inter, out_ld) == out_ld) {
+    rc = moc_fill_zero(grad_g, rows * out_ld * esz, stream);
+    if (rc == MOC_OK) rc = moc_fill_zero(grad_u, rows * out_ld * esz, stream);
+  } else {
+    // rows out_ld apart that leave room for other data: zero only the rows
+    const int64_t wb = out_row_width(inter, out_ld) * esz;
+    const dim3 zgrid(static_cast<unsigned>(std::min<int64_t>((wb / 16 + 255) / 256, 64)),
+                     static_cast<unsigned>(rows));
+    zero_rows_kernel<<<zgrid, 256, 0, st>>>(static_cast<char*>(grad_g), rows, wb, out_ld * esz);
+    zero_rows_kernel<<<zgrid, 256, 0, st>>>(static_cast<char*>(grad_u), rows, wb, out_ld * esz);
+    rc = check_launch("zero_rows_kernel");
+  }
   if (rc != MOC_OK) return rc;
   const int64_t n = rows * k;
-  hipStream_t st = as_stream(stream);
 #define MOC_BWD(T)                                                                            \
   if (dtype == MOC_BF16)                                                                      \
     sparse_backward_aux_kernel<true, T><<<grid_for(n), 256, 0, st>>>(                         \

@@ -239,14 +239,33 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     wd = K.aligned_rows(down_w)
     gz = K.padded_empty(go.shape[0], inter, x.dtype, dev)
     K.gemm(go, wd, out=gz)
-    grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
-    del gz
-    grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=grad_dtype)
-    grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=grad_dtype)
+    pitch = K.row_pitch(inter, x.dtype)
+    if _stack_weight_grads(dev, inter, d, pitch, x.dtype):
+        # dWg and dWu as one GEMM over the stacked [gG | gU]: twice the tiles
+        # of each, so a K split half as deep and half the partial tiles
+        grad_g, grad_u, ggu = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter, stacked=True)
+        del gz
+        dw = K.gemm(ggu.t(), x2, out_dtype=grad_dtype)
+        grad_gate_w, grad_up_w = dw[:inter], dw[pitch:pitch + inter]
+    else:
+        grad_g, grad_u = K.sparse_backward_aux(idx, g_s, u_s, s_s, gz, inter)
+        del gz
+        grad_gate_w = K.gemm(grad_g.t(), x2, out_dtype=grad_dtype)
+        grad_up_w = K.gemm(grad_u.t(), x2, out_dtype=grad_dtype)
     grad_x = K.gemm(grad_g, K.aligned_rows(gate_w), a2=grad_u, b2=K.aligned_rows(up_w))
     if side is not None:
         main.wait_stream(side)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
+
+
+def _stack_weight_grads(dev, inter: int, d: int, pitch: int, dtype) -> bool:
+    """dWg and dWu as one stacked GEMM when each alone leaves most CUs idle
+    (split-K territory: the 130m and 350m shapes).  At the 1b shape (176
+    tiles each) two launches with their own two-part K splits measured
+    faster than one stacked launch (632-649 us against 660 us)."""
+    if dtype != torch.bfloat16 or 2 * pitch > 8192:  # the backward row kernel's limit
+        return False
+    return 2 * K.gemm_tiles(inter, d) <= K.cu_count(dev.index) // 2
 
 
 def _autocast_dtype(x):

@@ -228,8 +228,12 @@ def gcp_recompute_scatter(g_sparse: torch.Tensor, u_sparse: torch.Tensor, topk_i
 
 
 def sparse_backward_aux(topk_idx: torch.Tensor, g_sparse: torch.Tensor, u_sparse: torch.Tensor,
-                        s_sparse: torch.Tensor | None, grad_z_full: torch.Tensor, inter: int):
-    """-> (grad_g, grad_u) as zero-filled [rows, inter] views of padded buffers."""
+                        s_sparse: torch.Tensor | None, grad_z_full: torch.Tensor, inter: int,
+                        stacked: bool = False):
+    """-> (grad_g, grad_u) as zero-filled [rows, inter] views of padded buffers.
+    stacked: both are views of one [rows, 2 pitch] buffer (grad_g in columns
+    [0, inter), grad_u from column pitch), returned third, so that
+    [grad_g | grad_u]^T x is one GEMM."""
     N.require_device(topk_idx, g_sparse, u_sparse, s_sparse, grad_z_full)
     idx = _sparse_2d(topk_idx)
     g = _sparse_2d(g_sparse)
@@ -239,12 +243,17 @@ def sparse_backward_aux(topk_idx: torch.Tensor, g_sparse: torch.Tensor, u_sparse
     gz, gz_ld = _rows_view(grad_z_full.reshape(rows, -1) if grad_z_full.dim() != 2 else grad_z_full)
     if gz.dtype != g.dtype:
         raise ValueError(f"dtype mismatch: g_sparse {g.dtype}, grad_z_full {gz.dtype}")
-    gg = padded_empty(rows, inter, g.dtype, g.device)
-    gu = padded_empty(rows, inter, g.dtype, g.device)
+    if stacked:
+        pitch = row_pitch(inter, g.dtype)
+        buf = _empty((rows, 2 * pitch), g.dtype, g.device)
+        gg, gu = buf[:, :inter], buf[:, pitch:pitch + inter]
+    else:
+        gg = padded_empty(rows, inter, g.dtype, g.device)
+        gu = padded_empty(rows, inter, g.dtype, g.device)
     N.call("moc_sparse_backward_aux", N.dtype_code(g.dtype), idx.data_ptr(), N.idx_code(idx.dtype),
            g.data_ptr(), u.data_ptr(), N.ptr(s), gz.data_ptr(), gz_ld, rows, k, inter,
            gg.data_ptr(), gu.data_ptr(), gg.stride(0), N.stream_of(g))
-    return gg, gu
+    return (gg, gu, buf) if stacked else (gg, gu)
 
 
 # ---------------------------------------------------------------------- GEMM
