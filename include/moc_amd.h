@@ -319,6 +319,53 @@ int moc_selected_grouped_down_residual_bf16(const void* sz, const void* idx, int
                                             const void* residual, void* y, void* workspace,
                                             int64_t workspace_bytes, void* stream);
 
+/* 2:4-packed form of a 2:8 selection (this library's operand format for the
+ * structured-sparse MFMA, no reference counterpart; it carries exactly the
+ * (idx, sz) of moc_grouped_top2_up_silu_bf16).  For nb rows and
+ * nt = ceil(inter / 64) channel tiles:
+ *   ap[nb, ld_ap] bf16, ld_ap >= 32 nt: 4-channel group q of a row keeps two
+ *     stored values at columns 2q, 2q + 1 (its selected values in channel
+ *     order, zeros for the rest; columns of groups past inter hold zeros);
+ *   meta[nt][meta_rows][2] uint32 (meta_rows >= nb, a multiple of 64; 256
+ *     for moc_sparse28_down_bf16): word h of row r for tile t holds the 2-bit
+ *     position inside its 4-group of each stored value of channels
+ *     64t + 16h .. +16 (bits 0-15, stored value v at bits 2v..2v+1) and of
+ *     64t + 32 + 16h .. +16 (bits 16-31).
+ * moc_pack28_bf16 builds it from (sz, idx) as moc_grouped_top2_up_silu_bf16
+ * writes them (idx int64 [nb, inter/4]: top-1, top-2 of each 8-group).  An
+ * index outside its own 8-group, or a repeated one, cannot be packed: that
+ * group's values become NaN.  zero4k (optional, 16-byte aligned) gets 4096
+ * zero bytes (the counter block of a moc_sparse28_down_bf16 workspace). */
+int moc_pack28_bf16(const void* sz, const void* idx, int64_t nb, int64_t inter, void* ap, int64_t ld_ap,
+                    uint32_t* meta, int64_t meta_rows, void* zero4k, void* stream);
+
+/* moc_grouped_top2_up_silu_bf16 (same selection and sz values) writing the
+ * 2:4-packed form above (ap, meta) instead of (idx, sz): the fused gate/up
+ * kernel's epilogue packs directly, for moc_sparse28_down_bf16 to consume
+ * (the prefill pair of kernel A and kernel B, triton_fused_ffn_kernels.py:
+ * 29-156, 228-267, without the int64 indices in between).  Rows of meta past
+ * nb are left as they are (the Down never reads them as data: its A rows
+ * there are zero). */
+int moc_grouped_top2_up_silu_packed_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
+                                         const void* w_up, int64_t inter, void* ap, int64_t ld_ap,
+                                         uint32_t* meta, int64_t meta_rows, void* stream);
+
+/* Workspace bytes of moc_sparse28_down_bf16 (its first MOC_GEMM_WS_COUNTER_BYTES
+ * are arrival counters: zero when a call starts, left zero). */
+int64_t moc_sparse28_down_workspace_size(int64_t nb, int64_t inter, int64_t hidden);
+
+/* The MoC 2:8 compacted Down at prefill: y[nb, hidden] = bf16(A W^T) with A
+ * the 2:4-packed activations (ap, meta above, meta_rows >= nb rounded up to
+ * 256), on the structured-sparse MFMA (v_smfmac_f32_32x32x32_bf16: half the
+ * MFMA work and half the activation bytes of the dense product, twice the
+ * 2:8 product's own FLOP).  w: W_down [hidden, inter] (w_kc = 1) or W_down^T
+ * [inter, hidden] (w_kc = 0), row pitch ldw.  Replaces the gathered down of
+ * moc::selected_grouped_down (triton_grouped_moc_ops.py:96-131; kernel
+ * triton_fused_ffn_kernels.py:228-267) for prefill batches. */
+int moc_sparse28_down_bf16(const void* ap, int64_t ld_ap, const uint32_t* meta, int64_t meta_rows,
+                           int64_t nb, int64_t inter, const void* w, int64_t ldw, int w_kc, int64_t hidden,
+                           void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -83,6 +83,12 @@ SIGNATURES: dict[str, tuple] = {
     "moc_selected_grouped_down_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
     "moc_selected_grouped_down_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
                                               _i64, _vp]),
+    "moc_pack28_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp]),
+    "moc_grouped_top2_up_silu_packed_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,
+                                                    _i64, _vp]),
+    "moc_sparse28_down_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "moc_sparse28_down_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _int, _i64, _vp,
+                                      _i64, _vp, _i64, _vp]),
 }
 
 _LIB = None

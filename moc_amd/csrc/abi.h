@@ -39,7 +39,8 @@ int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_
 // MoC 2:8 gate/up + top-2-of-8 for nb tokens on the MFMA GEMM kernel
 // (gemm.hip); 1: shape not supported there (nothing launched).
 int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* wg, const void* wu,
-                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st);
+                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st, uint16_t* ap = nullptr,
+                        int64_t ld_ap = 0, uint32_t* meta = nullptr, int64_t meta_rows = 0);
 
 }  // namespace moc
 

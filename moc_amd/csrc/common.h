@@ -93,26 +93,66 @@ __device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + ex
 // value with the lowest index among equal maxima, top-2 the largest of the
 // other seven under the same rule, sz = bf16((g * sigmoid(g)) * u) in f32
 // (moc/inference/triton_fused_ffn_kernels.py:103-114,126-129).
-__device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
-                                                  int64_t* __restrict__ idx_out,
-                                                  uint16_t* __restrict__ sz_out) {
+__device__ __forceinline__ void select_group_top2(const float* g, const float* u, int& b1, int& b2,
+                                                  uint16_t& s1, uint16_t& s2) {
   uint32_t key[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) key[j] = bf16_order_key(f32_to_bf16(g[j]));
-  int b1 = 0;
+  b1 = 0;
 #pragma unroll
   for (int j = 1; j < 8; ++j)
     if (key[j] > key[b1]) b1 = j;
-  int b2 = (b1 == 0) ? 1 : 0;
+  b2 = (b1 == 0) ? 1 : 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j)
     if (j != b1 && key[j] > key[b2]) b2 = j;
   const float g1 = g[b1], g2 = g[b2];
+  s1 = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
+  s2 = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
+}
+
+__device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
+                                                  int64_t* __restrict__ idx_out,
+                                                  uint16_t* __restrict__ sz_out) {
+  int b1, b2;
+  uint16_t s1, s2;
+  select_group_top2(g, u, b1, b2, s1, s2);
   idx_out[0] = c0 + b1;
   idx_out[1] = c0 + b2;
-  sz_out[0] = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
-  sz_out[1] = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
+  sz_out[0] = s1;
+  sz_out[1] = s2;
 }
+
+// 2:4 packing of one 8-channel group holding two selected channels at
+// positions p1 != p2 (0-7) with values v1, v2: each 4-channel half keeps two
+// stored values (its selected values in channel order, zeros for the rest,
+// at distinct positions).  out: lo0, lo1, hi0, hi1; the return value holds
+// the four 2-bit positions in the same order (bits 0-7).
+__device__ __forceinline__ uint32_t pack_group_2of8(int p1, uint16_t v1, int p2, uint16_t v2,
+                                                    uint16_t (&out)[4]) {
+  const bool sw = p2 < p1;
+  const int qa = sw ? p2 : p1, qb = sw ? p1 : p2;
+  const uint16_t va = sw ? v2 : v1, vb = sw ? v1 : v2;
+  uint32_t pos;
+  if (qb < 4) {  // both in the low half
+    out[0] = va; out[1] = vb; out[2] = 0; out[3] = 0;
+    pos = static_cast<uint32_t>(qa) | (static_cast<uint32_t>(qb) << 2) | (0x4u << 4);
+  } else if (qa >= 4) {  // both in the high half
+    out[0] = 0; out[1] = 0; out[2] = va; out[3] = vb;
+    pos = 0x4u | ((static_cast<uint32_t>(qa - 4) | (static_cast<uint32_t>(qb - 4) << 2)) << 4);
+  } else {  // one in each half
+    uint32_t lo, hi;
+    if (qa == 0) { out[0] = va; out[1] = 0; lo = 0x4u; }
+    else { out[0] = 0; out[1] = va; lo = static_cast<uint32_t>(qa) << 2; }
+    if (qb == 4) { out[2] = vb; out[3] = 0; hi = 0x4u; }
+    else { out[2] = 0; out[3] = vb; hi = static_cast<uint32_t>(qb - 4) << 2; }
+    pos = lo | (hi << 4);
+  }
+  return pos;
+}
+
+// Positions byte of an 8-group with nothing to pack (zeros at 0, 1 per half).
+constexpr uint32_t kPackEmpty2of8 = 0x44u;
 
 // Dot product of 8 bf16 pairs (two 16-byte chunks) accumulated in f32.
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {

@@ -50,6 +50,7 @@ namespace moc {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x16_t __attribute__((ext_vector_type(16)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -68,6 +69,8 @@ constexpr int kRowsPerLoad = 64 / kCpr;         // KC rows one wave instruction 
 constexpr int kBufferFlags = 0x00020000;        // raw buffer, 32-bit dwords
 constexpr int kGroupM = 4;                      // M tiles per L2 group
 constexpr uint32_t kOob = 0x80000000u;          // a buffer offset that reads as zero
+constexpr int kSpATile = 256 * 32 * 2;          // SP: packed A tile; its positions follow (2 KB)
+static_assert(kSpATile + 2048 <= kTileBytes, "SP: packed A and positions share the A stage");
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kLoads == 2 * (kBK / 16), "each k16 step issues two loads per operand");
 
@@ -113,6 +116,22 @@ struct GemmArgs {
   int ncat_tn, N2, vec_store2;
   void* C2;
   int64_t ldc2;
+  // MoC 2:8 compacted Down (gemm_pp_kernel<..., SP = true>): a[0] holds the
+  // activations 2:4-packed (two stored values per 4 channels: 32 values per
+  // 64-channel K tile, a[0].K = 32 nk[0]) and sp_meta the stored values'
+  // positions inside their 4-channel groups, laid out [nk][sp_rows][2] u32:
+  // word h of row r for K tile t holds 2 bits per stored value, those of
+  // channels 64t + 16h .. +16 in bits 0-15 and of 64t + 32 + 16h .. +16 in
+  // bits 16-31 (the two 32-channel steps of the tile).
+  const uint32_t* sp_meta;
+  int sp_rows;
+  // MoC 2:8 gate/up launch writing the 2:4-packed form of its selection
+  // (gu_ap != nullptr) instead of (gu_idx, gu_sz): values ap[M, gu_ld_ap],
+  // positions gu_meta in the sp_meta layout ([gu_nt][gu_meta_rows][2]).
+  uint16_t* gu_ap;
+  int64_t gu_ld_ap;
+  uint32_t* gu_meta;
+  int gu_meta_rows, gu_nt;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -164,6 +183,11 @@ __device__ __forceinline__ int kc_swz(int r) {
   return kCpr == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (((r >> 1) ^ (r >> 3)) & 3);
 }
 __device__ __forceinline__ int mn_swz(int r) { return ((r & 1) << 2) + ((r >> 1) & 1) * 10; }
+// 2:4-packed A tile (64-byte rows of four 16-byte chunks): chunk c of row r
+// in slot c ^ sp_swz(r & 15).  Rows r .. r + 15 reading one logical chunk hit
+// 16 distinct 16-byte bank groups, and rows r .. r + 7 eight distinct ones
+// within their 128 bytes.
+__device__ __forceinline__ int sp_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 // -------------------------------------------------------------- tile loading
 // Thread (wave w, lane l) moves kLoads chunks of 16 bytes per operand tile;
@@ -355,6 +379,60 @@ __device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
     // read back: 16-byte segments
     constexpr int kSegs = kCols * kEsz / 16;        // per row
+    constexpr int kIters = 32 * kSegs / 64;
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int e = it * 64 + lane;
+      const int row = e / kSegs, seg = e % kSegs;
+      const uint4 v = *reinterpret_cast<const uint4*>(reg + row * kPitch + seg * 16);
+      const int grow = row0 + wm + 32 * i + row;
+      const int gcol = col0 + wn + seg * (16 / kEsz);
+      if (grow >= g.M || gcol >= g.N) continue;
+      char* dst = static_cast<char*>(g.C) + (static_cast<int64_t>(grow) * g.ldc + gcol) * kEsz;
+      if (vec && gcol + 16 / kEsz <= g.N) {
+        *reinterpret_cast<uint4*>(dst) = v;
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        if (OUT_F32) {
+          for (int q = 0; q < 4 && gcol + q < g.N; ++q)
+            reinterpret_cast<float*>(dst)[q] = __uint_as_float(w[q]);
+        } else {
+          for (int q = 0; q < 8 && gcol + q < g.N; ++q)
+            reinterpret_cast<uint16_t*>(dst)[q] = static_cast<uint16_t>(w[q >> 1] >> (16 * (q & 1)));
+        }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+  }
+}
+
+// The same write-back for accumulators in the MFMA's own orientation (the
+// structured-sparse product, whose sparse operand must come first): lane l
+// holds column 32 j + (l & 31) of rows 8q + 4(l >> 5) + r.  Each element is
+// staged with its own LDS write, then rows go out as 16-byte segments.
+template <bool OUT_F32, int NJ>
+__device__ __forceinline__ void store_tile_t(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][NJ],
+                                             int row0, int col0, int wm, int wn, int wave, int lane) {
+  constexpr int kEsz = OUT_F32 ? 4 : 2;
+  constexpr int kCols = 32 * NJ;
+  constexpr int kPitch = kCols * kEsz + 16;
+  char* reg = lds + wave * (32 * kPitch);
+  const bool vec = g.vec_store != 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          char* dst = reg + (8 * q + 4 * (lane >> 5) + r) * kPitch + (32 * j + (lane & 31)) * kEsz;
+          const float v = acc[i][j][4 * q + r];
+          if (OUT_F32) *reinterpret_cast<float*>(dst) = v;
+          else *reinterpret_cast<uint16_t*>(dst) = static_cast<uint16_t>(pack_bf16x2(v, 0.f) & 0xFFFFu);
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    constexpr int kSegs = kCols * kEsz / 16;
     constexpr int kIters = 32 * kSegs / 64;
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
@@ -641,9 +719,10 @@ struct LoadMap {
 // its f32 partial tile in accumulator order (16-byte word (b, q, tid) =
 // acc[b / 2][b % 2][4q .. 4q+3] of thread tid: one wave instruction covers
 // 1 KB) with device-coherent stores, waits for them and bumps the tile's
-// arrival counter; the one that finishes second (it finds the counter at 1,
-// or its own increment returns 1) reads that partial back with
-// device-coherent loads, adds it to its registers (a + b = b + a, so the
+// arrival counter (an agent-scope release); the one that finishes second
+// (it finds the counter at 1, or its own increment returns 1, each an
+// agent-scope acquire) reads that partial back with device-coherent loads,
+// adds it to its registers (a + b = b + a, so the
 // result does not depend on which part came second), writes C and resets
 // the counter.  Nothing waits on another workgroup.
 constexpr int kPartBytes = 8 * 4 * kPpThreads * 16;  // one partial tile (256 KB)
@@ -659,7 +738,11 @@ __device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4]
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       g.fix_part + static_cast<int64_t>(slot) * 2 * kPartBytes, (short)0, 2 * kPartBytes, kBufferFlags);
   int* cnt = g.fix_cnt + slot;
-  if (tid == 0) *flag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // acquire: if the other part has arrived, its partial is visible to the
+  // loads below (on this GPU the L2 of each XCD is private, so the two parts
+  // of a tile need the agent-scope release/acquire pair, not just coherent
+  // data stores, whichever XCDs they run on)
+  if (tid == 0) *flag = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (*flag == 0) {
     // first so far: publish the partial, then arrive
@@ -676,7 +759,7 @@ __device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4]
       }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is stored
     __syncthreads();
-    if (tid == 0) *flag = atomicAdd(cnt, 1);
+    if (tid == 0) *flag = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (*flag == 0) return false;
   }
@@ -729,6 +812,49 @@ __device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, cons
   }
   __syncthreads();
   const int kout = g.gu_inter / 4;
+  if (g.gu_ap != nullptr) {
+    // packed form: item (token, 8-group G) writes its four stored values
+    // (8 bytes) and its positions byte; the four 8-groups of one position
+    // word sit in lanes l, l ^ 1, l ^ 4, l ^ 5 (G & 15 = l & 15), which
+    // combine it before one of them stores it.
+#pragma unroll 2
+    for (int item = tid; item < 256 * 16; item += kPpThreads) {
+      const int tr = item >> 4, grp8 = item & 15;
+      const int tok = row0 + tr, cg = col0 + grp8 * 8;
+      const int G = cg >> 3;
+      uint16_t q[4] = {0, 0, 0, 0};
+      uint32_t pos = kPackEmpty2of8;
+      if (tok < g.M && cg < g.gu_inter) {
+        const int off = tr * 256 + ((grp8 ^ (tr & 15)) << 4);
+        const uint4 gv = *reinterpret_cast<const uint4*>(lds + off);
+        const uint4 uv = *reinterpret_cast<const uint4*>(lds + kU + off);
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+        float gf[8], uf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          gf[2 * e] = __uint_as_float(gw[e] << 16);
+          gf[2 * e + 1] = __uint_as_float(gw[e] & 0xFFFF0000u);
+          uf[2 * e] = __uint_as_float(uw[e] << 16);
+          uf[2 * e + 1] = __uint_as_float(uw[e] & 0xFFFF0000u);
+        }
+        int b1, b2;
+        uint16_t s1, s2;
+        select_group_top2(gf, uf, b1, b2, s1, s2);
+        pos = pack_group_2of8(b1, s1, b2, s2, q);
+      }
+      // 64-channel tile t = G / 8; G % 8 = 4s + 2h + jj
+      const int t = G >> 3, s = (G >> 2) & 1, h = (G >> 1) & 1, jj = G & 1;
+      uint32_t w = pos << (16 * s + 8 * jj);
+      w |= __shfl_xor(w, 1);
+      w |= __shfl_xor(w, 4);
+      if (tok < g.M && t < g.gu_nt) {
+        *reinterpret_cast<uint2*>(g.gu_ap + static_cast<int64_t>(tok) * g.gu_ld_ap + 4 * G) =
+            make_uint2(q[0] | (static_cast<uint32_t>(q[1]) << 16), q[2] | (static_cast<uint32_t>(q[3]) << 16));
+        if (s == 0 && jj == 0) g.gu_meta[(static_cast<int64_t>(t) * g.gu_meta_rows + tok) * 2 + h] = w;
+      }
+    }
+    return;
+  }
 #pragma unroll 2
   for (int item = tid; item < 256 * 16; item += kPpThreads) {
     const int tr = item >> 4, grp8 = item & 15;
@@ -753,7 +879,14 @@ __device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, cons
 
 // SPLIT: split-K launch (f32 partial tiles into the workspace slices).
 // GU: MoC 2:8 gate/up launch (see GemmArgs::gu_idx).
-template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT, bool GU = false>
+// SP: A is 2:4-packed (see GemmArgs::sp_meta) and each 32-channel step of a
+// K tile runs on v_smfmac_f32_32x32x32_bf16: half the MFMA instructions and
+// half the A bytes of the dense form.  A K tile of A is then 256 rows x 32
+// stored values (16 KB, 64-byte rows, chunks swizzled by sp_swz) plus 2 KB of
+// positions, both in the A stage; B and everything else are unchanged.  The
+// sparse operand is the MFMA's first, so the accumulators come out in the
+// MFMA's orientation and leave through store_tile_t.
+template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT, bool GU = false, bool SP = false>
 __global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
@@ -812,28 +945,73 @@ void gemm_pp_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  bf16x8_t fa[4][4], fb[4][2];  // [k16 step][block]
+  bf16x8_t fa[4][4], fb[4][2];  // [k16 step][block]  (SP: fa[32-channel step][block])
+  uint32_t fm[4];               // SP: positions of the stored A values, per block
+  // SP: the lane's A fragment of block 0, step 0 (row wm + (lane & 31),
+  // logical chunk lane >> 5); step s is chunk 2s + (lane >> 5), one XOR away
+  const uint32_t spa_base =
+      static_cast<uint32_t>((wm + (lane & 31)) * 64 + (((lane >> 5) ^ sp_swz(lane & 15)) << 4));
+  const uint32_t spm_base = static_cast<uint32_t>(kSpATile + (wm + (lane & 31)) * 8 + (lane >> 5) * 4);
   auto read_frags = [&](int st) {
     const uint32_t so = st * kTileBytes;
+    if constexpr (SP) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
+        for (int i = 0; i < 4; ++i)
+          fa[s][i] = __builtin_bit_cast(
+              bf16x8_t, *reinterpret_cast<const uint4*>(lds + ((spa_base + so) ^ (32u * s)) + i * 2048));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
+      for (int i = 0; i < 4; ++i) fm[i] = *reinterpret_cast<const uint32_t*>(lds + so + spm_base + i * 256);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
+      }
     }
   };
-  // The 32 MFMAs of a K tile (order pinned).
+  // The 32 MFMAs of a K tile (order pinned); SP: 16 structured-sparse ones,
+  // B of a 32-channel step being the two k16 fragments of the dense form
+  // (the operand layout of v_smfmac_f32_32x32x32_bf16: lane l's B holds
+  // channels 8(l >> 5) .. +8 and 16 + 8(l >> 5) .. +8 of column l & 31).
   auto compute = [&]() {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    if constexpr (SP) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+          const bf16x16_t b = __builtin_shufflevector(fb[0][j], fb[1][j], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10,
+                                                      11, 12, 13, 14, 15);
+          acc[i][j] = __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[0][i], b, acc[i][j], fm[i], 0, 0);
           __builtin_amdgcn_sched_barrier(0);
         }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bf16x16_t b = __builtin_shufflevector(fb[2][j], fb[3][j], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10,
+                                                      11, 12, 13, 14, 15);
+          acc[i][j] = __builtin_amdgcn_smfmac_f32_32x32x32_bf16(fa[1][i], b, acc[i][j], fm[i], 0, 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+    }
   };
 
   // Workgroup barrier between phases; the scheduling fences keep the compiler
@@ -863,10 +1041,46 @@ void gemm_pp_kernel(GemmArgs g) {
     mb1.init(g.b[1], col0 - 128, sw, lane);
     rb1 = make_rsrc(g.b[1]);
   }
+  // SP: the 16 wave loads of a packed A tile (load L fills tile rows
+  // 16L .. 16L + 15: lane l row 16L + l/4, slot l % 4) and the 2 of its
+  // positions (load L covers rows 128L .. 128L + 127, two per lane).
+  const __amdgpu_buffer_rsrc_t rm = SP ? __builtin_amdgcn_make_buffer_rsrc(
+                                             const_cast<uint32_t*>(g.sp_meta), (short)0,
+                                             g.nk[0] * g.sp_rows * 8, kBufferFlags)
+                                       : ra0;
+  const uint32_t spa_voff = static_cast<uint32_t>(
+      (static_cast<int64_t>(row0 + (lane >> 2)) * g.a[0].ld + 8 * ((lane & 3) ^ sp_swz(lane >> 2))) * 2);
+  auto sp_load = [&](int t, int half) {
+    const uint32_t at = lds0 + (t % kStages) * kTileBytes;
+    const uint32_t kofs = static_cast<uint32_t>(t) * 64u;
+    const uint32_t rstride = static_cast<uint32_t>(16 * g.a[0].ld * 2);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int L = 8 * half + 4 * u + sw;
+      uint32_t off = spa_voff + kofs + static_cast<uint32_t>(L) * rstride;
+      asm volatile("" : "+v"(off));
+      dma16(ra0, __builtin_amdgcn_readfirstlane(at + L * 1024), off);
+    }
+    if (half == 1 && sw >= 2) {
+      const int L = sw - 2;
+      const uint32_t off = static_cast<uint32_t>(
+          ((static_cast<int64_t>(t) * g.sp_rows + row0 + 128 * L + 2 * lane) * 8));
+      dma16(rm, __builtin_amdgcn_readfirstlane(at + kSpATile + L * 1024), off);
+    }
+  };
   // Loads [j0, j1) of A and of B of K tile t into its stage.
   auto load_tile = [&](int t, int j0, int j1) {
     const int st = t % kStages;
     const uint32_t at = lds0 + st * kTileBytes, bt = lds0 + kBOffset + st * kTileBytes;
+    if constexpr (SP) {
+      // A: group 0's share is the first half, group 1's the second
+      for (int half = j0 / kG0Loads; half < j1 / kG0Loads; ++half) sp_load(t, half);
+      const uint32_t bb = mb0.tile_base(g.b[0], t * kBK);
+#pragma unroll
+      for (int j = 0; j < kLoads; ++j)
+        if (j >= j0 && j < j1) mb0.issue(rb0, g.b[0], bb, bt, sw, j);
+      return;
+    }
     const bool p1 = DUAL && t >= nk0;
     const int k0 = (p1 ? t - nk0 : t) * kBK;
     const Operand& oa = p1 ? g.a[1] : g.a[0];
@@ -893,6 +1107,11 @@ void gemm_pp_kernel(GemmArgs g) {
     const bool p1 = DUAL && t >= nk0;
     const Operand& oa = p1 ? g.a[1] : g.a[0];
     const int k0 = (p1 ? t - nk0 : t) * kBK;
+    if (SP) {  // packed A tiles are whole; only a KC B can straddle K
+      if (B_KC && k0 + kBK > g.b[0].K && (g.b[0].K & 7) != 0)
+        mb0.zero_straddle(lds, g.b[0], k0, bt, sw, lane, j0, j1);
+      return;
+    }
     if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
     // kchunk depends on the lane only, so the product-0 maps serve both
     if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, j0, j1);
@@ -935,7 +1154,8 @@ void gemm_pp_kernel(GemmArgs g) {
       const int k0 = (p1 ? t - nk0 : t) * kBK;
       if (sw == 0) {
         const Operand& o = p1 ? g.a[1] : g.a[0];
-        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, k0, row0, sink, lane, tn_all & 7, 8);
+        // SP: the packed tile's 64-byte row segments (k0 in stored values)
+        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, SP ? t * 32 : k0, row0, sink, lane, tn_all & 7, 8);
       } else if (sw == 1) {
         const Operand& o = p1 ? g.b[1] : g.b[0];
         if (GU && (tm & 3) >= 2)  // quarters 2-3 of the B tile are W_up rows
@@ -972,11 +1192,13 @@ void gemm_pp_kernel(GemmArgs g) {
   } else if (SPLIT) {
     GemmArgs gs = g;
     gs.C = static_cast<float*>(g.C) + split * g.ws_stride;
-    store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
+    if (SP) store_tile_t<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
+    else store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
   } else {
     if (part >= 0 && !fix_arrive(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kSinkOffset)))
       return;
-    store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+    if (SP) store_tile_t<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+    else store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
   }
 }
 
@@ -1374,7 +1596,8 @@ FixPlan plan_fix(int64_t M, int64_t N, int nk) {
 // without launching when an operand is too large for its 32-bit buffer
 // offsets (the caller then uses its own kernel).
 int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* wg, const void* wu,
-                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st) {
+                        int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st, uint16_t* ap,
+                        int64_t ld_ap, uint32_t* meta, int64_t meta_rows) {
   GemmArgs a{};
   const bool ok = make_operand(x, hidden, true, nb, hidden, a.a[0]) &&
                   make_operand(wg, hidden, true, inter, hidden, a.b[0]) &&
@@ -1395,9 +1618,23 @@ int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* w
   a.gu_idx = idx;
   a.gu_sz = sz;
   a.gu_inter = static_cast<int>(inter);
+  a.gu_ap = ap;
+  a.gu_ld_ap = ld_ap;
+  a.gu_meta = meta;
+  a.gu_meta_rows = static_cast<int>(meta_rows);
+  a.gu_nt = static_cast<int>((inter + kBK - 1) / kBK);
   const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.tiles_m) * a.tiles_n));
   gemm_pp_kernel<true, true, false, false, false, true><<<grid, dim3(kPpThreads), 0, st>>>(a);
   return check_launch("gemm_pp_kernel (2:8 gate/up)");
+}
+
+template <bool W_KC>
+void launch_sparse_down_kernel(const GemmArgs& run, bool split, hipStream_t st) {
+  const int64_t units = run.fix_tail > 0 ? run.fix_full + 2 * static_cast<int64_t>(run.fix_tail)
+                                         : static_cast<int64_t>(run.tiles_m) * run.tiles_n * run.ksplit;
+  const dim3 grid(static_cast<unsigned>(units)), block(kPpThreads);
+  if (split) gemm_pp_kernel<true, W_KC, true, false, true, false, true><<<grid, block, 0, st>>>(run);
+  else gemm_pp_kernel<true, W_KC, false, false, false, false, true><<<grid, block, 0, st>>>(run);
 }
 
 }  // namespace moc
@@ -1415,6 +1652,92 @@ extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int6
   if (dtype != MOC_BF16) return 0;
   const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
   return std::max(plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes);
+}
+
+// MoC 2:8 compacted Down on the structured-sparse MFMA:
+//   y[nb, hidden] = A[nb, inter] W^T,  A 2:4-packed (ap, meta; see GemmArgs::sp_meta)
+// w: W_down [hidden, inter] (w_kc = 1, rows of ldw elements) or W_down^T
+// [inter, hidden] (w_kc = 0).  Tiles, split-K and the tail fix-up follow
+// moc_gemm_ws (same workspace size as the dense [nb, hidden, inter] GEMM).
+extern "C" int64_t moc_sparse28_down_workspace_size(int64_t nb, int64_t inter, int64_t hidden) {
+  return moc_gemm_workspace_size(MOC_BF16, nb, hidden, inter, 0);
+}
+
+extern "C" int moc_sparse28_down_bf16(const void* ap, int64_t ld_ap, const uint32_t* meta, int64_t meta_rows,
+                                      int64_t nb, int64_t inter, const void* w, int64_t ldw, int w_kc,
+                                      int64_t hidden, void* y, int64_t ldy, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(nb >= 0 && inter >= 1 && hidden >= 1 && inter < (1LL << 30) && hidden < (1LL << 30) &&
+                  nb < (1LL << 30),
+              "moc_sparse28_down_bf16: bad shape");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(ap && meta && w && y, "moc_sparse28_down_bf16: null pointer");
+  const int64_t nt = (inter + kBK - 1) / kBK;
+  const int64_t tiles_m = (nb + kBM - 1) / kBM;
+  MOC_REQUIRE(ld_ap >= 32 * nt && ld_ap % 8 == 0,
+              "moc_sparse28_down_bf16: ld_ap must be a multiple of 8 and >= 32 * ceil(inter / 64)");
+  MOC_REQUIRE(meta_rows >= tiles_m * kBM, "moc_sparse28_down_bf16: meta_rows must be >= nb rounded up to 256");
+  MOC_REQUIRE(ldw % 8 == 0 && ldw >= (w_kc ? inter : ((hidden + 7) & ~7LL)),
+              "moc_sparse28_down_bf16: bad ldw");
+  MOC_REQUIRE(ldy >= hidden, "moc_sparse28_down_bf16: ldy < hidden");
+  MOC_REQUIRE(aligned16(ap) && aligned16(meta) && aligned16(w),
+              "moc_sparse28_down_bf16: operands must be 16-byte aligned");
+  MOC_REQUIRE(nt * meta_rows * 8 < (1LL << 31), "moc_sparse28_down_bf16: position array too large");
+  GemmArgs a{};
+  bool ok = make_operand(ap, ld_ap, true, nb, 32 * nt, a.a[0]) && make_operand(w, ldw, w_kc != 0, hidden, inter, a.b[0]);
+  auto no_wrap = [](const Operand& o) {
+    return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
+  };
+  MOC_REQUIRE(ok && no_wrap(a.a[0]) && no_wrap(a.b[0]),
+              "moc_sparse28_down_bf16: an operand exceeds 32-bit buffer addressing");
+  a.a[1] = a.a[0];
+  a.b[1] = a.b[0];
+  a.nk[0] = static_cast<int>(nt);
+  a.nk[1] = 0;
+  a.M = static_cast<int>(nb);
+  a.N = static_cast<int>(hidden);
+  a.C = y;
+  a.ldc = ldy;
+  a.vec_store = (reinterpret_cast<uintptr_t>(y) % 16 == 0 && (ldy * 2) % 16 == 0) ? 1 : 0;
+  a.tiles_m = static_cast<int>(tiles_m);
+  a.tiles_n = static_cast<int>((hidden + kBN - 1) / kBN);
+  a.pp = 1;
+  a.ksplit = 1;
+  a.kper = a.nk[0];
+  a.sp_meta = meta;
+  a.sp_rows = static_cast<int>(meta_rows);
+  const SplitPlan sp = plan_split(nb, hidden, a.nk[0]);
+  const bool split = sp.ksplit > 1 && workspace != nullptr && workspace_bytes >= sp.bytes &&
+                     reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
+  GemmArgs run = a;
+  if (split) {
+    run.ksplit = sp.ksplit;
+    run.kper = sp.kper;
+    run.ws_stride = nb * sp.ldw;
+    run.C = static_cast<char*>(workspace) + kFixCounterBytes;
+    run.ldc = sp.ldw;
+    run.vec_store = 1;
+  }
+  const FixPlan fp = split ? FixPlan() : plan_fix(nb, hidden, a.nk[0]);
+  if (fp.tail > 0 && workspace != nullptr && workspace_bytes >= fp.bytes &&
+      reinterpret_cast<uintptr_t>(workspace) % 256 == 0) {
+    run.fix_full = fp.full;
+    run.fix_tail = fp.tail;
+    run.fix_split = fp.split;
+    run.fix_cnt = static_cast<int*>(workspace);
+    run.fix_part = static_cast<char*>(workspace) + kFixCounterBytes;
+  }
+  hipStream_t st = as_stream(stream);
+  if (w_kc) launch_sparse_down_kernel<true>(run, split, st);
+  else launch_sparse_down_kernel<false>(run, split, st);
+  if (!split) return check_launch("gemm_pp_kernel (2:8 sparse down)");
+  const int rc = check_launch("gemm_pp_kernel (2:8 sparse down, split)");
+  if (rc != MOC_OK) return rc;
+  const int64_t quads = nb * ((hidden + 3) / 4);
+  splitk_reduce_kernel<false><<<dim3(static_cast<unsigned>((quads + 255) / 256)), 256, 0, st>>>(
+      static_cast<const float*>(run.C), run.ws_stride, sp.ksplit, (int)nb, (int)hidden, sp.ldw, y, ldy,
+      a.vec_store);
+  return check_launch("splitk_reduce_kernel");
 }
 
 // Two products of one A in one launch: C1 = A W1^T, C2 = A W2^T (the gate

@@ -38,6 +38,14 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
                            int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
                            void* workspace, int64_t workspace_bytes, void* stream);
 extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2);
+extern "C" int64_t moc_sparse28_down_workspace_size(int64_t nb, int64_t inter, int64_t hidden);
+extern "C" int moc_sparse28_down_bf16(const void* ap, int64_t ld_ap, const uint32_t* meta, int64_t meta_rows,
+                                      int64_t nb, int64_t inter, const void* w, int64_t ldw, int w_kc,
+                                      int64_t hidden, void* y, int64_t ldy, void* workspace,
+                                      int64_t workspace_bytes, void* stream);
+extern "C" int moc_pack28_bf16(const void* sz, const void* idx, int64_t nb, int64_t inter, void* ap,
+                               int64_t ld_ap, uint32_t* meta, int64_t meta_rows, void* zero4k,
+                               void* stream);
 
 namespace moc {
 namespace {
@@ -368,10 +376,97 @@ __global__ __launch_bounds__(kThreads) void grouped_prefill_kernel(
 
 inline int64_t align256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
+// ---------------------------------------------------------------------------
+// 2:4 packing of a 2:8 selection for the compacted Down on the structured-
+// sparse MFMA (moc_sparse28_down_bf16; layout in include/moc_amd.h).  Each
+// group of 8 channels holds two selected channels; its two 4-channel halves
+// get two stored values each (pack_group_2of8), so the packed row is half as
+// wide as the dense one.  A lane packs one 8-group G of one row: it reads
+// the group's (top-1, top-2) indices (16 bytes) and values (4 bytes) and
+// writes its four stored values (8 bytes), so a wave covers 64 consecutive
+// groups (8 channel tiles) of a row with contiguous loads and stores.  The
+// positions byte of G goes into bits 8(G & 1) + 16((G >> 2) & 1) of word
+// h = (G >> 1) & 1 of its tile G >> 3; lanes G, G ^ 1, G ^ 4, G ^ 5 combine
+// that word, which is staged in LDS and leaves as 128-byte runs of one tile
+// (16 rows).  An index outside its own group, or both equal, cannot be
+// packed: the group's values become NaN, so the token's output row is NaN
+// rather than silently wrong.  Workgroup: 16 rows x 64 groups, a wave per
+// row at a time.
+// ---------------------------------------------------------------------------
+constexpr int kPackRows = 16, kPackTiles = 8;
+
+__global__ __launch_bounds__(256) void pack28_kernel(const uint16_t* __restrict__ sz,
+                                                      const int64_t* __restrict__ idx, int nb, int inter,
+                                                      int nt, uint16_t* __restrict__ ap, int64_t ld_ap,
+                                                      uint32_t* __restrict__ meta, int meta_rows,
+                                                      uint32_t* __restrict__ zero4k) {
+  __shared__ uint32_t words[kPackTiles][kPackRows * 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (zero4k != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
+    reinterpret_cast<uint4*>(zero4k)[tid] = make_uint4(0, 0, 0, 0);  // 4 KB of GEMM counters
+  const int kp = inter / 4;       // entries per row
+  const int ngroups = inter / 8;  // 8-groups
+  const int G = blockIdx.x * 64 + lane;
+  const int t = G >> 3;
+#pragma unroll
+  for (int i = 0; i < kPackRows / 4; ++i) {
+    const int rl = wave * (kPackRows / 4) + i;
+    const int row = blockIdx.y * kPackRows + rl;
+    uint16_t q[4] = {0, 0, 0, 0};
+    uint32_t pos = kPackEmpty2of8;
+    if (row < nb && G < ngroups) {
+      const int64_t e = static_cast<int64_t>(row) * kp + 2 * G;
+      const int64_t p1 = idx[e] - 8 * static_cast<int64_t>(G), p2 = idx[e + 1] - 8 * static_cast<int64_t>(G);
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(sz + e);  // e is even: 4-byte aligned
+      if (p1 < 0 || p1 > 7 || p2 < 0 || p2 > 7 || p1 == p2) {
+        q[0] = q[1] = q[2] = q[3] = 0x7FC0;  // NaN
+      } else {
+        pos = pack_group_2of8(static_cast<int>(p1), static_cast<uint16_t>(v & 0xFFFFu), static_cast<int>(p2),
+                              static_cast<uint16_t>(v >> 16), q);
+      }
+    }
+    uint32_t w = pos << (16 * ((G >> 2) & 1) + 8 * (G & 1));
+    w |= __shfl_xor(w, 1);
+    w |= __shfl_xor(w, 4);
+    if (row < nb && t < nt)
+      *reinterpret_cast<uint2*>(ap + static_cast<int64_t>(row) * ld_ap + 4 * G) =
+          make_uint2(q[0] | (static_cast<uint32_t>(q[1]) << 16), q[2] | (static_cast<uint32_t>(q[3]) << 16));
+    if ((lane & 5) == 0) words[(lane >> 3)][rl * 2 + ((lane >> 1) & 1)] = w;
+  }
+  __syncthreads();
+  const int wt = tid >> 5, wi = tid & 31;  // tile, (row, h) of the write-out
+  const int ot = blockIdx.x * kPackTiles + wt, orow = blockIdx.y * kPackRows + (wi >> 1);
+  if (ot < nt && orow < meta_rows)
+    meta[(static_cast<int64_t>(ot) * meta_rows + orow) * 2 + (wi & 1)] = words[wt][wi];
+}
+
 }  // namespace
 }  // namespace moc
 
 using namespace moc;
+
+extern "C" int moc_pack28_bf16(const void* sz, const void* idx, int64_t nb, int64_t inter, void* ap,
+                               int64_t ld_ap, uint32_t* meta, int64_t meta_rows, void* zero4k,
+                               void* stream) {
+  MOC_REQUIRE(nb >= 0 && inter >= 8 && inter % 8 == 0 && inter < (1LL << 30) && nb < (1LL << 30),
+              "moc_pack28_bf16: bad shape (intermediate must be a multiple of 8)");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(sz && idx && ap && meta, "moc_pack28_bf16: null pointer");
+  MOC_REQUIRE(reinterpret_cast<uintptr_t>(sz) % 4 == 0 && reinterpret_cast<uintptr_t>(idx) % 8 == 0,
+              "moc_pack28_bf16: sz must be 4-byte and idx 8-byte aligned");
+  const int64_t nt = (inter + 63) / 64;
+  MOC_REQUIRE(ld_ap >= 32 * nt && ld_ap % 8 == 0 && aligned16(ap),
+              "moc_pack28_bf16: ap needs 16-byte aligned rows of >= 32 * ceil(inter / 64) values");
+  MOC_REQUIRE(meta_rows >= nb && meta_rows % 64 == 0, "moc_pack28_bf16: meta_rows must be >= nb, a multiple of 64");
+  MOC_REQUIRE(zero4k == nullptr || aligned16(zero4k), "moc_pack28_bf16: unaligned counter block");
+  const dim3 grid(static_cast<unsigned>((nt + kPackTiles - 1) / kPackTiles),
+                  static_cast<unsigned>(meta_rows / kPackRows));
+  MOC_REQUIRE(grid.y <= 65535, "moc_pack28_bf16: too many rows");
+  pack28_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t*>(sz), static_cast<const int64_t*>(idx), (int)nb, (int)inter, (int)nt,
+      static_cast<uint16_t*>(ap), ld_ap, meta, (int)meta_rows, static_cast<uint32_t*>(zero4k));
+  return check_launch("pack28_kernel");
+}
 
 extern "C" int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t hidden,
                                              const void* w_gate, const void* w_up, int64_t inter,
@@ -408,10 +503,61 @@ extern "C" int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t 
   return check_launch("grouped_prefill_kernel");
 }
 
+// Layout of the 2:4-packed operand inside the workspace of the prefill path.
+namespace {
+struct Packed28 {
+  int64_t nt, ld_ap, meta_rows, ap_bytes, meta_bytes;
+};
+Packed28 packed28_layout(int64_t nb, int64_t inter) {
+  Packed28 p;
+  p.nt = (inter + 63) / 64;
+  p.ld_ap = 32 * p.nt;
+  p.meta_rows = (nb + 255) / 256 * 256;
+  p.ap_bytes = align256(nb * p.ld_ap * 2);
+  p.meta_bytes = align256(p.nt * p.meta_rows * 8);
+  return p;
+}
+
+// The compacted (structured-sparse) prefill form applies to the 2:8 layout:
+// k = inter / 4 entries per token, (top-1, top-2) of each 8-group.
+bool sparse28_applies(int64_t nb, int64_t k, int64_t inter) {
+  return nb > 64 && inter % 8 == 0 && k == inter / 4;
+}
+}  // namespace
+
+extern "C" int moc_grouped_top2_up_silu_packed_bf16(const void* x, int64_t nb, int64_t hidden,
+                                                    const void* w_gate, const void* w_up, int64_t inter,
+                                                    void* ap, int64_t ld_ap, uint32_t* meta,
+                                                    int64_t meta_rows, void* stream) {
+  MOC_REQUIRE(nb >= 0 && hidden >= 1 && inter >= 8, "moc_grouped_top2_up_silu_packed_bf16: bad shape");
+  MOC_REQUIRE(inter % 8 == 0, "intermediate=%lld must be divisible by 8", (long long)inter);
+  MOC_REQUIRE(hidden % 8 == 0, "moc_grouped_top2_up_silu_packed_bf16: hidden must be a multiple of 8");
+  MOC_REQUIRE(inter < (1LL << 30) && hidden < (1LL << 30) && nb < (1LL << 30),
+              "moc_grouped_top2_up_silu_packed_bf16: too large");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && w_gate && w_up && ap && meta, "moc_grouped_top2_up_silu_packed_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up) && aligned16(ap) && aligned16(meta),
+              "moc_grouped_top2_up_silu_packed_bf16: operands must be 16-byte aligned");
+  const int64_t nt = (inter + 63) / 64;
+  MOC_REQUIRE(ld_ap >= 32 * nt && ld_ap % 8 == 0,
+              "moc_grouped_top2_up_silu_packed_bf16: ld_ap must be a multiple of 8 and >= 32 * ceil(inter / 64)");
+  MOC_REQUIRE(meta_rows >= nb && nt * meta_rows * 8 < (1LL << 31),
+              "moc_grouped_top2_up_silu_packed_bf16: bad meta_rows");
+  const int rc = launch_gate_up_2of8(x, nb, hidden, w_gate, w_up, inter, nullptr, nullptr, as_stream(stream),
+                                     static_cast<uint16_t*>(ap), ld_ap, meta, meta_rows);
+  MOC_REQUIRE(rc != 1, "moc_grouped_top2_up_silu_packed_bf16: operands exceed 32-bit buffer addressing");
+  return rc;
+}
+
 extern "C" int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t inter,
                                                             int64_t hidden) {
   if (nb <= 0 || k <= 0 || inter <= 0 || hidden <= 0) return 0;
   if (nb <= 64) return moc_selected_down_workspace_size(nb, k, hidden);
+  if (sparse28_applies(nb, k, inter)) {
+    // packed values and positions, then the sparse down GEMM's workspace
+    const Packed28 p = packed28_layout(nb, inter);
+    return p.ap_bytes + p.meta_bytes + moc_sparse28_down_workspace_size(nb, inter, hidden);
+  }
   // dense z, then the down GEMM's own workspace
   return align256(nb * inter * 2) + moc_gemm_workspace_size(MOC_BF16, nb, hidden, inter, 0);
 }
@@ -430,6 +576,20 @@ extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, i
     return moc_selected_down_bf16(sz, idx, MOC_I64, nb, k, w_down_t, inter, hidden, y, workspace,
                                   workspace_bytes, stream);
   MOC_REQUIRE(inter % 8 == 0, "moc_selected_grouped_down_bf16: intermediate must be a multiple of 8");
+  if (sparse28_applies(nb, k, inter)) {
+    // pack (sz, idx) 2:4, clearing the GEMM's counters on the way, then the
+    // structured-sparse GEMM over W_down^T
+    const Packed28 p = packed28_layout(nb, inter);
+    char* base = static_cast<char*>(workspace);
+    uint32_t* meta = reinterpret_cast<uint32_t*>(base + p.ap_bytes);
+    char* gws = base + p.ap_bytes + p.meta_bytes;
+    const int64_t gbytes = moc_sparse28_down_workspace_size(nb, inter, hidden);
+    int rc = moc_pack28_bf16(sz, idx, nb, inter, base, p.ld_ap, meta, p.meta_rows,
+                             gbytes > 0 ? gws : nullptr, stream);
+    if (rc != MOC_OK) return rc;
+    return moc_sparse28_down_bf16(base, p.ld_ap, meta, p.meta_rows, nb, inter, w_down_t, hidden, 0, hidden,
+                                  y, hidden, gbytes > 0 ? gws : nullptr, gbytes, stream);
+  }
   int rc = moc_scatter_sparse_to_dense(MOC_BF16, sz, idx, MOC_I64, nb, k, inter, workspace, inter,
                                        stream);
   if (rc != MOC_OK) return rc;

@@ -140,6 +140,10 @@ def make_optimized_global_moc_graph_runner(module, batch_size: int = 1):
         return module._restore_output_shape(y_buf, original_shape)
 
     runner.graph = graph
+    # the graph's buffers live as long as the runner (a freed one would be
+    # handed to other tensors while replays still use it; the workspace
+    # carries the after-gate kernel's zeroed arrival counters between replays)
+    runner.buffers = (x_buf, gate_buf, y_buf, ws, up_w, down_t, gate_w)
     return runner
 
 

@@ -608,6 +608,66 @@ def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None
     return idx, sz
 
 
+def packed28_layout(nb: int, inter: int) -> tuple[int, int, int]:
+    """(channel tiles, ld_ap, meta_rows) of the 2:4-packed 2:8 operand."""
+    nt = (inter + 63) // 64
+    return nt, 32 * nt, round_up(max(nb, 1), 256)
+
+
+def packed28_buffers(nb: int, inter: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Empty (ap [nb, ld_ap] bf16, meta [nt, meta_rows, 2] int32) buffers."""
+    nt, ld_ap, meta_rows = packed28_layout(nb, inter)
+    return (_empty((nb, ld_ap), torch.bfloat16, device),
+            _empty((nt, meta_rows, 2), torch.int32, device))
+
+
+def grouped_top2_up_silu_packed(x, gate_weight, up_weight, ap, meta) -> None:
+    """The 2:8 gate/up + top-2-of-8 with the selection written 2:4-packed
+    (ap, meta from packed28_buffers) instead of as (idx, sz)."""
+    N.require_device(x, gate_weight, up_weight, ap, meta)
+    x, wg, wu = _bf16_contig(x, gate_weight, up_weight)
+    nb, hidden = x.shape
+    inter = wg.shape[0]
+    if inter % 8 != 0:
+        raise ValueError(f"intermediate={inter} must be divisible by 8")
+    if wg.shape != wu.shape or wg.shape[1] != hidden:
+        raise ValueError(f"H mismatch: x={tuple(x.shape)}, gate={tuple(wg.shape)}, up={tuple(wu.shape)}")
+    nt, ld_ap, meta_rows = packed28_layout(nb, inter)
+    if ap.shape != (nb, ld_ap) or meta.shape != (nt, meta_rows, 2):
+        raise ValueError("packed buffers do not match packed28_layout")
+    N.call("moc_grouped_top2_up_silu_packed_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(),
+           wu.data_ptr(), inter, ap.data_ptr(), ld_ap, meta.data_ptr(), meta_rows, N.stream_of(x))
+
+
+def sparse28_down_workspace(nb: int, inter: int, hidden: int, device) -> torch.Tensor:
+    """A zeroed workspace for sparse28_down (its counters start at zero and
+    every call leaves them zero, so it is reused without clearing)."""
+    b = N.query("moc_sparse28_down_workspace_size", nb, inter, hidden)
+    return torch.zeros((max(b, 1),), dtype=torch.uint8, device=device)
+
+
+def sparse28_down(ap, meta, inter: int, down_weight_t, *, workspace, out=None) -> torch.Tensor:
+    """y = A W_down (A 2:4-packed) on the structured-sparse MFMA; W_down
+    given transposed [inter, hidden]."""
+    N.require_device(ap, meta, down_weight_t, workspace, out)
+    nb = ap.shape[0]
+    wdt = down_weight_t if down_weight_t.is_contiguous() else down_weight_t.contiguous()
+    if wdt.shape[0] != inter or wdt.dtype != torch.bfloat16:
+        raise ValueError("down_weight_t must be a bf16 [inter, hidden] tensor")
+    hidden = wdt.shape[1]
+    nt, ld_ap, meta_rows = packed28_layout(nb, inter)
+    y = _empty((nb, hidden), torch.bfloat16, ap.device) if out is None else out
+    if y.shape != (nb, hidden) or not y.is_contiguous():
+        raise ValueError(f"out shape must be ({nb},{hidden})")
+    ws_bytes = N.query("moc_sparse28_down_workspace_size", nb, inter, hidden)
+    if workspace.numel() < ws_bytes:
+        raise ValueError(f"sparse28_down needs a workspace of {ws_bytes} bytes")
+    N.call("moc_sparse28_down_bf16", ap.data_ptr(), ld_ap, meta.data_ptr(), meta_rows, nb, inter,
+           wdt.data_ptr(), wdt.stride(0), 0, hidden, y.data_ptr(), y.stride(0), workspace.data_ptr(),
+           ws_bytes, N.stream_of(ap))
+    return y
+
+
 def selected_grouped_down_workspace_bytes(nb: int, k: int, inter: int, hidden: int) -> int:
     return N.query("moc_selected_grouped_down_workspace_size", nb, k, inter, hidden)
 

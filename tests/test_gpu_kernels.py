@@ -618,6 +618,138 @@ def test_grouped_2of8_1b_device_projections(nb):
     close(y, y_ref)
 
 
+def random_2of8(nb, inter, seed):
+    """A random 2:8 selection in moc_grouped_top2_up_silu_bf16's layout:
+    per 8-group two distinct channels in either order, N(0,1) bf16 values."""
+    g = gen(seed)
+    groups = inter // 8
+    pos = torch.argsort(torch.rand(nb, groups, 8, generator=g), dim=-1)[..., :2]
+    idx = (pos + 8 * torch.arange(groups)[None, :, None]).reshape(nb, groups * 2)
+    sz = torch.randn(nb, groups * 2, generator=g).to(torch.bfloat16)
+    return idx.to(torch.int64), sz
+
+
+def packed28(sz, idx, inter):
+    """moc_pack28_bf16 into fresh buffers -> (ap, ld_ap, meta, meta_rows)."""
+    nb = sz.shape[0]
+    nt = (inter + 63) // 64
+    ld_ap = 32 * nt
+    meta_rows = (nb + 255) // 256 * 256
+    ap = torch.full((nb, ld_ap), 7.0, dtype=torch.bfloat16, device=DEV)  # pad columns must be zeroed
+    meta = torch.full((nt, meta_rows, 2), -1, dtype=torch.int32, device=DEV)
+    N().call("moc_pack28_bf16", sz.data_ptr(), idx.data_ptr(), nb, inter, ap.data_ptr(), ld_ap,
+             meta.data_ptr(), meta_rows, None, N().stream_of(sz))
+    return ap, ld_ap, meta, meta_rows
+
+
+def sparse28_down(ap, ld_ap, meta, meta_rows, inter, w, w_kc):
+    nb = ap.shape[0]
+    hidden = w.shape[0] if w_kc else w.shape[1]
+    y = torch.empty(nb, hidden, dtype=torch.bfloat16, device=DEV)
+    ws_bytes = N().query("moc_sparse28_down_workspace_size", nb, inter, hidden)
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    N().call("moc_sparse28_down_bf16", ap.data_ptr(), ld_ap, meta.data_ptr(), meta_rows, nb, inter,
+             w.data_ptr(), w.stride(0), int(w_kc), hidden, y.data_ptr(), y.stride(0), ws.data_ptr(),
+             ws_bytes, N().stream_of(ap))
+    return y, ws
+
+
+@pytest.mark.parametrize("nb,hidden,inter", [(65, 64, 200), (300, 2048, 5464), (1000, 768, 2048),
+                                             (700, 72, 96), (4096, 2048, 5464)])
+@pytest.mark.parametrize("w_kc", [0, 1])
+def test_sparse28_down_vs_oracle(nb, hidden, inter, w_kc):
+    """The 2:4-packed 2:8 Down on the structured-sparse MFMA against the
+    oracle's gathered Down (f32 sums of the selected rows): whole tiles,
+    partial channel tiles (inter % 64 != 0), split-K (65 tokens: one tile
+    row), the two-part K split (4096 tokens: 128 tiles) and both W layouts;
+    every element within 2e-2.  The workspace's counters are zero again
+    after the call."""
+    idx, sz = random_2of8(nb, inter, 300 + nb + inter)
+    wd = (torch.randn(hidden, inter, generator=gen(301 + nb)) * 0.02).to(torch.bfloat16)
+    wdt = wd.t().contiguous()
+    ap, ld_ap, meta, meta_rows = packed28(sz.to(DEV), idx.to(DEV), inter)
+    w = (wd if w_kc else wdt).to(DEV)
+    y, ws = sparse28_down(ap, ld_ap, meta, meta_rows, inter, w, w_kc)
+    close(y, O.selected_down(sz, idx.numpy(), wdt))
+    assert int(ws[:4096].count_nonzero()) == 0
+    # the op path (pack + sparse GEMM over W_down^T inside one entry point)
+    y2 = K().selected_grouped_down(sz.to(DEV), idx.to(DEV), wdt.to(DEV))
+    if nb > 64:
+        assert torch.equal(y2, sparse28_down(ap, ld_ap, meta, meta_rows, inter, wdt.to(DEV), 0)[0])
+
+
+@pytest.mark.parametrize("nb,hidden,inter", [(300, 2048, 5464), (4096, 2048, 5464), (130, 64, 200)])
+def test_grouped_2of8_packed_epilogue(nb, hidden, inter):
+    """The gate/up kernel's packed epilogue writes exactly what
+    moc_pack28_bf16 makes of the (idx, sz) the same kernel writes unpacked
+    (every stored value and position bit of every token), and the module's
+    prefill path (packed gate/up, then the sparse Down) matches the oracle."""
+    g = gen(40 + nb)
+    x = torch.randn(nb, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, hidden, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, hidden, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    idx, sz = K().grouped_top2_up_silu(x, wg, wu)
+    ap_ref, _, meta_ref, _ = packed28(sz, idx, inter)
+    ap, meta = K().packed28_buffers(nb, inter, DEV)
+    K().grouped_top2_up_silu_packed(x, wg, wu, ap, meta)
+    assert torch.equal(ap, ap_ref)
+    assert torch.equal(meta[:, :nb], meta_ref[:, :nb])
+    from moc_amd.inference.inference_ffn import InferenceMoCSwiGLUFFN
+    m = InferenceMoCSwiGLUFFN(hidden, inter, inter // 4, grouped_a=2, grouped_b=8).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        m.gate_proj.weight.copy_(wg)
+        m.up_proj.weight.copy_(wu)
+        m.down_proj.weight.copy_((torch.randn(hidden, inter, generator=g) * 0.02).to(torch.bfloat16))
+    y = m(x, mode="moc_inference_grouped_top2of8")
+    wdt = m.down_proj.weight.t().contiguous().cpu()
+    close(y, O.selected_down(sz.cpu(), idx.cpu().numpy(), wdt))
+    y2 = m(x, mode="moc_inference_grouped_top2of8")  # workspace reused: same result
+    assert torch.equal(y, y2)
+
+
+def test_pack28_layout_and_bad_indices():
+    """moc_pack28_bf16 against a CPU packing of the documented layout (values
+    in channel order per 4-group, zeros elsewhere, 2-bit positions), and an
+    index outside its 8-group turns that token's output into NaN."""
+    nb, inter = 70, 136  # 3 channel tiles, the last one partial
+    idx, sz = random_2of8(nb, inter, 17)
+    ap, ld_ap, meta, meta_rows = packed28(sz.to(DEV), idx.to(DEV), inter)
+    nt = (inter + 63) // 64
+    want_ap = torch.zeros(nb, ld_ap, dtype=torch.bfloat16)
+    want_meta = torch.zeros(nt, meta_rows, 2, dtype=torch.int64)
+    dense = torch.zeros(nb, nt * 64, dtype=torch.bfloat16)
+    for r in range(nb):
+        dense[r, idx[r]] = sz[r]
+    sel = torch.zeros(nb, nt * 64, dtype=torch.bool)
+    sel.scatter_(1, idx, True)
+    for r in range(meta_rows):
+        for q in range(nt * 16):  # 4-groups
+            chans = [c for c in range(4 * q, 4 * q + 4) if r < nb and sel[r, c]]
+            if len(chans) == 2:
+                p = [chans[0] - 4 * q, chans[1] - 4 * q]
+            elif len(chans) == 1:
+                p = [0, 1] if chans[0] == 4 * q else [0, chans[0] - 4 * q]
+            else:
+                p = [0, 1]
+            if r < nb:
+                for slot in range(2):
+                    c = 4 * q + p[slot]
+                    want_ap[r, 2 * q + slot] = dense[r, c] if sel[r, c] else 0.0
+            t, rem = divmod(q, 16)
+            s, rem = divmod(rem, 8)
+            h, j = divmod(rem, 4)
+            for slot in range(2):
+                want_meta[t, r, h] |= p[slot] << (16 * s + 2 * (2 * j + slot))
+    assert torch.equal(ap.cpu(), want_ap)
+    assert torch.equal(meta.cpu().to(torch.int64) & 0xFFFFFFFF, want_meta)
+    bad = idx.clone()
+    bad[5, 6] = bad[5, 6] + 8  # channel of the next group
+    ap, ld_ap, meta, meta_rows = packed28(sz.to(DEV), bad.to(DEV), inter)
+    wd = (torch.randn(64, inter, generator=gen(5)) * 0.02).to(torch.bfloat16).to(DEV)
+    y, _ = sparse28_down(ap, ld_ap, meta, meta_rows, inter, wd, 1)
+    assert bool(torch.isnan(y[5]).all()) and not bool(torch.isnan(y[4]).any())
+
+
 def tie_heavy_rows(nb, inter, kind, seed):
     g = gen(seed)
     if kind == "levels":  # seven values: ~780 channels share each one
