@@ -81,10 +81,13 @@ def parse_args():
     p.add_argument("--roofline-only", action="store_true",
                    help="only the seven GEMM launches of the roofline (for rocprofv3 kernel "
                         "traces whose per-kernel averages match roofline.per_launch)")
-    p.add_argument("--pmc-target", choices=["gemm", "dx", "copy", "decode"], default=None,
+    p.add_argument("--pmc-target", choices=["gemm", "dx", "copy", "decode", "down28", "down28_dense"],
+                   default=None,
                    help="only launch one workload a few times (for rocprofv3 --pmc runs): the G,U "
                         "pair GEMM of the 1b layer, its dX GEMM (two products), a plain 256 MiB "
-                        "copy kernel (counter scale), or the B=1 decode layer over 8 weight sets")
+                        "copy kernel (counter scale), the B=1 decode layer over 8 weight sets, or "
+                        "config 4's 2:8 Down (down28: structured-sparse MFMA over the packed "
+                        "selection; down28_dense: the same selection scattered dense)")
     return p.parse_args()
 
 
@@ -179,6 +182,29 @@ def pmc_target(which: str) -> None:
             for wg, wu, wdt in layers:
                 K.gemv(x, wg, out=gate)
                 K.global_after_gate(x, gate, wu, wdt, K1B, workspace=ws, out=y)
+    elif which in ("down28", "down28_dense"):
+        # config 4's Down: 4096 tokens, the 1b shape padded to 5464 channels;
+        # the 2:4-packed selection on the structured-sparse MFMA, or the same
+        # selection scattered dense on the dense MFMA
+        t, d, inter = 4096, D1B, 5464
+        gen = torch.Generator(device="cuda").manual_seed(11)
+        groups = inter // 8
+        pos = torch.argsort(torch.rand(t, groups, 8, device="cuda", generator=gen), dim=-1)[..., :2]
+        idx = (pos + 8 * torch.arange(groups, device="cuda")[None, :, None]).reshape(t, groups * 2)
+        sz = torch.randn(t, groups * 2, device="cuda", generator=gen).to(torch.bfloat16)
+        wdt = (torch.randn(inter, d, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+        if which == "down28":
+            ap, meta = K.packed28_buffers(t, inter, "cuda")
+            nt, ld_ap, meta_rows = K.packed28_layout(t, inter)
+            N.call("moc_pack28_bf16", sz.data_ptr(), idx.data_ptr(), t, inter, ap.data_ptr(), ld_ap,
+                   meta.data_ptr(), meta_rows, None, N.stream_of(sz))
+            ws = K.sparse28_down_workspace(t, inter, d, "cuda")
+            for _ in range(5):
+                K.sparse28_down(ap, meta, inter, wdt, workspace=ws)
+        else:
+            z = K.scatter_sparse_to_dense(sz, idx, inter)
+            for _ in range(5):
+                K.gemm(z, wdt)
     else:
         rows, cols = 16384, 8192  # 256 MiB of bf16 read and written
         src = torch.ones(rows, cols, device="cuda", dtype=torch.bfloat16)

@@ -279,8 +279,11 @@ __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_
     for (int j = 0; j < W; ++j) {
       if constexpr (KEY_BITS == 16) {
         if (pass == 0) {
-          bump((w[j] >> 8) & 0xFFu);
-          bump(w[j] >> 24);
+          // padding channels (key 0) are never counted: they would all hit
+          // bin 0 of their copy at once (a serialised atomic per lane), and
+          // bin 0 holds no real key
+          if ((w[j] & 0xFFFFu) != 0u) bump((w[j] >> 8) & 0xFFu);
+          if ((w[j] >> 16) != 0u) bump(w[j] >> 24);
         } else {
           // (key - phi:00) per half; off-prefix keys land at >= 256 -> spare
           const sel_u16x2 x = __builtin_elementwise_min(
