@@ -175,13 +175,11 @@ def pmc_target(which: str) -> None:
             wdt = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
             layers.append((wg, wu, wdt))
         x = torch.randn(1, D1B, device="cuda", generator=gen).to(torch.bfloat16)
-        gate = torch.empty(1, I1B, device="cuda", dtype=torch.bfloat16)
         y = torch.empty(1, D1B, device="cuda", dtype=torch.bfloat16)
-        ws = K.global_after_gate_workspace(1, I1B, K1B, D1B, "cuda")
+        ws = K.global_decode_workspace(1, I1B, K1B, D1B, "cuda")
         for _ in range(3):
             for wg, wu, wdt in layers:
-                K.gemv(x, wg, out=gate)
-                K.global_after_gate(x, gate, wu, wdt, K1B, workspace=ws, out=y)
+                K.global_decode(x, wg, wu, wdt, K1B, workspace=ws, out=y)
     elif which in ("down28", "down28_dense"):
         # config 4's Down: 4096 tokens, the 1b shape padded to 5464 channels;
         # the 2:4-packed selection on the structured-sparse MFMA, or the same
@@ -383,12 +381,11 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
     x = torch.randn(nb, d, device="cuda", generator=gen).to(torch.bfloat16)
     gate = [torch.empty(nb, inter, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
     ys = [torch.empty(nb, d, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
-    ws = K.global_after_gate_workspace(nb, inter, k, d, "cuda")
+    ws = K.global_decode_workspace(nb, inter, k, d, "cuda")
 
     def run_all():
-        for (wg, wu, wdt), g, y in zip(layers, gate, ys):
-            K.gemv(x, wg, out=g)
-            K.global_after_gate(x, g, wu, wdt, k, workspace=ws, out=y)
+        for (wg, wu, wdt), y in zip(layers, ys):
+            K.global_decode(x, wg, wu, wdt, k, workspace=ws, out=y)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -415,7 +412,8 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
     # algorithmic bytes: all of W_gate + the union of selected rows of W_up and
     # W_down^T + activations (x in, G out+in, y out), counted from the masks
     union = []
-    for g in gate:
+    for (wg, _, _), g in zip(layers, gate):
+        K.gemv(x, wg, out=g)
         _, idx, _ = K.topk_rows(g, k, want_vals=False)
         union.append(int(torch.unique(idx).numel()))
     u_avg = sum(union) / len(union)

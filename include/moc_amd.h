@@ -265,6 +265,23 @@ int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, 
                                         void* y, void* idx_out, void* workspace,
                                         int64_t workspace_bytes, void* stream);
 
+/* Workspace bytes moc_global_decode_bf16 needs: the after-gate workspace
+ * followed by the gate scores. */
+int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, int64_t k, int64_t hidden);
+
+/* The global-MoC decode layer from x (nb <= 16 tokens): the gate projection
+ * G = x W_gate^T (bf16, into the workspace) and then
+ * moc_global_after_gate_bf16 on it, i.e. module.gate_proj(x) followed by
+ * moc_native::optimized_global_after_gate_bf16 (moc/inference/
+ * inference_ffn.py:181-196, optimized_global_moc_ext.cu:457-540).  From 4
+ * tokens on the dense U = x W_up^T the after-gate kernel uses is computed in
+ * the same GEMV launch as G.  Same selection, rounding and results as the
+ * two calls; same workspace rules (64 KB of counters at its start, zero
+ * before the first call). */
+int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
+                           const void* w_up, int64_t inter, const void* w_down_t, int64_t k, void* y,
+                           void* idx_out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Bytes of the library's own device scratch array (one per GPU, held until
  * the process ends) behind moc_global_after_gate_noalloc_bf16. */
 #define MOC_NOALLOC_SCRATCH_BYTES (4 * 1024 * 1024)

@@ -73,6 +73,9 @@ SIGNATURES: dict[str, tuple] = {
     "moc_selected_down_bf16": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
                                       _i64, _vp]),
     "moc_global_after_gate_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
+    "moc_global_decode_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
+    "moc_global_decode_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+                                      _i64, _vp]),
     "moc_global_after_gate_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
                                           _i64, _vp]),
     "moc_grouped_top2_up_silu_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),

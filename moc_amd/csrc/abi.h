@@ -30,11 +30,12 @@ int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb
 constexpr int64_t kAfterGateCounterBytes = 64 * 1024;
 
 // moc_global_after_gate_bf16 / _residual_bf16 (res may be null, idx_out may
-// be null) on a caller workspace (decode.hip).
+// be null) on a caller workspace (decode.hip).  up_ready: the dense U that
+// the workspace holds from 4 tokens on was already written by the caller.
 int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
                       int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
                       const void* res, void* y, void* idx_out, void* workspace,
-                      int64_t workspace_bytes, void* stream);
+                      int64_t workspace_bytes, void* stream, bool up_ready = false);
 
 // MoC 2:8 gate/up + top-2-of-8 for nb tokens on the MFMA GEMM kernel
 // (gemm.hip); 1: shape not supported there (nothing launched).

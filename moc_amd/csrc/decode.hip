@@ -72,16 +72,31 @@ constexpr int kGvLdsBytes = 128 * 1024;
 constexpr int kGvMaxHidden = 2048;
 constexpr int kGvMaxSteps = kGvMaxHidden / 32 / 4;  // k steps per wave
 
+// Pair form (W2 != nullptr): workgroups nwg .. gridDim.x - 1 do the same for
+// a second matrix W2 [rows2, hidden] into y2, so two projections of the same
+// tokens stream in one launch.
 __global__ __launch_bounds__(256) void gemv_stream_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int nb, const uint16_t* __restrict__ W,
     int64_t ldw, int rows, int hidden, int nwg, uint16_t* __restrict__ y, int64_t ldy,
-    int wbytes) {
+    int wbytes, const uint16_t* __restrict__ W2, int64_t ldw2, int rows2, uint16_t* __restrict__ y2,
+    int64_t ldy2, int wbytes2) {
   __shared__ __attribute__((aligned(1024))) char lw[kGvLdsBytes];
   __shared__ f32x4_t red[2][4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r_lo = static_cast<int>(static_cast<int64_t>(blockIdx.x) * rows / nwg);
-  const int r_hi = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * rows / nwg);
+  int blk = static_cast<int>(blockIdx.x);
+  if (W2 != nullptr && blk >= nwg) {
+    blk -= nwg;
+    nwg = static_cast<int>(gridDim.x) - nwg;
+    W = W2;
+    ldw = ldw2;
+    rows = rows2;
+    y = y2;
+    ldy = ldy2;
+    wbytes = wbytes2;
+  }
+  const int r_lo = static_cast<int>(static_cast<int64_t>(blk) * rows / nwg);
+  const int r_hi = static_cast<int>(static_cast<int64_t>(blk + 1) * rows / nwg);
   const int nr = r_hi - r_lo;
   const int cpr = hidden / 8;  // 16-byte chunks per row (a multiple of 16)
 
@@ -229,15 +244,29 @@ __global__ __launch_bounds__(256) void gemv16_kernel(const uint16_t* __restrict_
 // benchmark_decode.py:101-109,303): xn = bf16(bf16(x * r) * w) with
 // r = 1 / sqrt(mean(x^2) + eps) in f32; every wave normalises its own copy
 // of x, and wave 0 of workgroup 0 also writes xn for the kernels after it.
+// Pair form (W2 != nullptr): the waves from row2_start on (a workgroup
+// boundary) take the rows of a second matrix W2 [rows2, hidden] into y2 (two
+// projections of the same tokens in one launch).
 template <int NB, int CHN, bool NORM>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                         const uint16_t* __restrict__ W, int64_t ldw,
                                                         int rows, int hidden,
                                                         uint16_t* __restrict__ y, int64_t ldy,
                                                         const uint16_t* __restrict__ norm_w, float eps,
-                                                        uint16_t* __restrict__ xn, int64_t ldxn) {
+                                                        uint16_t* __restrict__ xn, int64_t ldxn,
+                                                        const uint16_t* __restrict__ W2, int64_t ldw2,
+                                                        int row2_start, int rows2, uint16_t* __restrict__ y2,
+                                                        int64_t ldy2) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (W2 != nullptr && row >= row2_start) {
+    row -= row2_start;
+    rows = rows2;
+    W = W2;
+    ldw = ldw2;
+    y = y2;
+    ldy = ldy2;
+  }
   if (row >= rows) return;
   const int nch = hidden / 8;
   uint4 wv[CHN];
@@ -299,13 +328,18 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
 template <int NB, bool NORM = false>
 void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, int rows, int hidden,
                       void* y, int64_t ldy, hipStream_t st, const void* norm_w = nullptr,
-                      float eps = 0.f, void* xn = nullptr, int64_t ldxn = 0) {
-  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+                      float eps = 0.f, void* xn = nullptr, int64_t ldxn = 0, const void* W2 = nullptr,
+                      int64_t ldw2 = 0, int rows2 = 0, void* y2 = nullptr, int64_t ldy2 = 0) {
+  // the pair's second row range starts at a workgroup boundary
+  const int wg1 = (rows + 3) / 4, wg2 = W2 != nullptr ? (rows2 + 3) / 4 : 0;
+  const dim3 grid(static_cast<unsigned>(wg1 + wg2)), block(256);
   const int chn = (hidden / 8 + 63) / 64;
 #define MOC_GR(C)                                                                                  \
   gemv_rows_kernel<NB, C, NORM><<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (const uint16_t*)W, \
                                                          ldw, rows, hidden, (uint16_t*)y, ldy,       \
-                                                         (const uint16_t*)norm_w, eps, (uint16_t*)xn, ldxn)
+                                                         (const uint16_t*)norm_w, eps, (uint16_t*)xn, ldxn, \
+                                                         (const uint16_t*)W2, ldw2, wg1 * 4, rows2, (uint16_t*)y2, \
+                                                         ldy2)
   if (chn <= 1) MOC_GR(1);
   else if (chn <= 2) MOC_GR(2);
   else if (chn <= 4) MOC_GR(4);
@@ -724,6 +758,53 @@ void launch_fused(const void* x, int hidden, const void* gate, int inter, int k,
 
 using namespace moc;
 
+namespace moc {
+// One GEMV launch for W [rows, hidden] -> y, or (W2 != nullptr) for W and a
+// second matrix W2 [rows2, hidden] -> y2 of the same tokens; shapes checked
+// by the callers.  The streaming form needs each matrix within 2 GiB.
+int gemv_launch(const void* x, int64_t ldx, int64_t nb, const void* W, int64_t ldw, int64_t rows,
+                int64_t hidden, void* y, int64_t ldy, const void* W2, int64_t ldw2, int64_t rows2, void* y2,
+                int64_t ldy2, hipStream_t st) {
+  if (nb <= 4 && hidden <= 4096) {
+    switch (nb) {
+      case 1: launch_gemv_rows<1>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, nullptr, 0.f, nullptr, 0, W2, ldw2, (int)rows2, y2, ldy2); break;
+      case 2: launch_gemv_rows<2>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, nullptr, 0.f, nullptr, 0, W2, ldw2, (int)rows2, y2, ldy2); break;
+      case 3: launch_gemv_rows<3>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, nullptr, 0.f, nullptr, 0, W2, ldw2, (int)rows2, y2, ldy2); break;
+      default: launch_gemv_rows<4>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st, nullptr, 0.f, nullptr, 0, W2, ldw2, (int)rows2, y2, ldy2); break;
+    }
+    return check_launch("gemv_rows_kernel");
+  }
+  const int64_t wbytes = rows * ldw * 2, wbytes2 = W2 != nullptr ? rows2 * ldw2 * 2 : 0;
+  const int64_t max_rows = kGvLdsBytes / (2 * hidden);
+  if (hidden % 128 == 0 && hidden <= kGvMaxHidden && max_rows >= 16 && wbytes < (1LL << 31) - 1024 &&
+      wbytes2 < (1LL << 31) - 1024) {
+    // balanced split over >= 256 workgroups (per matrix) with <= min(32,
+    // max_rows) rows each
+    const int64_t cap = max_rows < kGvMaxRows ? max_rows : kGvMaxRows;
+    auto split = [&](int64_t r) {
+      int64_t n = (r + cap - 1) / cap;
+      if (n < 256) n = r < 256 ? r : 256;
+      return n;
+    };
+    const int64_t nwg = split(rows), nwg2 = W2 != nullptr ? split(rows2) : 0;
+    gemv_stream_kernel<<<dim3(static_cast<unsigned>(nwg + nwg2)), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw, (int)rows, (int)hidden,
+        (int)nwg, (uint16_t*)y, ldy, (int)wbytes, (const uint16_t*)W2, ldw2, (int)rows2, (uint16_t*)y2, ldy2,
+        (int)wbytes2);
+    return check_launch("gemv_stream_kernel");
+  }
+  const dim3 grid(static_cast<unsigned>((rows + 15) / 16)), block(256);
+  gemv16_kernel<<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw,
+                                        (int)rows, (int)hidden, (uint16_t*)y, ldy);
+  int rc = check_launch("gemv16_kernel");
+  if (rc != MOC_OK || W2 == nullptr) return rc;
+  const dim3 grid2(static_cast<unsigned>((rows2 + 15) / 16));
+  gemv16_kernel<<<grid2, block, 0, st>>>((const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W2, ldw2,
+                                         (int)rows2, (int)hidden, (uint16_t*)y2, ldy2);
+  return check_launch("gemv16_kernel");
+}
+}  // namespace moc
+
 extern "C" int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void* W, int64_t ldw,
                              int64_t rows, int64_t hidden, void* y, int64_t ldy, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_gemv_bf16: 0 <= nb <= 16 tokens (got %lld)", (long long)nb);
@@ -735,33 +816,7 @@ extern "C" int moc_gemv_bf16(const void* x, int64_t ldx, int64_t nb, const void*
   if (nb == 0 || rows == 0) return MOC_OK;
   MOC_REQUIRE(x && W && y, "moc_gemv_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(W), "moc_gemv_bf16: x and W must be 16-byte aligned");
-  hipStream_t st = as_stream(stream);
-  if (nb <= 4 && hidden <= 4096) {
-    switch (nb) {
-      case 1: launch_gemv_rows<1>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
-      case 2: launch_gemv_rows<2>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
-      case 3: launch_gemv_rows<3>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
-      default: launch_gemv_rows<4>(x, ldx, W, ldw, (int)rows, (int)hidden, y, ldy, st); break;
-    }
-    return check_launch("gemv_rows_kernel");
-  }
-  const int64_t wbytes = rows * ldw * 2;
-  const int64_t max_rows = kGvLdsBytes / (2 * hidden);
-  if (hidden % 128 == 0 && hidden <= kGvMaxHidden && max_rows >= 16 &&
-      wbytes < (1LL << 31) - 1024) {
-    // balanced split over >= 256 workgroups with <= min(32, max_rows) rows each
-    const int64_t cap = max_rows < kGvMaxRows ? max_rows : kGvMaxRows;
-    int64_t nwg = (rows + cap - 1) / cap;
-    if (nwg < 256) nwg = rows < 256 ? rows : 256;
-    gemv_stream_kernel<<<dim3(static_cast<unsigned>(nwg)), 256, 0, st>>>(
-        (const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw, (int)rows, (int)hidden,
-        (int)nwg, (uint16_t*)y, ldy, (int)wbytes);
-    return check_launch("gemv_stream_kernel");
-  }
-  const dim3 grid(static_cast<unsigned>((rows + 15) / 16)), block(256);
-  gemv16_kernel<<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw,
-                                        (int)rows, (int)hidden, (uint16_t*)y, ldy);
-  return check_launch("gemv16_kernel");
+  return gemv_launch(x, ldx, nb, W, ldw, rows, hidden, y, ldy, nullptr, 0, 0, nullptr, 0, as_stream(stream));
 }
 
 extern "C" int moc_gemv_rmsnorm_bf16(const void* x, int64_t ldx, int64_t nb, const void* norm_w,
@@ -879,7 +934,8 @@ extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inte
 namespace moc {
 int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter, int64_t hidden,
                       const void* w_up, const void* w_down_t, int64_t k, const void* res, void* y,
-                      void* idx_out, void* workspace, int64_t workspace_bytes, void* stream) {
+                      void* idx_out, void* workspace, int64_t workspace_bytes, void* stream,
+                      bool up_ready) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64, "moc_global_after_gate_bf16: bad shape");
   MOC_REQUIRE(hidden % 64 == 0, "moc_global_after_gate_bf16: hidden must be a multiple of 64");
@@ -900,9 +956,12 @@ int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_
   const void* up = w_up;
   int64_t up_ld = 0;
   if (dense_up_bytes(nb, inter) > 0) {
+    // up_ready: the caller's pair GEMV has already written U there
     void* u = ws + kFusedCounterBytes + nb * f.P * hidden * 4;
-    const int rc = moc_gemv_bf16(x, hidden, nb, w_up, hidden, inter, hidden, u, inter, stream);
-    if (rc != MOC_OK) return rc;
+    if (!up_ready) {
+      const int rc = moc_gemv_bf16(x, hidden, nb, w_up, hidden, inter, hidden, u, inter, stream);
+      if (rc != MOC_OK) return rc;
+    }
     up = u;
     up_ld = inter;
   }
@@ -923,6 +982,48 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
                                           void* workspace, int64_t workspace_bytes, void* stream) {
   return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out,
                            workspace, workspace_bytes, stream);
+}
+
+// The whole decode layer from x: the gate projection (with, from 4 tokens
+// on, the dense U of the same tokens in the same GEMV launch: two
+// projections of one x stream as one pass over both weights), then the
+// after-gate kernel.  Workspace: the after-gate workspace, then G.
+extern "C" int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, int64_t k, int64_t hidden) {
+  const int64_t a = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
+  return a > 0 ? a + align256(nb * inter * 2) : 0;
+}
+
+extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
+                                      const void* w_up, int64_t inter, const void* w_down_t, int64_t k,
+                                      void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_decode_bf16: 0 <= nb <= 16 tokens");
+  MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64 && hidden % 64 == 0 && hidden < (1LL << 30),
+              "moc_global_decode_bf16: bad shape");
+  MOC_REQUIRE(k >= 1 && k <= inter, "invalid k");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && w_gate && w_up && w_down_t && y, "moc_global_decode_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down_t),
+              "moc_global_decode_bf16: x and weights must be 16-byte aligned");
+  const int64_t need = moc_global_decode_workspace_size(nb, inter, k, hidden);
+  MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "moc_global_decode_bf16: workspace of %lld bytes required", (long long)need);
+  const int64_t abytes = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
+  char* ws = static_cast<char*>(workspace);
+  void* g = ws + abytes;
+  hipStream_t st = as_stream(stream);
+  int rc;
+  const bool pair = dense_up_bytes(nb, inter) > 0;
+  if (pair) {
+    const FusedShape f = fused_shape(nb, k, hidden);
+    void* u = ws + kFusedCounterBytes + nb * f.P * hidden * 4;
+    rc = gemv_launch(x, hidden, nb, w_gate, hidden, inter, hidden, g, inter, w_up, hidden, inter, u, inter, st);
+  } else {
+    rc = gemv_launch(x, hidden, nb, w_gate, hidden, inter, hidden, g, inter, nullptr, 0, 0, nullptr, 0, st);
+  }
+  if (rc != MOC_OK) return rc;
+  return global_after_gate(x, g, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out, workspace, abytes,
+                           stream, pair);
 }
 
 extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,

@@ -111,14 +111,22 @@ def make_optimized_global_moc_graph_runner(module, batch_size: int = 1):
     x_buf = torch.zeros(batch_size, hidden, device=device, dtype=dtype)
     gate_buf = torch.empty(batch_size, inter, device=device, dtype=dtype)
     y_buf = torch.empty(batch_size, hidden, device=device, dtype=dtype)
-    ws = K.global_after_gate_workspace(batch_size, inter, k, hidden, device)
     up_w = module.up_proj.weight.contiguous()
     down_t = module._down_weight_t.contiguous()
     gate_w = module.gate_proj.weight.contiguous()
+    if batch_size <= 16 and dtype == torch.bfloat16:
+        # gate GEMV (+ dense U from 4 tokens on, same launch) and the
+        # after-gate kernel through the one layer entry
+        ws = K.global_decode_workspace(batch_size, inter, k, hidden, device)
 
-    def path():
-        K.gemv(x_buf, gate_w, out=gate_buf)
-        K.global_after_gate(x_buf, gate_buf, up_w, down_t, k, workspace=ws, out=y_buf)
+        def path():
+            K.global_decode(x_buf, gate_w, up_w, down_t, k, workspace=ws, out=y_buf)
+    else:
+        ws = K.global_after_gate_workspace(batch_size, inter, k, hidden, device)
+
+        def path():
+            K.gemv(x_buf, gate_w, out=gate_buf)
+            K.global_after_gate(x_buf, gate_buf, up_w, down_t, k, workspace=ws, out=y_buf)
 
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())

@@ -577,6 +577,40 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
     return y
 
 
+def global_decode_workspace(nb: int, inter: int, k: int, hidden: int, device) -> torch.Tensor:
+    """A fresh zero-initialised workspace for global_decode."""
+    nbytes = N.query("moc_global_decode_workspace_size", nb, inter, int(k), hidden)
+    return torch.zeros((max(nbytes, 256),), dtype=torch.uint8, device=device)
+
+
+def global_decode(x, gate_weight, up_weight, down_weight_t, k: int, *, workspace=None, out=None,
+                  idx_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The global-MoC decode layer from x (<= 16 tokens): gate projection,
+    then Top-K + selected Up * SiLU + selected Down; the result of
+    global_after_gate(x, gemv(x, gate_weight), ...)."""
+    N.require_device(x, gate_weight, up_weight, down_weight_t, idx_out)
+    x, wg, wu, wdt = _bf16_contig(x, gate_weight, up_weight, down_weight_t)
+    nb, hidden = x.shape
+    inter = wg.shape[0]
+    if nb > 16:
+        raise ValueError(f"global_decode takes at most 16 tokens (got {nb})")
+    if wg.shape != (inter, hidden) or wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
+        raise ValueError("gate_weight, up_weight and down_weight_t must be [intermediate, hidden]")
+    if idx_out is not None and (idx_out.dtype != torch.int32 or idx_out.shape != (nb, int(k))
+                                or not idx_out.is_contiguous()):
+        raise ValueError(f"idx_out must be a contiguous int32 [{nb}, {int(k)}] tensor")
+    y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
+    ws_bytes = N.query("moc_global_decode_workspace_size", nb, inter, int(k), hidden)
+    if workspace is None:
+        workspace = _decode_workspace(x.device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"global_decode: workspace of {ws_bytes} bytes required")
+    N.call("moc_global_decode_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(), wu.data_ptr(), inter,
+           wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out), workspace.data_ptr(), ws_bytes,
+           N.stream_of(x))
+    return y
+
+
 # ----------------------------------------------------------------------- 2:8
 def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None,
                          norm_weight: torch.Tensor | None = None, eps: float = 1e-6):

@@ -241,10 +241,20 @@ def test_inference_global_modes(nb):
     close(m(x, mode="masked_reference")[:, 0], y_ref, 2e-2, 2e-2, "masked_reference")
     del gate
     runner = make_optimized_global_moc_graph_runner(m, batch_size=nb)
+    x2 = torch.randn(nb, 1, d, device=DEV, dtype=torch.bfloat16)
     for _ in range(3):  # replays must all agree with the eager result
         yr = runner(x)
         torch.cuda.synchronize()
         close(yr, y, 0, 0, "graph replay")
+        # eager work (the module's own workspace) and a replay on other input
+        # between the checked replays; temporaries freed meanwhile must not
+        # land in the graph's buffers
+        y2 = m(x2)
+        junk = [torch.full((1 << 20,), 7.0, device=DEV) for _ in range(4)]
+        yr2 = runner(x2)
+        torch.cuda.synchronize()
+        close(yr2, y2, 0, 0, "graph replay, second input")
+        del junk
 
 
 @pytest.mark.parametrize("nb", [1, 4, 16])
@@ -321,10 +331,17 @@ def test_inference_moc28_modes(nb):
     y_ref, _, _ = O.masked_reference(x, wg, wu, wd, inter // 4, grouped=True)
     close(y, y_ref, 2e-2, 2e-2, "2:8 native vs oracle")
     runner = m.make_moc2_8_graph_runner(batch_size=nb)
+    x2 = xd.flip(0).contiguous()
     for _ in range(3):
         yr = runner(xd)
         torch.cuda.synchronize()
         close(yr, y, 0, 0, "2:8 graph replay")
+        # eager work of the same module (its own buffers and workspace) and a
+        # replay on other input between the checked replays
+        y_other = m(x2)
+        yr2 = runner(x2)
+        torch.cuda.synchronize()
+        close(yr2, y_other, 0, 0, "2:8 graph replay, second input")
 
 
 def test_ffn_bf16_350m_shape_config5():

@@ -471,6 +471,33 @@ def test_global_decode_path_1b(nb):
     close(y2, y, rtol=1e-2, atol=1e-3)
 
 
+@pytest.mark.parametrize("nb,inter,d", [(1, 5461, 2048), (3, 5461, 2048), (4, 5461, 2048),
+                                         (5, 5461, 2048), (16, 5461, 2048), (4, 1000, 256),
+                                         (8, 777, 4096)])
+def test_global_decode_layer_entry(nb, inter, d):
+    """moc_global_decode_bf16 (gate GEMV, from 4 tokens on with the dense U
+    in the same launch, then the after-gate kernel) equals gemv +
+    global_after_gate bit for bit: y and the selected channels.  (8, 777,
+    4096) takes the GEMV fallback that launches twice; every G row is also
+    checked against the f32 product."""
+    k = max(1, inter // 5)
+    g = gen(360 + nb + inter)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    G = K().gemv(x, wg)
+    bf16_close(G.cpu(), x.float().cpu() @ wg.float().cpu().t(), ulps=1, atol=1e-3)
+    i_two = torch.empty(nb, k, dtype=torch.int32, device=DEV)
+    y_two = K().global_after_gate(x, G, wu, wdt, k, idx_out=i_two)
+    i_one = torch.empty(nb, k, dtype=torch.int32, device=DEV)
+    ws = K().global_decode_workspace(nb, inter, k, d, DEV)
+    for _ in range(2):  # the counters are left zero for the next call
+        y_one = K().global_decode(x, wg, wu, wdt, k, workspace=ws, idx_out=i_one)
+        assert torch.equal(i_one, i_two)
+        assert torch.equal(y_one, y_two)
+
+
 @pytest.mark.parametrize("nb", [1, 2, 3, 4])
 def test_gemv_rmsnorm_fused_prologue(nb):
     """The gate GEMV with the FFN's RMSNorm in front: xn matches the
