@@ -88,27 +88,81 @@ __device__ __forceinline__ uint32_t f32_order_key(uint32_t u) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
 
-// MoC 2:8: top-2 of one group of 8 channels from bf16-rounded g[8], u[8]
-// (values as f32), emitted as (idx, sz) pairs: top-1 is the largest gate
-// value with the lowest index among equal maxima, top-2 the largest of the
-// other seven under the same rule, sz = bf16((g * sigmoid(g)) * u) in f32
+// MoC 2:8: top-2 of one group of 8 channels from its bf16 gate and up
+// values (gw, uw: channel 2e in the low half of word e, 2e + 1 in the high
+// half): top-1 is the largest gate value with the lowest index among equal
+// maxima, top-2 the largest of the other seven under the same rule (NaN
+// above +inf, -0 equal to +0), sz = bf16((g * sigmoid(g)) * u) in f32
 // (moc/inference/triton_fused_ffn_kernels.py:103-114,126-129).
+// Each channel's key is its 16-bit order key (0x8000 + |v| for v >= 0,
+// 0x8000 - |v| for v < 0, NaN 0xFFFF) above 7 - index, so the eight keys
+// are distinct, a larger key is the better channel, and the top two come
+// out of a max/min tournament.
+typedef unsigned short g8_u16x2 __attribute__((ext_vector_type(2)));
+typedef short g8_s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void select_group_top2_bits(const uint32_t (&gw)[4], const uint32_t (&uw)[4],
+                                                       int& b1, int& b2, uint16_t& s1, uint16_t& s2) {
+  uint32_t k[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const g8_u16x2 v = __builtin_bit_cast(g8_u16x2, gw[e]);
+    const g8_u16x2 m = __builtin_bit_cast(g8_u16x2, __builtin_bit_cast(g8_s16x2, gw[e]) >> 15);
+    const g8_u16x2 a = v & static_cast<unsigned short>(0x7FFF);
+    uint32_t key2 = __builtin_bit_cast(uint32_t, ((a ^ m) + static_cast<unsigned short>(0x8000)) - m);
+    // NaN: |v| > 0x7F80 in either half -> key 0xFFFF
+    const uint32_t lo_nan = (a.x > 0x7F80u) ? 0xFFFFu : 0u, hi_nan = (a.y > 0x7F80u) ? 0xFFFF0000u : 0u;
+    key2 |= lo_nan | hi_nan;
+    k[2 * e] = (key2 << 16) | static_cast<uint32_t>(7 - 2 * e);
+    k[2 * e + 1] = (key2 & 0xFFFF0000u) | static_cast<uint32_t>(6 - 2 * e);
+  }
+  uint32_t f[4], sc[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    f[p] = max(k[2 * p], k[2 * p + 1]);
+    sc[p] = min(k[2 * p], k[2 * p + 1]);
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const uint32_t hi = max(f[2 * p], f[2 * p + 1]), lo = min(f[2 * p], f[2 * p + 1]);
+    sc[p] = max(lo, max(sc[2 * p], sc[2 * p + 1]));
+    f[p] = hi;
+  }
+  const uint32_t F = max(f[0], f[1]);
+  const uint32_t S = max(min(f[0], f[1]), max(sc[0], sc[1]));
+  b1 = 7 - static_cast<int>(F & 7u);
+  b2 = 7 - static_cast<int>(S & 7u);
+  auto value_of = [](const uint32_t (&w4)[4], int b) {
+    const uint32_t w = (b >> 1) == 0 ? w4[0] : (b >> 1) == 1 ? w4[1] : (b >> 1) == 2 ? w4[2] : w4[3];
+    return __uint_as_float((b & 1) ? (w & 0xFFFF0000u) : (w << 16));
+  };
+  const float g1 = value_of(gw, b1), g2 = value_of(gw, b2);
+  s1 = bf16_rne((g1 * sigmoid_f32(g1)) * value_of(uw, b1));
+  s2 = bf16_rne((g2 * sigmoid_f32(g2)) * value_of(uw, b2));
+}
+
+// The same from bf16-exact f32 values g[8], u[8].
 __device__ __forceinline__ void select_group_top2(const float* g, const float* u, int& b1, int& b2,
                                                   uint16_t& s1, uint16_t& s2) {
-  uint32_t key[8];
+  uint32_t gw[4], uw[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) key[j] = bf16_order_key(f32_to_bf16(g[j]));
-  b1 = 0;
-#pragma unroll
-  for (int j = 1; j < 8; ++j)
-    if (key[j] > key[b1]) b1 = j;
-  b2 = (b1 == 0) ? 1 : 0;
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (j != b1 && key[j] > key[b2]) b2 = j;
-  const float g1 = g[b1], g2 = g[b2];
-  s1 = f32_to_bf16((g1 * sigmoid_f32(g1)) * u[b1]);
-  s2 = f32_to_bf16((g2 * sigmoid_f32(g2)) * u[b2]);
+  for (int e = 0; e < 4; ++e) {
+    gw[e] = (__float_as_uint(g[2 * e]) >> 16) | (__float_as_uint(g[2 * e + 1]) & 0xFFFF0000u);
+    uw[e] = (__float_as_uint(u[2 * e]) >> 16) | (__float_as_uint(u[2 * e + 1]) & 0xFFFF0000u);
+  }
+  select_group_top2_bits(gw, uw, b1, b2, s1, s2);
+}
+
+__device__ __forceinline__ void select_group_emit_bits(const uint32_t (&gw)[4], const uint32_t (&uw)[4],
+                                                       int64_t c0, int64_t* __restrict__ idx_out,
+                                                       uint16_t* __restrict__ sz_out) {
+  int b1, b2;
+  uint16_t s1, s2;
+  select_group_top2_bits(gw, uw, b1, b2, s1, s2);
+  idx_out[0] = c0 + b1;
+  idx_out[1] = c0 + b2;
+  sz_out[0] = s1;
+  sz_out[1] = s2;
 }
 
 __device__ __forceinline__ void select_group_emit(const float* g, const float* u, int64_t c0,
@@ -130,25 +184,23 @@ __device__ __forceinline__ void select_group_emit(const float* g, const float* u
 // the four 2-bit positions in the same order (bits 0-7).
 __device__ __forceinline__ uint32_t pack_group_2of8(int p1, uint16_t v1, int p2, uint16_t v2,
                                                     uint16_t (&out)[4]) {
+  // branch-free: (qa, va) the lower position, (qb, vb) the higher
   const bool sw = p2 < p1;
   const int qa = sw ? p2 : p1, qb = sw ? p1 : p2;
   const uint16_t va = sw ? v2 : v1, vb = sw ? v1 : v2;
-  uint32_t pos;
-  if (qb < 4) {  // both in the low half
-    out[0] = va; out[1] = vb; out[2] = 0; out[3] = 0;
-    pos = static_cast<uint32_t>(qa) | (static_cast<uint32_t>(qb) << 2) | (0x4u << 4);
-  } else if (qa >= 4) {  // both in the high half
-    out[0] = 0; out[1] = 0; out[2] = va; out[3] = vb;
-    pos = 0x4u | ((static_cast<uint32_t>(qa - 4) | (static_cast<uint32_t>(qb - 4) << 2)) << 4);
-  } else {  // one in each half
-    uint32_t lo, hi;
-    if (qa == 0) { out[0] = va; out[1] = 0; lo = 0x4u; }
-    else { out[0] = 0; out[1] = va; lo = static_cast<uint32_t>(qa) << 2; }
-    if (qb == 4) { out[2] = vb; out[3] = 0; hi = 0x4u; }
-    else { out[2] = 0; out[3] = vb; hi = static_cast<uint32_t>(qb - 4) << 2; }
-    pos = lo | (hi << 4);
-  }
-  return pos;
+  const bool lo_both = qb < 4, hi_both = qa >= 4, split = !lo_both && !hi_both;
+  // low half: both there -> (qa, qb); none -> zeros at (0, 1); qa alone ->
+  // stored at 0 when qa is 0 (zero at 1), else zero at 0 and qa
+  const uint32_t l0 = lo_both ? static_cast<uint32_t>(qa) : 0u;
+  const uint32_t l1 = lo_both ? static_cast<uint32_t>(qb) : hi_both ? 1u : static_cast<uint32_t>(max(qa, 1));
+  out[0] = (lo_both || (split && qa == 0)) ? va : uint16_t(0);
+  out[1] = lo_both ? vb : (split && qa != 0) ? va : uint16_t(0);
+  // high half, the same with qb alone in the split case
+  const uint32_t h0 = hi_both ? static_cast<uint32_t>(qa - 4) : 0u;
+  const uint32_t h1 = hi_both ? static_cast<uint32_t>(qb - 4) : lo_both ? 1u : static_cast<uint32_t>(max(qb - 4, 1));
+  out[2] = hi_both ? va : (split && qb == 4) ? vb : uint16_t(0);
+  out[3] = (hi_both || (split && qb != 4)) ? vb : uint16_t(0);
+  return l0 | (l1 << 2) | (h0 << 4) | (h1 << 6);
 }
 
 // Positions byte of an 8-group with nothing to pack (zeros at 0, 1 per half).

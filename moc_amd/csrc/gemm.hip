@@ -829,17 +829,9 @@ __device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, cons
         const uint4 gv = *reinterpret_cast<const uint4*>(lds + off);
         const uint4 uv = *reinterpret_cast<const uint4*>(lds + kU + off);
         const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-        float gf[8], uf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          gf[2 * e] = __uint_as_float(gw[e] << 16);
-          gf[2 * e + 1] = __uint_as_float(gw[e] & 0xFFFF0000u);
-          uf[2 * e] = __uint_as_float(uw[e] << 16);
-          uf[2 * e + 1] = __uint_as_float(uw[e] & 0xFFFF0000u);
-        }
         int b1, b2;
         uint16_t s1, s2;
-        select_group_top2(gf, uf, b1, b2, s1, s2);
+        select_group_top2_bits(gw, uw, b1, b2, s1, s2);
         pos = pack_group_2of8(b1, s1, b2, s2, q);
       }
       // 64-channel tile t = G / 8; G % 8 = 4s + 2h + jj
@@ -864,16 +856,8 @@ __device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, cons
     const uint4 gv = *reinterpret_cast<const uint4*>(lds + off);
     const uint4 uv = *reinterpret_cast<const uint4*>(lds + kU + off);
     const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-    float gf[8], uf[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      gf[2 * e] = __uint_as_float(gw[e] << 16);
-      gf[2 * e + 1] = __uint_as_float(gw[e] & 0xFFFF0000u);
-      uf[2 * e] = __uint_as_float(uw[e] << 16);
-      uf[2 * e + 1] = __uint_as_float(uw[e] & 0xFFFF0000u);
-    }
     const int64_t o = static_cast<int64_t>(tok) * kout + (cg / 8) * 2;
-    select_group_emit(gf, uf, cg, g.gu_idx + o, g.gu_sz + o);
+    select_group_emit_bits(gw, uw, cg, g.gu_idx + o, g.gu_sz + o);
   }
 }
 
