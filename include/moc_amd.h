@@ -199,6 +199,44 @@ int moc_gemm_pair(int64_t M, int64_t K, const void* A, int64_t lda, const void* 
  * are library calls). */
 int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int64_t K, int64_t K2);
 
+/* ----------------------------------------------------------------- layer */
+/* GEMM workspace bytes of moc_ffn_forward_bf16 (0: none). */
+int64_t moc_ffn_forward_workspace_size(int64_t rows, int64_t d, int64_t inter);
+
+/* The MoC FFN forward for rows tokens, bf16, as one call
+ * (_MoCFunction.forward, moc/ffn.py:130-173; the 2:8 and post-SiLU variants
+ * :266-308, :322-367; _MoCGCPFunction.forward :378-421): G = x Wg^T and
+ * U = x Wu^T, the selection (0: Top-K of G, 1: Top-K of |SiLU(G)|, 2: top-2
+ * of every 8 channels, k its 2 floor(I/8) + min(2, I mod 8)), u_s = U[idx],
+ * s_s = SiLU(vals), z_s = s_s u_s (s_s, z_s may be NULL), the dense Z
+ * (written into g's buffer), out = Z W_down^T.  g, u [rows, ld_gu] are
+ * scratch; wd is W_down [d, inter] with 16-byte aligned rows.  Same launches
+ * and results as the per-kernel entry points in that order. */
+int moc_ffn_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection, const void* x,
+                         int64_t ldx, const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
+                         const void* wd, int64_t ldwd, void* g, void* u, int64_t ld_gu, void* vals,
+                         void* idx, int idx_dtype, void* u_s, void* s_s, void* z_s, void* out, int64_t ldo,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/* GEMM workspace bytes of moc_ffn_backward_bf16 (0: none). */
+int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu, int stacked);
+
+/* The MoC FFN backward for rows tokens, bf16 operands, as one call
+ * (_MoCFunction.backward, moc/ffn.py:175-259; _MoCGCPFunction.backward
+ * :423-497): with s_s NULL (GCP) S and Z are recomputed from g_s, u_s and Z
+ * scattered dense (s into s_tmp), else Z is scattered from z_s; dWd =
+ * go^T Z, gZ = go W_down (into zbuf after Z), gG and gU dense from gZ, dWg =
+ * gG^T x, dWu = gU^T x (stacked: one GEMM over [gG | gU], gu = gg + ld_ggu/2
+ * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Weight gradients in
+ * grad_dtype (MOC_BF16 or MOC_F32), dX in bf16. */
+int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* go, int64_t ldgo,
+                          const void* x, int64_t ldx, const void* idx, int idx_dtype, const void* g_s,
+                          const void* u_s, const void* s_s, const void* z_s, const void* wg, int64_t ldwg,
+                          const void* wu, int64_t ldwu, const void* wd, int64_t ldwd, void* zbuf, int64_t ldz,
+                          void* gg, void* gu, int64_t ld_ggu, int stacked, void* s_tmp, void* dx, int64_t lddx,
+                          void* dwg, void* dwu, int64_t ld_dw, void* dwd, int64_t lddwd, int grad_dtype,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- decode */
 /* y[b, r] = bf16(sum_h x[b,h] W[r,h]) for b < nb <= 16 tokens: the decode
  * gate projection (module.gate_proj(x) before

@@ -59,6 +59,15 @@ SIGNATURES: dict[str, tuple] = {
     "moc_gemm_ws": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                            _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp]),
     "moc_gemm_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64]),
+    "moc_ffn_forward_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "moc_ffn_forward_bf16": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
+                                    _i64, _vp, _vp, _i64, _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp,
+                                    _i64, _vp]),
+    "moc_ffn_backward_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "moc_ffn_backward_bf16": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _vp,
+                                     _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
+                                     _i64, _int, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp,
+                                     _i64, _vp]),
     "moc_gemm_pair": (_int, [_i64, _i64, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
                              _vp, _i64, _vp, _i64, _vp]),
     "moc_gemv_bf16": (_int, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),

@@ -1,0 +1,150 @@
+// The MoC FFN layer's forward and backward as one C-ABI call each: the
+// launches of the bf16 single-stream path (moc/ffn.py:124-259 for `moc`,
+// :262-369 for the 2:8 and post-SiLU selections, :372-497 for `moc_gcp`)
+// issued from here instead of one host call per kernel.  At the shapes
+// whose GEMMs fill the CUs about once (the 130m and 350m layers) the layer
+// is host-bound otherwise: every Python wrapper and ctypes call costs
+// microseconds that the GPU spends idle.
+//
+// No kernels of its own: the steps are the library's entry points, in the
+// order of the reference's autograd Functions, on the caller's stream.
+#include <algorithm>
+
+#include "abi.h"
+
+namespace {
+
+int64_t gemm_ws(int64_t M, int64_t N, int64_t K, int64_t K2) {
+  const int64_t b = moc_gemm_workspace_size(MOC_BF16, M, N, K, K2);
+  return b > 0 ? b : 0;
+}
+
+int64_t effective_2of8(int64_t inter) { return (inter / 8) * 2 + std::min<int64_t>(2, inter % 8); }
+
+bool ld_ok(const void* p, int64_t ld, int64_t cols) {
+  return p != nullptr && moc::aligned16(p) && ld % 8 == 0 && ld >= cols;
+}
+
+}  // namespace
+
+// GEMM workspace of moc_ffn_forward_bf16: the G,U pair and D = Z W_down^T.
+extern "C" int64_t moc_ffn_forward_workspace_size(int64_t rows, int64_t d, int64_t inter) {
+  if (rows <= 0 || d <= 0 || inter <= 0) return 0;
+  return std::max(gemm_ws(rows, inter, d, 0), gemm_ws(rows, d, inter, 0));
+}
+
+extern "C" int moc_ffn_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection,
+                                    const void* x, int64_t ldx, const void* wg, int64_t ldwg,
+                                    const void* wu, int64_t ldwu, const void* wd, int64_t ldwd, void* g,
+                                    void* u, int64_t ld_gu, void* vals, void* idx, int idx_dtype,
+                                    void* u_s, void* s_s, void* z_s, void* out, int64_t ldo,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(rows >= 1 && d >= 1 && inter >= 1 && k >= 1 && k <= inter, "moc_ffn_forward_bf16: bad shape");
+  MOC_REQUIRE(selection >= 0 && selection <= 2, "moc_ffn_forward_bf16: selection 0 (Top-K), 1 (Top-K of "
+              "|SiLU(G)|) or 2 (top-2 of 8)");
+  MOC_REQUIRE(selection != 2 || k == effective_2of8(inter),
+              "moc_ffn_forward_bf16: the 2:8 selection keeps %lld channels", (long long)effective_2of8(inter));
+  MOC_REQUIRE(ld_ok(x, ldx, d) && ld_ok(wg, ldwg, d) && ld_ok(wu, ldwu, d) && ld_ok(wd, ldwd, inter) &&
+                  ld_ok(g, ld_gu, inter) && ld_ok(u, ld_gu, inter) && ld_ok(out, ldo, d),
+              "moc_ffn_forward_bf16: operands need 16-byte aligned rows (leading dimensions multiples of 8)");
+  MOC_REQUIRE(vals && idx && u_s, "moc_ffn_forward_bf16: null output");
+  const int64_t need = moc_ffn_forward_workspace_size(rows, d, inter);
+  MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "moc_ffn_forward_bf16: workspace of %lld bytes required", (long long)need);
+  // G = x Wg^T and U = x Wu^T (one launch)
+  int rc = moc_gemm_pair(rows, d, x, ldx, wg, ldwg, inter, g, ld_gu, wu, ldwu, inter, u, ld_gu, workspace,
+                         workspace_bytes, stream);
+  if (rc != MOC_OK) return rc;
+  // the selection (indices in ascending channel order) and its gate values
+  if (selection == 2)
+    rc = moc_select_2of8(MOC_BF16, g, rows, inter, ld_gu, vals, idx, idx_dtype, stream);
+  else
+    rc = moc_topk_rows(MOC_BF16, g, rows, inter, ld_gu, k, selection, vals, idx, idx_dtype, nullptr, 0, stream);
+  if (rc != MOC_OK) return rc;
+  // U at the selection, SiLU, Z; the dense zero-filled Z goes into G's
+  // buffer, which nothing reads after the selection
+  rc = moc_sparse_forward_aux(MOC_BF16, vals, idx, idx_dtype, u, ld_gu, rows, k, inter, u_s, s_s, z_s, g,
+                              ld_gu, stream);
+  if (rc != MOC_OK) return rc;
+  // D = Z W_down^T
+  return moc_gemm_ws(MOC_BF16, rows, d, inter, g, ld_gu, 1, wd, 1, ldwd, 0, nullptr, 0, 0, nullptr, 0, 0, out,
+                     ldo, MOC_BF16, workspace, workspace_bytes, stream);
+}
+
+// GEMM workspace of moc_ffn_backward_bf16 (stacked: dWg and dWu as one GEMM
+// over [gG | gU] with rows ld_ggu / 2 apart).
+extern "C" int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu,
+                                                   int stacked) {
+  if (rows <= 0 || d <= 0 || inter <= 0) return 0;
+  int64_t w = std::max(gemm_ws(d, inter, rows, 0), gemm_ws(rows, inter, d, 0));
+  w = std::max(w, stacked ? gemm_ws(ld_ggu, d, rows, 0) : gemm_ws(inter, d, rows, 0));
+  return std::max(w, gemm_ws(rows, d, inter, inter));
+}
+
+extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* go,
+                                     int64_t ldgo, const void* x, int64_t ldx, const void* idx, int idx_dtype,
+                                     const void* g_s, const void* u_s, const void* s_s, const void* z_s,
+                                     const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
+                                     const void* wd, int64_t ldwd, void* zbuf, int64_t ldz, void* gg, void* gu,
+                                     int64_t ld_ggu, int stacked, void* s_tmp, void* dx, int64_t lddx,
+                                     void* dwg, void* dwu, int64_t ld_dw, void* dwd, int64_t lddwd,
+                                     int grad_dtype, void* workspace, int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(rows >= 1 && d >= 1 && inter >= 1 && k >= 1 && k <= inter, "moc_ffn_backward_bf16: bad shape");
+  MOC_REQUIRE(grad_dtype == MOC_BF16 || grad_dtype == MOC_F32, "moc_ffn_backward_bf16: grad dtype bf16 or f32");
+  MOC_REQUIRE(ld_ok(go, ldgo, d) && ld_ok(x, ldx, d) && ld_ok(wg, ldwg, d) && ld_ok(wu, ldwu, d) &&
+                  ld_ok(wd, ldwd, inter) && ld_ok(zbuf, ldz, inter) && ld_ok(gg, ld_ggu, inter) &&
+                  ld_ok(gu, ld_ggu, inter) && ld_ok(dx, lddx, d),
+              "moc_ffn_backward_bf16: operands need 16-byte aligned rows (leading dimensions multiples of 8)");
+  MOC_REQUIRE(idx && g_s && u_s && dwg && dwu && dwd && ld_dw >= d && lddwd >= inter,
+              "moc_ffn_backward_bf16: null operand or bad leading dimension");
+  MOC_REQUIRE(s_s != nullptr || s_tmp != nullptr, "moc_ffn_backward_bf16: GCP needs s_tmp");
+  MOC_REQUIRE(s_s == nullptr || z_s != nullptr, "moc_ffn_backward_bf16: saved S needs saved Z");
+  const int64_t esz = grad_dtype == MOC_BF16 ? 2 : 4;
+  const int64_t pitch = ld_ggu / 2;
+  if (stacked) {
+    MOC_REQUIRE(ld_ggu % 16 == 0 && pitch >= inter &&
+                    static_cast<const char*>(gu) == static_cast<const char*>(gg) + pitch * 2 &&
+                    static_cast<const char*>(dwu) == static_cast<const char*>(dwg) + pitch * ld_dw * esz,
+                "moc_ffn_backward_bf16: stacked gG | gU and dWg | dWu must be one buffer each, pitch apart");
+  }
+  const int64_t need = moc_ffn_backward_workspace_size(rows, d, inter, ld_ggu, stacked);
+  MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "moc_ffn_backward_bf16: workspace of %lld bytes required", (long long)need);
+  int rc;
+  const void* s_use = s_s;
+  if (s_s == nullptr) {
+    // GCP: S = SiLU(G M), Z = S U M recomputed, Z scattered dense (:435-442)
+    rc = moc_gcp_recompute_scatter(MOC_BF16, g_s, u_s, idx, idx_dtype, rows, k, inter, s_tmp, zbuf, ldz, stream);
+    s_use = s_tmp;
+  } else {
+    rc = moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
+  }
+  if (rc != MOC_OK) return rc;
+  // dWd = go^T Z
+  rc = moc_gemm_ws(MOC_BF16, d, inter, rows, go, 1, ldgo, zbuf, ldz, 1, 0, nullptr, 0, 0, nullptr, 0, 0, dwd,
+                   lddwd, grad_dtype, workspace, workspace_bytes, stream);
+  if (rc != MOC_OK) return rc;
+  // gZ = go W_down, into Z's buffer (Z is consumed)
+  rc = moc_gemm_ws(MOC_BF16, rows, inter, d, go, ldgo, 1, wd, ldwd, 1, 0, nullptr, 0, 0, nullptr, 0, 0, zbuf,
+                   ldz, MOC_BF16, workspace, workspace_bytes, stream);
+  if (rc != MOC_OK) return rc;
+  // gG, gU dense (:455-480)
+  rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_use, zbuf, ldz, rows, k, inter, gg, gu,
+                               ld_ggu, stream);
+  if (rc != MOC_OK) return rc;
+  // dWg = gG^T x, dWu = gU^T x (:483-490)
+  if (stacked) {
+    rc = moc_gemm_ws(MOC_BF16, 2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, 0, nullptr, 0, 0, nullptr, 0, 0,
+                     dwg, ld_dw, grad_dtype, workspace, workspace_bytes, stream);
+  } else {
+    rc = moc_gemm_ws(MOC_BF16, inter, d, rows, gg, 1, ld_ggu, x, ldx, 1, 0, nullptr, 0, 0, nullptr, 0, 0, dwg,
+                     ld_dw, grad_dtype, workspace, workspace_bytes, stream);
+    if (rc != MOC_OK) return rc;
+    rc = moc_gemm_ws(MOC_BF16, inter, d, rows, gu, 1, ld_ggu, x, ldx, 1, 0, nullptr, 0, 0, nullptr, 0, 0, dwu,
+                     ld_dw, grad_dtype, workspace, workspace_bytes, stream);
+  }
+  if (rc != MOC_OK) return rc;
+  // dX = gG Wg + gU Wu (:491-497)
+  return moc_gemm_ws(MOC_BF16, rows, d, inter, gg, ld_ggu, 1, wg, ldwg, 1, inter, gu, ld_ggu, 1, wu, ldwu, 1, dx,
+                     lddx, MOC_BF16, workspace, workspace_bytes, stream);
+}

@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _native as N
 from . import kernels as K
 
 _MODES = (
@@ -129,6 +130,65 @@ def _side_for(device, rows: int, inter: int):
     return None
 
 
+_SELECTION_CODE = {"topk": 0, "post_silu_abs": 1, "2of8": 2}
+_LAYER_WS: dict = {}
+# The one-call native layer for single-stream shapes; False runs the same
+# launches one host call per kernel (the tests compare the two).
+USE_NATIVE_LAYER = True
+
+
+def _layer_ok(x2, *weights) -> bool:
+    """True if the one-call native layer (moc_ffn_forward_bf16 /
+    moc_ffn_backward_bf16) takes these operands: bf16, several rows, every
+    row 16-byte aligned without a copy (hidden and intermediate sizes
+    multiples of 8, contiguous weights)."""
+    # the GEMM timing probe brackets every GEMM launch from Python
+    if not USE_NATIVE_LAYER or K._GEMM_PROBE is not None or x2.dtype != torch.bfloat16 or x2.shape[0] < 2 or x2.shape[1] % 8 or x2.stride(1) != 1 \
+            or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        return False
+    for w in weights:
+        if w.dtype != torch.bfloat16 or not w.is_contiguous() or w.data_ptr() % 16 or w.shape[1] % 8:
+            return False
+    return True
+
+
+def _layer_ws_bytes(key, query, *args) -> int:
+    n = _LAYER_WS.get(key)
+    if n is None:
+        n = _LAYER_WS[key] = N.query(query, *args)
+    return n
+
+
+def _layer_forward(x, x2, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool):
+    """_forward_common's launches as one native call (same results)."""
+    rows, d = x2.shape
+    inter = gate_w.shape[0]
+    dev = x2.device
+    bf16 = torch.bfloat16
+    pitch = K.row_pitch(inter, bf16)
+    kk = _moc_2_8_effective_k(inter) if selection == "2of8" else k
+    g = torch.empty((rows, pitch), dtype=bf16, device=dev)
+    u = torch.empty((rows, pitch), dtype=bf16, device=dev)
+    vals = torch.empty((rows, kk), dtype=bf16, device=dev)
+    idx = torch.empty((rows, kk), dtype=idx_dtype, device=dev)
+    u_s = torch.empty((rows, kk), dtype=bf16, device=dev)
+    s_s = torch.empty((rows, kk), dtype=bf16, device=dev) if save_s else None
+    z_s = torch.empty((rows, kk), dtype=bf16, device=dev) if save_s else None
+    d_out = down_w.shape[0]
+    out = torch.empty((rows, d_out), dtype=bf16, device=dev)
+    nbytes = _layer_ws_bytes(("f", dev.index, rows, d, inter), "moc_ffn_forward_workspace_size",
+                             rows, d, inter)
+    ws = K._gemm_workspace(dev, nbytes) if nbytes > 0 else None
+    N.call("moc_ffn_forward_bf16", rows, d, inter, kk, _SELECTION_CODE[selection], x2.data_ptr(),
+             x2.stride(0), gate_w.data_ptr(), d, up_w.data_ptr(), d, down_w.data_ptr(), inter,
+             g.data_ptr(), u.data_ptr(), pitch, vals.data_ptr(), idx.data_ptr(), N.idx_code(idx_dtype),
+             u_s.data_ptr(), N.ptr(s_s), N.ptr(z_s), out.data_ptr(), d_out, N.ptr(ws), nbytes,
+             N.stream_of(x2))
+    shp = (*x.shape[:-1], kk)
+    return (out.reshape(*x.shape[:-1], d_out), idx.reshape(shp), vals.reshape(shp), u_s.reshape(shp),
+            None if s_s is None else s_s.reshape(shp), None if z_s is None else z_s.reshape(shp))
+
+
 def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool,
                     want_mask: bool = False):
     """Shared MoC forward: G -> select -> U -> sparse aux -> D.
@@ -145,6 +205,9 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     # which the backward reuses, then runs on the side stream beside the
     # selection.  f32: U on the side stream beside G and the selection.
     side = _side_for(x.device, rows, inter)
+    if side is None and not want_mask and down_w.shape[0] == d and _layer_ok(x2, gate_w, up_w, down_w):
+        # one native call for the whole single-stream forward (host-bound shapes)
+        return _layer_forward(x, x2, gate_w, up_w, down_w, k, selection, idx_dtype, save_s)
     g = K.padded_empty(rows, inter, x.dtype, x.device)
     u = K.padded_empty(rows, inter, x.dtype, x.device)
     wd = (K.padded_empty(down_w.shape[0], down_w.shape[1], down_w.dtype, x.device)
@@ -225,6 +288,11 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     x2 = K.aligned_rows(x.reshape(-1, d))
     side = _side_for(dev, x2.shape[0], inter)
     go = K.aligned_rows(grad_out.reshape(-1, grad_out.shape[-1]).to(x.dtype))
+    if side is None and _layer_ok(x2, gate_w, up_w, down_w) and _layer_ok(go) \
+            and (not gcp or K.row_pitch(inter, x.dtype) <= 8192):
+        # one native call for the whole single-stream backward
+        return _layer_backward(x, x2, go, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp,
+                               grad_dtype or down_w.dtype)
     if gcp and x.dtype == torch.bfloat16 and K.row_pitch(inter, torch.bfloat16) <= 8192:
         s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter)
     else:
@@ -256,6 +324,47 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
     if side is not None:
         main.wait_stream(side)
     return grad_x.reshape(x.shape).to(x.dtype), grad_gate_w, grad_up_w, grad_down_w
+
+
+def _layer_backward(x, x2, go, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp: bool, grad_dtype):
+    """_backward_common's launches as one native call (same results)."""
+    rows, d = x2.shape
+    inter = gate_w.shape[0]
+    dev = x2.device
+    bf16 = torch.bfloat16
+    pitch = K.row_pitch(inter, bf16)
+    idx2 = idx.reshape(rows, -1)
+    kk = idx2.shape[1]
+    g2, u2 = g_s.reshape(rows, kk), u_s.reshape(rows, kk)
+    s2 = None if gcp else s_s.reshape(rows, kk)
+    z2 = None if gcp else z_s.reshape(rows, kk)
+    for t in (idx2, g2, u2, s2, z2):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("saved selection tensors must be contiguous")
+    stacked = _stack_weight_grads(dev, inter, d, pitch, bf16)
+    zbuf = torch.empty((rows, pitch), dtype=bf16, device=dev)
+    ggu = torch.empty((rows, 2 * pitch), dtype=bf16, device=dev)
+    s_tmp = torch.empty((rows, kk), dtype=bf16, device=dev) if gcp else None
+    dx = torch.empty((rows, d), dtype=bf16, device=dev)
+    if stacked:
+        dw = torch.empty((2 * pitch, d), dtype=grad_dtype, device=dev)
+        dwg, dwu = dw[:inter], dw[pitch:pitch + inter]
+    else:
+        dwg = torch.empty((inter, d), dtype=grad_dtype, device=dev)
+        dwu = torch.empty((inter, d), dtype=grad_dtype, device=dev)
+    d_out = go.shape[1]
+    dwd = torch.empty((d_out, inter), dtype=grad_dtype, device=dev)
+    nbytes = _layer_ws_bytes(("b", dev.index, rows, d, inter, stacked), "moc_ffn_backward_workspace_size",
+                             rows, d, inter, 2 * pitch, int(stacked))
+    ws = K._gemm_workspace(dev, nbytes) if nbytes > 0 else None
+    gg = ggu.data_ptr()
+    N.call("moc_ffn_backward_bf16", rows, d, inter, kk, go.data_ptr(), go.stride(0), x2.data_ptr(),
+             x2.stride(0), idx2.data_ptr(), N.idx_code(idx2.dtype), g2.data_ptr(), u2.data_ptr(),
+             N.ptr(s2), N.ptr(z2), gate_w.data_ptr(), d, up_w.data_ptr(), d, down_w.data_ptr(), inter,
+             zbuf.data_ptr(), pitch, gg, gg + 2 * pitch, 2 * pitch, int(stacked), N.ptr(s_tmp),
+             dx.data_ptr(), d, dwg.data_ptr(), dwu.data_ptr(), d, dwd.data_ptr(), inter,
+             N.dtype_code(grad_dtype), N.ptr(ws), nbytes, N.stream_of(x2))
+    return dx.reshape(x.shape).to(x.dtype), dwg, dwu, dwd
 
 
 def _stack_weight_grads(dev, inter: int, d: int, pitch: int, dtype) -> bool:

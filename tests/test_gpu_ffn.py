@@ -344,6 +344,62 @@ def test_inference_moc28_modes(nb):
         close(yr2, y_other, 0, 0, "2:8 graph replay, second input")
 
 
+@pytest.mark.parametrize("mode", ["moc", "moc_gcp", "moc_2_8", "moc_post_silu_abs"])
+@pytest.mark.parametrize("shape", [(512, 256, 1024, 192), (256, 4096, 4096, 512)])
+def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
+    """The one-call layer entries (moc_ffn_forward_bf16 / _backward_bf16)
+    issue the same launches as the per-kernel path: outputs and every
+    gradient equal bit for bit.  (512, 256, 1024) stacks dWg | dWu into one
+    GEMM; (256, 4096, 4096) computes them separately; both fill the CUs at
+    most once, the shapes the layer entries serve."""
+    from moc_amd import _native, ffn
+    rows, d, inter, k = shape
+    x, wg, wu, wd, go = make_inputs(rows, d, inter, torch.bfloat16, seed=rows + d)
+    calls = []
+    real_call = _native.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_native, "call", spy)
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", True)
+    a = run_module(mode, x, wg, wu, wd, go, k)
+    assert "moc_ffn_forward_bf16" in calls and "moc_ffn_backward_bf16" in calls
+    calls.clear()
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", False)
+    b = run_module(mode, x, wg, wu, wd, go, k)
+    assert "moc_ffn_forward_bf16" not in calls and "moc_ffn_backward_bf16" not in calls
+    for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, b):
+        assert p.dtype == q.dtype and p.shape == q.shape, name
+        assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
+
+
+def test_native_layer_f32_master_grads(monkeypatch):
+    """Under autocast with f32 parameters the layer entry's weight
+    gradients come out in f32, equal to the per-kernel path's."""
+    from moc_amd import ffn
+    from moc_amd.ffn import MoCSwiGLUFFN
+    rows, d, inter, k = 512, 256, 1024, 192
+    x, wg, wu, wd, go = make_inputs(rows, d, inter, torch.float32, seed=7)
+    res = []
+    for native in (True, False):
+        monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", native)
+        m = MoCSwiGLUFFN(d, inter, k, mode="moc_gcp", index_save_dtype=torch.int16).to(DEV)
+        with torch.no_grad():
+            m.gate_proj.weight.copy_(wg)
+            m.up_proj.weight.copy_(wu)
+            m.down_proj.weight.copy_(wd)
+        xd = x.to(DEV).requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = m(xd)
+        out.float().backward(go.to(DEV))
+        res.append((out, xd.grad, m.gate_proj.weight.grad, m.up_proj.weight.grad, m.down_proj.weight.grad))
+    for p, q in zip(*res):
+        assert p.dtype == q.dtype and torch.equal(p, q)
+    assert res[0][2].dtype == torch.float32
+
+
 def test_ffn_bf16_350m_shape_config5():
     """Config 5's FFN layer: the 350m preset shape (d 1024, I 2736, K 512) at
     16 x 256 tokens, moc_gcp fwd+bwd against the oracle."""
