@@ -350,8 +350,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
-template <bool OUT_F32, int NJ>
-__device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const f32x16_t (&acc)[4][NJ],
+template <bool OUT_F32, int NJ, int MI = 4>
+__device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const f32x16_t (&acc)[MI][NJ],
                                              int row0, int col0, int wm, int wn, int wave, int lane) {
   constexpr int kEsz = OUT_F32 ? 4 : 2;
   constexpr int kCols = 32 * NJ;  // columns of the wave's tile
@@ -361,7 +361,7 @@ __device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const
   char* reg = lds + wave * (32 * kPitch);
   const bool vec = g.vec_store != 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < MI; ++i) {
     char* rowp = reg + (lane & 31) * kPitch;
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
@@ -615,20 +615,21 @@ void gemm_bf16_kernel(GemmArgs g) {
 // end of its compute phase, a whole K tile after issuing them.
 // ---------------------------------------------------------------------------
 constexpr int kPpThreads = 512;
+constexpr int kShortMaxKTiles = 40;  // longest K (in 64-deep tiles) run on 128-row tiles
 constexpr int kG0Loads = 4;   // of the 8 loads per operand and wave, those group 0 issues
 
 // One 16-byte load into the LDS sink for line `idx` of slice `slice` (of n)
 // of the K tile at k0: a KC tile is 256 rows of 128 bytes, an MN tile 64
 // k-rows of four 128-byte lines.  Lines past the operand or the slice read
 // as zero.
-template <bool KC>
+template <bool KC, int ROWS = 256>
 __device__ __forceinline__ void prefetch_slice(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
                                                int row0, uint32_t sink, int idx, int slice, int n) {
   uint32_t off;
-  if (idx >= 256 / n) {
+  if (idx >= (KC ? ROWS : 256) / n) {
     off = kOob;
   } else if (KC) {
-    const int r = row0 + slice * (256 / n) + idx;
+    const int r = row0 + slice * (ROWS / n) + idx;
     off = (r < o.ext && k0 < o.K) ? static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + k0) * 2)
                                   : kOob;
   } else {
@@ -733,7 +734,8 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Returns true in the second workgroup of the tile; acc then holds the sum
 // of both parts.  flag: one LDS word.
-__device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4][2], int slot, int part,
+template <int MI = 4>
+__device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[MI][2], int slot, int part,
                                            int tid, int* flag) {
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       g.fix_part + static_cast<int64_t>(slot) * 2 * kPartBytes, (short)0, 2 * kPartBytes, kBufferFlags);
@@ -747,7 +749,7 @@ __device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4]
   if (*flag == 0) {
     // first so far: publish the partial, then arrive
 #pragma unroll
-    for (int b = 0; b < 8; ++b)
+    for (int b = 0; b < 2 * MI; ++b)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const f32x16_t& a = acc[b >> 1][b & 1];
@@ -766,7 +768,7 @@ __device__ __forceinline__ bool fix_arrive(const GemmArgs& g, f32x16_t (&acc)[4]
   // second: the other part's partial plus ours
   const uint32_t other = static_cast<uint32_t>((1 - part) * kPartBytes);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
+  for (int b = 0; b < 2 * MI; ++b) {
     f32x16_t& a = acc[b >> 1][b & 1];
     u32x4_t w[4];
 #pragma unroll
@@ -870,9 +872,13 @@ __device__ __forceinline__ void gu28_epilogue(const GemmArgs& g, char* lds, cons
 // positions, both in the A stage; B and everything else are unchanged.  The
 // sparse operand is the MFMA's first, so the accumulators come out in the
 // MFMA's orientation and leave through store_tile_t.
-template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT, bool GU = false, bool SP = false>
+template <bool A_KC, bool B_KC, bool OUT_F32, bool DUAL, bool SPLIT, bool GU = false, bool SP = false,
+          bool SHORT = false>
 __global__ __launch_bounds__(kPpThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_pp_kernel(GemmArgs g) {
+  static_assert(!SHORT || (A_KC && !GU && !SP), "128-row tiles: K-contiguous A, plain products");
+  // SHORT: 128 x 256 C tiles (the A tile half as tall; wave tiles 64 x 64)
+  constexpr int MI = SHORT ? 2 : 4;  // 32-row blocks of a wave's tile
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
 
   const int tid = threadIdx.x;
@@ -904,9 +910,9 @@ void gemm_pp_kernel(GemmArgs g) {
     g.ldc = g.ldc2;
     g.vec_store = g.vec_store2;
   }
-  const int row0 = tm * kBM;
+  const int row0 = tm * (SHORT ? 128 : kBM);
   const int col0 = GU ? tn * 128 : tn * kBN;  // GU: channel base of the gate and up halves
-  const int wm = (sw >> 1) * 128;
+  const int wm = (sw >> 1) * (SHORT ? 64 : 128);
   const int wn = (sw & 1) * 128 + grp * 64;
   const uint32_t lds0 = lds_addr(lds);
 
@@ -921,15 +927,15 @@ void gemm_pp_kernel(GemmArgs g) {
   fa_map.init(0, wm, lane);
   fb_map.init(kBOffset, wn, lane);
 
-  f32x16_t acc[4][2];
+  f32x16_t acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  bf16x8_t fa[4][4], fb[4][2];  // [k16 step][block]  (SP: fa[32-channel step][block])
+  bf16x8_t fa[4][MI], fb[4][2];  // [k16 step][block]  (SP: fa[32-channel step][block])
   uint32_t fm[4];               // SP: positions of the stored A values, per block
   // SP: the lane's A fragment of block 0, step 0 (row wm + (lane & 31),
   // logical chunk lane >> 5); step s is chunk 2s + (lane >> 5), one XOR away
@@ -955,7 +961,7 @@ void gemm_pp_kernel(GemmArgs g) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
+        for (int i = 0; i < MI; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
 #pragma unroll
         for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
       }
@@ -989,7 +995,7 @@ void gemm_pp_kernel(GemmArgs g) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
@@ -1075,13 +1081,17 @@ void gemm_pp_kernel(GemmArgs g) {
     const uint32_t ba = la.tile_base(oa, k0);
     const uint32_t bb = GU && j0 >= kHalf ? 0u : lb.tile_base(ob, k0);
     const uint32_t bu = GU && j1 > kHalf ? mb1.tile_base(g.b[1], k0) : 0u;
+    // SHORT: the 128-row A tile is loads [0, kHalf); a group issues the
+    // half of them that matches its half of B's
+    const int ja0 = SHORT ? j0 / 2 : j0, ja1 = SHORT ? j1 / 2 : j1;
 #pragma unroll
-    for (int j = 0; j < kLoads; ++j)
+    for (int j = 0; j < kLoads; ++j) {
+      if (j >= ja0 && j < ja1) la.issue(p1 ? ra1 : ra0, oa, ba, at, sw, j);
       if (j >= j0 && j < j1) {
-        la.issue(p1 ? ra1 : ra0, oa, ba, at, sw, j);
         if (GU && j >= kHalf) mb1.issue(rb1, g.b[1], bu, bt, sw, j);
         else lb.issue(p1 ? rb1 : rb0, ob, bb, bt, sw, j);
       }
+    }
   };
   // After loads [j0, j1) of tile t have landed: zero KC elements beyond a K
   // that is not a multiple of 8 (only the last tile of a product can need it).
@@ -1098,7 +1108,7 @@ void gemm_pp_kernel(GemmArgs g) {
     }
     if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
     // kchunk depends on the lane only, so the product-0 maps serve both
-    if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, j0, j1);
+    if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, SHORT ? j0 / 2 : j0, SHORT ? j1 / 2 : j1);
     if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane, j0, j1);
   };
 
@@ -1139,7 +1149,8 @@ void gemm_pp_kernel(GemmArgs g) {
       if (sw == 0) {
         const Operand& o = p1 ? g.a[1] : g.a[0];
         // SP: the packed tile's 64-byte row segments (k0 in stored values)
-        prefetch_slice<A_KC>(p1 ? ra1 : ra0, o, SP ? t * 32 : k0, row0, sink, lane, tn_all & 7, 8);
+        prefetch_slice<A_KC, SHORT ? 128 : 256>(p1 ? ra1 : ra0, o, SP ? t * 32 : k0, row0, sink, lane,
+                                                tn_all & 7, 8);
       } else if (sw == 1) {
         const Operand& o = p1 ? g.b[1] : g.b[0];
         if (GU && (tm & 3) >= 2)  // quarters 2-3 of the B tile are W_up rows
@@ -1171,18 +1182,18 @@ void gemm_pp_kernel(GemmArgs g) {
     compute();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  if (GU) {
+  if constexpr (GU) {
     gu28_epilogue(g, lds, acc, row0, col0, wm, wn, tid, lane);
-  } else if (SPLIT) {
+  } else if constexpr (SPLIT) {
     GemmArgs gs = g;
     gs.C = static_cast<float*>(g.C) + split * g.ws_stride;
-    if (SP) store_tile_t<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
-    else store_tile_w<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
+    if constexpr (SP) store_tile_t<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
+    else store_tile_w<OUT_F32, 2, MI>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
   } else {
-    if (part >= 0 && !fix_arrive(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kSinkOffset)))
+    if (part >= 0 && !fix_arrive<MI>(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kSinkOffset)))
       return;
-    if (SP) store_tile_t<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
-    else store_tile_w<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+    if constexpr (SP) store_tile_t<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
+    else store_tile_w<OUT_F32, 2, MI>(g, lds, acc, row0, col0, wm, wn, wave, lane);
   }
 }
 
@@ -1420,11 +1431,24 @@ struct F32Split {
 };
 
 template <bool A_KC, bool B_KC>
-void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st) {
+void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st, bool short_m = false) {
   const int64_t units = a.fix_tail > 0 ? a.fix_full + 2 * static_cast<int64_t>(a.fix_tail)
                                        : static_cast<int64_t>(a.tiles_m) * a.tiles_n * a.ksplit;
   const dim3 grid(static_cast<unsigned>(units)), block(kThreads);
   const bool dual = a.nk[1] > 0;
+  if constexpr (A_KC) {
+    if (a.pp && short_m) {  // 128 x 256 tiles, whole (no split, no fix-up)
+      const dim3 pblock(kPpThreads);
+      if (out_f32) {
+        if (dual) gemm_pp_kernel<A_KC, B_KC, true, true, false, false, false, true><<<grid, pblock, 0, st>>>(a);
+        else gemm_pp_kernel<A_KC, B_KC, true, false, false, false, false, true><<<grid, pblock, 0, st>>>(a);
+      } else {
+        if (dual) gemm_pp_kernel<A_KC, B_KC, false, true, false, false, false, true><<<grid, pblock, 0, st>>>(a);
+        else gemm_pp_kernel<A_KC, B_KC, false, false, false, false, false, true><<<grid, pblock, 0, st>>>(a);
+      }
+      return;
+    }
+  }
   if (a.pp) {
     const dim3 pblock(kPpThreads);
     if (a.ksplit > 1) {  // partial tiles are f32
@@ -1916,10 +1940,23 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
   };
   a.pp = no_wrap(a.a[0]) && no_wrap(a.b[0]) && no_wrap(a.a[1]) && no_wrap(a.b[1]);
+  // 128-row tiles when 256 x 256 tiles would fill more than a quarter but at
+  // most half of the CUs and K is short (the 130m layer's D: 96 tiles, 32 K
+  // tiles): twice the tiles run whole, where 256 x 256 tiles need a two-part
+  // K split whose f32 partial tile (256 KB) passes through one CU per tile
+  // (45 -> 40 us).  A 128-row tile runs its K tiles at ~0.7 of the 256-row
+  // tile's rate per FLOP (half the MFMA work per phase, more than half the
+  // fragment reads), so for long K the split wins (the 130m dX, 64 K tiles:
+  // 72 us split against 78 us).
+  const int64_t cus = cu_count();
+  const int64_t tiles256 = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
+  const bool short_m = a.pp && la == 1 && 4 * tiles256 > cus && 2 * tiles256 <= cus &&
+                       a.nk[0] + a.nk[1] <= kShortMaxKTiles;
+  if (short_m) a.tiles_m = static_cast<int>((M + 127) / 128);
   a.ksplit = 1;
   a.kper = a.nk[0] + a.nk[1];
   a.ws_stride = 0;
-  const SplitPlan sp = plan_split(M, N, a.nk[0] + a.nk[1]);
+  const SplitPlan sp = short_m ? SplitPlan() : plan_split(M, N, a.nk[0] + a.nk[1]);
   const bool split = a.pp && sp.ksplit > 1 && workspace != nullptr && workspace_bytes >= sp.bytes &&
                      reinterpret_cast<uintptr_t>(workspace) % 16 == 0;
   GemmArgs run = a;
@@ -1932,7 +1969,7 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     run.ldc = sp.ldw;
     run.vec_store = 1;
   }
-  const FixPlan fp = split ? FixPlan() : plan_fix(M, N, a.nk[0] + a.nk[1]);
+  const FixPlan fp = (split || short_m) ? FixPlan() : plan_fix(M, N, a.nk[0] + a.nk[1]);
   const bool fix = a.pp && fp.tail > 0 && workspace != nullptr && workspace_bytes >= fp.bytes &&
                    reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
   if (fix) {
@@ -1943,8 +1980,8 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     run.fix_part = static_cast<char*>(workspace) + kFixCounterBytes;
   }
   const bool of_run = split ? true : of;
-  if (la && lb) launch_bf16<true, true>(run, of_run, st);
-  else if (la && !lb) launch_bf16<true, false>(run, of_run, st);
+  if (la && lb) launch_bf16<true, true>(run, of_run, st, short_m);
+  else if (la && !lb) launch_bf16<true, false>(run, of_run, st, short_m);
   else if (!la && lb) launch_bf16<false, true>(run, of_run, st);
   else launch_bf16<false, false>(run, of_run, st);
   if (!split) return check_launch("gemm_bf16_kernel");

@@ -260,6 +260,51 @@ def test_gemm_tail_fixup_dual():
     close(out, _unsplit(gg, wg, T, d, I, gu, wu, I), rtol=1e-5, atol=1e-3)
 
 
+@pytest.mark.parametrize("layout,mnk", [
+    ("kckc", (8192, 768, 2048)),   # 130m D = Z W_down^T: 96 tiles of 256x256 -> 192 of 128x256
+    ("kcmn", (8192, 768, 2048)),
+    ("kckc", (8100, 700, 1000)),   # ragged M (not a multiple of 128) and N
+    ("kckc", (8192, 768, 1001)),   # K % 8 != 0: the straddling chunk of A and B zeroed
+])
+def test_gemm_short_tiles(layout, mnk):
+    """Products whose 256x256 tiles would fill more than a quarter but at
+    most half of the CUs run 128x256 tiles whole: results match the fp32
+    reference, repeat bit for bit, and the workspace-free entry gives the
+    same bits (no split either way)."""
+    M, Nn, Kk = mnk
+    tiles = ((M + 255) // 256) * ((Nn + 255) // 256)
+    cus = K().cu_count(torch.cuda.current_device())
+    assert 4 * tiles > cus and 2 * tiles <= cus
+    g = torch.Generator(device=DEV).manual_seed(16)
+    a = torch.randn(M, Kk, device=DEV, generator=g).to(torch.bfloat16)
+    b = (torch.randn(Kk, Nn, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    ad = K().aligned_rows(a)
+    bd = K().aligned_rows(b.t().contiguous()).t() if layout == "kckc" else K().aligned_rows(b)
+    first = K().gemm(ad, bd, out_dtype=torch.float32)
+    ref = a.float() @ b.float()
+    close(first, ref, rtol=1e-4, atol=2e-3)
+    assert torch.equal(first, K().gemm(ad, bd, out_dtype=torch.float32))
+    assert torch.equal(first, _unsplit(ad, bd, M, Nn, Kk))
+    bf16_close(K().gemm(ad, bd), ref, ulps=1, atol=2e-3)
+
+
+def test_gemm_short_tiles_dual():
+    """A dX-shaped dual product with short K (M 8192, N 768, K 1024 + 1024)
+    on 128x256 tiles against the fp32 reference."""
+    g = torch.Generator(device=DEV).manual_seed(17)
+    T, I, d = 8192, 1024, 768
+    gg = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    gu = torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    out = K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32)
+    ref = gg.float() @ wg.float() + gu.float() @ wu.float()
+    close(out, ref, rtol=1e-4, atol=1e-3)
+    assert torch.equal(out, K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32))
+    assert torch.equal(out, _unsplit(gg, wg, T, d, I, gu, wu, I))
+    bf16_close(K().gemm(gg, wg, a2=gu, b2=wu), ref, ulps=1, atol=1e-3)
+
+
 def test_gemm_workspace_shared_by_split_and_fixup():
     """Split-K and fix-up launches take turns on the stream's one workspace:
     the split-K partials leave the fix-up's arrival counters untouched."""
