@@ -177,6 +177,127 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Gate GEMV for 5..16 tokens, pipelined: one workgroup per CU walks a run of
+// 16-row blocks (of W, then of W2 in the pair form).  A block's rows (64 KB
+// at hidden 2048; chunk c of row r in slot c ^ (r & 15), as above) stream
+// into one of two LDS buffers by direct-to-LDS loads while the previous block
+// is multiplied (MFMA 16x16x32, the four waves splitting k as the streaming
+// kernel does, so both give the same bits).  Every wave issues exactly
+// kGpLoads loads per block (the ones past the block's bytes land in a sink),
+// so the wait for a block is one constant vmcnt.
+constexpr int kGpRows = 16;
+constexpr int kGpMaxHidden = 2048;
+constexpr int kGpBufBytes = kGpRows * 2 * kGpMaxHidden;          // 64 KB
+constexpr int kGpLoads = kGpBufBytes / 1024 / 4;                 // per wave and block: 16
+constexpr int kGpMaxSteps = kGpMaxHidden / 32 / 4;               // k steps per wave
+
+__global__ __launch_bounds__(256) void gemv_pipe_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int nb, const uint16_t* __restrict__ W, int64_t ldw,
+    int rows, int hidden, uint16_t* __restrict__ y, int64_t ldy, int wbytes, int nblk1, int nblk,
+    const uint16_t* __restrict__ W2, int64_t ldw2, int rows2, uint16_t* __restrict__ y2, int64_t ldy2,
+    int wbytes2) {
+  __shared__ __attribute__((aligned(1024))) char lw[2 * kGpBufBytes + 1024];  // two buffers, a sink
+  __shared__ f32x4_t red[4][64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b_lo = static_cast<int>(static_cast<int64_t>(blockIdx.x) * nblk / gridDim.x);
+  const int b_hi = static_cast<int>(static_cast<int64_t>(blockIdx.x + 1) * nblk / gridDim.x);
+  const int cpr = hidden / 8;  // 16-byte chunks per row
+  const __amdgpu_buffer_rsrc_t rs1 =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W), (short)0, wbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs2 =
+      W2 != nullptr ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(W2), (short)0, wbytes2, 0x00020000)
+                    : rs1;
+  const uint32_t lbase = lds_addr(lw);
+  // the loads of block bi into buffer buf
+  // linear chunk q = 64 i + lane of a block -> (row rr, slot sl); i advances
+  // by 4 per load, so (rr, sl) advance by 256 chunks incrementally
+  const int q0 = wave * 64 + lane;
+  const int rr0 = q0 / cpr, sl0 = q0 - rr0 * cpr;
+  auto issue = [&](int bi, int buf) {
+    const bool second = bi >= nblk1;
+    const int r0 = (second ? bi - nblk1 : bi) * kGpRows;
+    const int nr = min(kGpRows, (second ? rows2 : rows) - r0);
+    const uint32_t rowb = static_cast<uint32_t>((second ? ldw2 : ldw) * 2);
+    const int nq = (nr * cpr + 63) / 64;  // wave instructions that carry rows
+    const __amdgpu_buffer_rsrc_t rs = second ? rs2 : rs1;
+    int rr = rr0, sl = sl0;
+    uint32_t rowoff = static_cast<uint32_t>(r0 + rr0) * rowb;
+    for (int u = 0; u < kGpLoads; ++u) {
+      const int i = wave + 4 * u;
+      const bool real = i < nq;
+      const uint32_t off = (real && rr < nr) ? rowoff + static_cast<uint32_t>(((sl ^ (rr & 15)) * 16)) : kOob;
+      const uint32_t m0 = real ? lbase + buf * kGpBufBytes + i * 1024 : lbase + 2 * kGpBufBytes;
+      dma16(rs, __builtin_amdgcn_readfirstlane(m0), off);
+      sl += 256;
+      while (sl >= cpr) {
+        sl -= cpr;
+        ++rr;
+        rowoff += rowb;
+      }
+    }
+  };
+  // the wave's x fragments, kept for every block
+  const int tok = lane & 15, kq = lane >> 4;
+  const bool tok_ok = tok < nb;
+  const uint16_t* xr = x + static_cast<int64_t>(tok_ok ? tok : 0) * ldx;
+  const int steps = hidden / 32;
+  const int s_lo = wave * steps / 4, s_hi = (wave + 1) * steps / 4;
+  uint4 xf[kGpMaxSteps];
+#pragma unroll
+  for (int u = 0; u < kGpMaxSteps; ++u) {
+    const int c = (s_lo + u) * 4 + kq;
+    xf[u] = (tok_ok && s_lo + u < s_hi) ? *reinterpret_cast<const uint4*>(xr + c * 8) : make_uint4(0, 0, 0, 0);
+  }
+  if (b_lo < b_hi) issue(b_lo, 0);
+  const int r0l = lane & 15;
+  for (int bi = b_lo; bi < b_hi; ++bi) {
+    const int buf = (bi - b_lo) & 1;
+    if (bi + 1 < b_hi) {
+      issue(bi + 1, buf ^ 1);
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // kGpLoads: block bi has landed
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __syncthreads();
+    const char* lb = lw + buf * kGpBufBytes;
+    uint4 wf[kGpMaxSteps];
+#pragma unroll
+    for (int u = 0; u < kGpMaxSteps; ++u) {
+      const int c = (s_lo + u) * 4 + kq;
+      wf[u] = s_lo + u < s_hi ? *reinterpret_cast<const uint4*>(lb + r0l * (2 * hidden) + ((c ^ r0l) * 16))
+                              : make_uint4(0, 0, 0, 0);
+    }
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kGpMaxSteps; ++u)
+      if (s_lo + u < s_hi)  // wave-uniform
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wf[u]),
+                                                      __builtin_bit_cast(bf16x8_t, xf[u]), acc, 0, 0, 0);
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && tok_ok) {
+      f32x4_t t = red[0][lane];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const f32x4_t o = red[w][lane];
+        t[0] += o[0]; t[1] += o[1]; t[2] += o[2]; t[3] += o[3];
+      }
+      const bool second = bi >= nblk1;
+      const int r0 = (second ? bi - nblk1 : bi) * kGpRows;
+      const int nrows = second ? rows2 : rows;
+      uint16_t* yy = second ? y2 : y;
+      const int64_t ly = second ? ldy2 : ldy;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = r0 + 4 * kq + j;
+        if (row < nrows) yy[static_cast<int64_t>(tok) * ly + row] = f32_to_bf16(t[j]);
+      }
+    }
+  }
+}
+
 // Fallback gate GEMV for shapes the streaming kernel does not take
 // (hidden not a multiple of 128 or larger than the LDS row budget).
 constexpr int kGemvUnroll = 8;
@@ -775,6 +896,21 @@ int gemv_launch(const void* x, int64_t ldx, int64_t nb, const void* W, int64_t l
     return check_launch("gemv_rows_kernel");
   }
   const int64_t wbytes = rows * ldw * 2, wbytes2 = W2 != nullptr ? rows2 * ldw2 * 2 : 0;
+  // the pair (gate and dense U, ~2.7 blocks of 16 rows per CU) on the
+  // pipelined kernel: 35.3 -> 30.9 us per 16-token layer, 31.6 -> 27.9 at 8;
+  // one projection (~1.3 blocks per CU, nothing to overlap) stays on the
+  // streaming kernel (8.9 against 9.6 us at 16 tokens); both give the same bits
+  if (W2 != nullptr && hidden % 128 == 0 && hidden <= kGpMaxHidden && wbytes < (1LL << 31) - 1024 &&
+      wbytes2 < (1LL << 31) - 1024) {
+    const int64_t nblk1 = (rows + kGpRows - 1) / kGpRows;
+    const int64_t nblk = nblk1 + (W2 != nullptr ? (rows2 + kGpRows - 1) / kGpRows : 0);
+    const int64_t grid = std::min<int64_t>(nblk, cu_count());
+    gemv_pipe_kernel<<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+        (const uint16_t*)x, ldx, (int)nb, (const uint16_t*)W, ldw, (int)rows, (int)hidden, (uint16_t*)y, ldy,
+        (int)wbytes, (int)nblk1, (int)nblk, (const uint16_t*)W2, ldw2, (int)rows2, (uint16_t*)y2, ldy2,
+        (int)wbytes2);
+    return check_launch("gemv_pipe_kernel");
+  }
   const int64_t max_rows = kGvLdsBytes / (2 * hidden);
   if (hidden % 128 == 0 && hidden <= kGvMaxHidden && max_rows >= 16 && wbytes < (1LL << 31) - 1024 &&
       wbytes2 < (1LL << 31) - 1024) {

@@ -1493,19 +1493,6 @@ bool make_operand(const void* p, int64_t ld, bool kc, int64_t ext, int64_t K, Op
   return true;
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
 
 F32Split plan_f32(int64_t M, int64_t N, int64_t K, int64_t K2) {
   F32Split p{1, 0, 0, 0};

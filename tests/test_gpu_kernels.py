@@ -518,7 +518,7 @@ def test_global_decode_path_1b(nb):
 
 @pytest.mark.parametrize("nb,inter,d", [(1, 5461, 2048), (3, 5461, 2048), (4, 5461, 2048),
                                          (5, 5461, 2048), (16, 5461, 2048), (4, 1000, 256),
-                                         (8, 777, 4096)])
+                                         (8, 777, 4096), (7, 50, 1024), (12, 3001, 384)])
 def test_global_decode_layer_entry(nb, inter, d):
     """moc_global_decode_bf16 (gate GEMV, from 4 tokens on with the dense U
     in the same launch, then the after-gate kernel) equals gemv +
