@@ -1296,135 +1296,181 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgsF32 g) {
     }
 }
 
-// f32 tiled path: 64x64 tile, 256 threads x (4x4) outputs, K step 32,
-// operands loaded as float4 along their contiguous dimension (K or M/N),
-// the next step's loads issued into registers before this step's FMAs,
-// two LDS stages.  The K range (both products concatenated, the first's K a
+// f32 tiled path on the fp32 MFMA (v_mfma_f32_32x32x2_f32): 64x64 C tile
+// per 512-thread workgroup.  Waves w and w + 4 share the 32x32 block w of
+// the tile and split each 32-deep K step between them (two waves per SIMD:
+// one's LDS reads and barrier wait overlap the other's MFMAs, which one wave
+// per SIMD leaves exposed when the tiles fill each CU once); their sums are
+// added through LDS at the end.  Each step's two 8 KB operand tiles come in
+// by direct-to-LDS buffer loads (1 KB per wave instruction, 16 per step)
+// into four LDS stages, the loads of steps i + 1 .. i + 3 in flight while
+// step i multiplies.  Rows beyond the extent and K beyond the product's K
+// read as zeros through out-of-range buffer offsets (the dispatch keeps the
+// contiguous extent a multiple of 4, so a 16-byte chunk is all in range or
+// all out).  MFMA step s (0-7) of wave group g multiplies K values
+// 8 g + s (lanes 0-31) and 16 + 8 g + s (lanes 32-63): the order of the K
+// sum is the hardware's, so results agree with a scalar loop to f32
+// rounding.  The K range (both products concatenated, the first's K a
 // multiple of 32) can be split over gridDim.z workgroups: split z adds
 // [z kchunk, (z+1) kchunk) and writes its f32 partial tile to ws + z stride,
 // summed in split order by splitk_reduce_kernel.  KC: operand contiguous
 // along K; else along M (A) or N (B).
-constexpr int kF32BM = 64, kF32BK = 32, kF32Pad = 68;
-
-struct F32Step {
-  float4 a[2], b[2];
-};
+//
+// LDS of an operand tile (8 rows of 1 KB, one per load instruction):
+// KC: tile row r (M or N) at (r / 8) * 1024 + (r % 8) * 128, its 16-byte K
+//     chunk c in slot c ^ ((r >> 1) & 7) — the 16-byte reads of one chunk
+//     of 16 consecutive rows are free of bank conflicts;
+// MN: K row k at (k / 4) * 1056 + (k % 4) * 256, 64 floats of M or N — the
+//     32-byte skew per load puts rows k and k + 16, read by the two lane
+//     halves of one MFMA step, on different banks.
+constexpr int kF32BM = 64, kF32BK = 32, kF32Stages = 4;
+constexpr int kF32OpBytes = 8 * 1056;
+constexpr int kF32StageBytes = 2 * kF32OpBytes;
 
 template <bool KC>
-__device__ __forceinline__ float4 f32_load4(const float* p, int64_t s_row, int64_t s_k, int row, int rows,
-                                           int k, int K) {
-  // four consecutive elements along the contiguous dimension, masked
-  float v[4];
-  if (KC) {
-    const float* q = p + static_cast<int64_t>(row) * s_row + k;
-    if (row < rows && k + 4 <= K) return *reinterpret_cast<const float4*>(q);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (row < rows && k + e < K) ? q[e] : 0.f;
-  } else {
-    const float* q = p + static_cast<int64_t>(k) * s_k + row;
-    if (k < K && row + 4 <= rows) return *reinterpret_cast<const float4*>(q);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (k < K && row + e < rows) ? q[e] : 0.f;
-  }
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-
-template <bool A_KC, bool B_KC>
-__device__ __forceinline__ void f32_load_step(F32Step& L, const GemmArgsF32& g, int k0, int m0, int n0) {
-  const int t = threadIdx.x;
-  const bool p2 = k0 >= g.K1;
-  const float* A = p2 ? g.A2 : g.A1;
-  const float* B = p2 ? g.B2 : g.B1;
-  const int K = p2 ? g.K2 : g.K1;
-  const int k = p2 ? k0 - g.K1 : k0;
-  const int64_t am = p2 ? g.a2m : g.a1m, ak = p2 ? g.a2k : g.a1k;
-  const int64_t bk = p2 ? g.b2k : g.b1k, bn = p2 ? g.b2n : g.b1n;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = t + 256 * h;  // 512 float4 per operand tile
-    if (A_KC) L.a[h] = f32_load4<true>(A, am, ak, m0 + q / 8, g.M, k + (q % 8) * 4, K);
-    else L.a[h] = f32_load4<false>(A, am, ak, m0 + (q % 16) * 4, g.M, k + q / 16, K);
-    if (B_KC) L.b[h] = f32_load4<true>(B, bn, bk, n0 + q / 8, g.N, k + (q % 8) * 4, K);
-    else L.b[h] = f32_load4<false>(B, bn, bk, n0 + (q % 16) * 4, g.N, k + q / 16, K);
-  }
-}
-
-// LDS: As[k][m], Bs[k][n] (row pitch kF32Pad floats)
-template <bool A_KC, bool B_KC>
-__device__ __forceinline__ void f32_store_step(const F32Step& L, float* As, float* Bs) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = t + 256 * h;
-    const float a[4] = {L.a[h].x, L.a[h].y, L.a[h].z, L.a[h].w};
-    const float b[4] = {L.b[h].x, L.b[h].y, L.b[h].z, L.b[h].w};
-    if (A_KC) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) As[((q % 8) * 4 + e) * kF32Pad + q / 8] = a[e];
-    } else {
-      *reinterpret_cast<float4*>(As + (q / 16) * kF32Pad + (q % 16) * 4) = L.a[h];
+struct F32Load {
+  static constexpr int kPitch = KC ? 1024 : 1056;  // LDS bytes per load instruction
+  // byte offset of lane `lane`'s 16 bytes of load j (0-7) of the tile of K
+  // step k0 (K the product's), or kOob
+  __device__ __forceinline__ static uint32_t offset(int j, int lane, int row0, int ext, int64_t ld, int k0,
+                                                    int K) {
+    if (KC) {
+      const int r = 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int k = k0 + 4 * c;
+      const bool ok = row0 + r < ext && k < K;
+      return ok ? static_cast<uint32_t>(((row0 + r) * ld + k) * 4) : kOob;
     }
-    if (B_KC) {
+    const int k = k0 + 4 * j + (lane >> 4);
+    const int m = row0 + 4 * (lane & 15);
+    const bool ok = k < K && m < ext;
+    return ok ? static_cast<uint32_t>((k * ld + m) * 4) : kOob;
+  }
+  // the lane's operands of the 8 MFMA steps of wave group g: tile row `row`,
+  // K values 16 h + 8 g + s (x4[j] holds steps 4j .. 4j + 3)
+  __device__ __forceinline__ static void read(const char* tile, int row, int h, int g, float4 (&x4)[2]) {
+    if (KC) {
+      const char* rp = tile + (row >> 3) * 1024 + (row & 7) * 128;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Bs[((q % 8) * 4 + e) * kF32Pad + q / 8] = b[e];
+      for (int j = 0; j < 2; ++j)
+        x4[j] = *reinterpret_cast<const float4*>(rp + (((4 * h + 2 * g + j) ^ ((row >> 1) & 7)) << 4));
     } else {
-      *reinterpret_cast<float4*>(Bs + (q / 16) * kF32Pad + (q % 16) * 4) = L.b[h];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int k = 16 * h + 8 * g + 4 * j + e;
+          v[e] = *reinterpret_cast<const float*>(tile + (k >> 2) * 1056 + (k & 3) * 256 + row * 4);
+        }
+        x4[j] = make_float4(v[0], v[1], v[2], v[3]);
+      }
     }
   }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t f32_rsrc(const float* p, int64_t rows, int64_t ld,
+                                                           int64_t cols) {
+  const int64_t bytes = rows > 0 && cols > 0 ? ((rows - 1) * ld + cols) * 4 : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, static_cast<int>(bytes),
+                                           kBufferFlags);
 }
 
 template <bool A_KC, bool B_KC>
-__global__ __launch_bounds__(256) void gemm_f32_tiled_kernel(GemmArgsF32 g, int kchunk, float* ws,
+__global__ __launch_bounds__(512) void gemm_f32_tiled_kernel(GemmArgsF32 g, int kchunk, float* ws,
                                                              int64_t ws_stride, int64_t ldw) {
-  __shared__ __attribute__((aligned(16))) float As[2][kF32BK * kF32Pad];
-  __shared__ __attribute__((aligned(16))) float Bs[2][kF32BK * kF32Pad];
+  __shared__ __attribute__((aligned(1024))) char lds[kF32Stages * kF32StageBytes];
   const int tid = threadIdx.x;
-  const int tr = tid / 16, tc = tid % 16;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int grp = wave >> 2, blk = wave & 3;
   const int m0 = blockIdx.y * kF32BM, n0 = blockIdx.x * kF32BM;
+  const int bm = (blk >> 1) * 32, bn = (blk & 1) * 32;
   const int ktot = g.K1 + g.K2;
   const int klo = blockIdx.z * kchunk;
   const int khi = min(ktot, klo + kchunk);
-  float acc[4][4] = {};
-  F32Step L;
-  if (klo < khi) {
-    f32_load_step<A_KC, B_KC>(L, g, klo, m0, n0);
-    f32_store_step<A_KC, B_KC>(L, As[0], Bs[0]);
+  const int nsteps = klo < khi ? (khi - klo + kF32BK - 1) / kF32BK : 0;
+  // operand resources: KC rows of K values, else K rows of M (N) values
+  const __amdgpu_buffer_rsrc_t ra1 = A_KC ? f32_rsrc(g.A1, g.M, g.a1m, g.K1) : f32_rsrc(g.A1, g.K1, g.a1k, g.M);
+  const __amdgpu_buffer_rsrc_t rb1 = B_KC ? f32_rsrc(g.B1, g.N, g.b1n, g.K1) : f32_rsrc(g.B1, g.K1, g.b1k, g.N);
+  const __amdgpu_buffer_rsrc_t ra2 = A_KC ? f32_rsrc(g.A2, g.M, g.a2m, g.K2) : f32_rsrc(g.A2, g.K2, g.a2k, g.M);
+  const __amdgpu_buffer_rsrc_t rb2 = B_KC ? f32_rsrc(g.B2, g.N, g.b2n, g.K2) : f32_rsrc(g.B2, g.K2, g.b2k, g.N);
+  const uint32_t lds0 = lds_addr(lds);
+  // the two loads of K step i (this wave's load `wave` of each operand
+  // tile) into stage i % 4
+  auto issue = [&](int i) {
+    const int kk = klo + i * kF32BK;
+    const bool p2 = kk >= g.K1;
+    const int k0 = p2 ? kk - g.K1 : kk;
+    const int K = p2 ? g.K2 : g.K1;
+    const __amdgpu_buffer_rsrc_t ra = p2 ? ra2 : ra1, rb = p2 ? rb2 : rb1;
+    const int64_t lda = A_KC ? (p2 ? g.a2m : g.a1m) : (p2 ? g.a2k : g.a1k);
+    const int64_t ldb = B_KC ? (p2 ? g.b2n : g.b1n) : (p2 ? g.b2k : g.b1k);
+    const uint32_t st = lds0 + (i % kF32Stages) * kF32StageBytes;
+    dma16(ra, __builtin_amdgcn_readfirstlane(st + wave * F32Load<A_KC>::kPitch),
+          F32Load<A_KC>::offset(wave, lane, m0, g.M, lda, k0, K));
+    dma16(rb, __builtin_amdgcn_readfirstlane(st + kF32OpBytes + wave * F32Load<B_KC>::kPitch),
+          F32Load<B_KC>::offset(wave, lane, n0, g.N, ldb, k0, K));
+  };
+  // wait until the loads of all but the `newer` most recent steps have landed
+  auto wait_steps = [](int newer) {
+    if (newer >= 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if (newer == 1) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  // two accumulation chains (even and odd MFMAs of a step)
+  f32x16_t acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.0f;
+  for (int i = 0; i < kF32Stages - 1 && i < nsteps; ++i) issue(i);
+  wait_steps(min(nsteps, kF32Stages - 1) - 1);
+  __syncthreads();
+  const int h = lane >> 5;
+  for (int i = 0; i < nsteps; ++i) {
+    const char* st = lds + (i % kF32Stages) * kF32StageBytes;
+    float4 a4[2], b4[2];
+    F32Load<A_KC>::read(st, bm + (lane & 31), h, grp, a4);
+    F32Load<B_KC>::read(st + kF32OpBytes, bn + (lane & 31), h, grp, b4);
+    // step i + 3 into the stage step i - 1 used (all its reads ended at the
+    // barrier that closed step i - 1)
+    if (i + kF32Stages - 1 < nsteps) issue(i + kF32Stages - 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[j].x, b4[j].x, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[j].y, b4[j].y, acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[j].z, b4[j].z, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[j].w, b4[j].w, acc1, 0, 0, 0);
+    }
+    // step i + 1's loads have landed (those of the steps after it may be in flight)
+    wait_steps(min(nsteps - 1, i + kF32Stages - 1) - (i + 1));
+    __syncthreads();
+  }
+  // group 1 hands its sums to group 0 through LDS (stage memory, free after
+  // the loop's last barrier): lane-major, 16 KB
+  float* red = reinterpret_cast<float*>(lds);
+  if (grp == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[(blk * 16 + r) * 64 + lane] = acc0[r] + acc1[r];
   }
   __syncthreads();
-  int buf = 0;
-  for (int k0 = klo; k0 < khi; k0 += kF32BK) {
-    const bool more = k0 + kF32BK < khi;
-    if (more) f32_load_step<A_KC, B_KC>(L, g, k0 + kF32BK, m0, n0);
-    const float* as = As[buf];
-    const float* bs = Bs[buf];
-#pragma unroll 8
-    for (int kk = 0; kk < kF32BK; ++kk) {
-      const float4 a4 = *reinterpret_cast<const float4*>(as + kk * kF32Pad + tr * 4);
-      const float4 b4 = *reinterpret_cast<const float4*>(bs + kk * kF32Pad + tc * 4);
-      const float a[4] = {a4.x, a4.y, a4.z, a4.w};
-      const float b[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-    }
-    if (more) f32_store_step<A_KC, B_KC>(L, As[buf ^ 1], Bs[buf ^ 1]);
-    __syncthreads();
-    buf ^= 1;
-  }
+  if (grp == 1) return;
+  // lane l holds column l & 31 of the wave's block, rows 8 (r / 4) + 4 (l / 32) + r % 4
   float* dst = ws ? ws + blockIdx.z * ws_stride : g.C;
   const int64_t ld = ws ? ldw : g.ldc;
+  const int c = n0 + bn + (lane & 31);
+  if (c < g.N) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int r = m0 + tr * 4 + i, c = n0 + tc * 4 + j;
-      if (r < g.M && c < g.N) dst[static_cast<int64_t>(r) * ld + c] = acc[i][j];
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + bm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (row < g.M) dst[static_cast<int64_t>(row) * ld + c] = (acc0[r] + acc1[r]) + red[(blk * 16 + r) * 64 + lane];
     }
+  }
 }
 
-// Split of an f32 GEMM over K: workgroups for about two per CU when the
-// tiles alone leave CUs idle, with at least two K steps per split.
+// Split of an f32 GEMM over K.  A CU's MFMA pipes run its workgroups'
+// steps one after another whatever their number, so the time of the
+// busiest CU is ceil(tiles * splits / CUs) workgroups of ceil(steps /
+// splits) K steps; a split adds the reduction of the f32 partials (a
+// launch of ~4 us, ~9 K steps).  The split count minimising that wins.
 struct F32Split {
   int ksplit, kchunk;
   int64_t ldw, bytes;
@@ -1495,20 +1541,27 @@ bool make_operand(const void* p, int64_t ld, bool kc, int64_t ext, int64_t K, Op
 
 
 F32Split plan_f32(int64_t M, int64_t N, int64_t K, int64_t K2) {
+  constexpr int64_t kReduceSteps = 9;
   F32Split p{1, 0, 0, 0};
   const int64_t ktot = K + K2;
   const int64_t tiles = ((M + kF32BM - 1) / kF32BM) * ((N + kF32BM - 1) / kF32BM);
   const int64_t steps = (ktot + kF32BK - 1) / kF32BK;
   p.kchunk = static_cast<int>(steps * kF32BK);
-  const int64_t want = 2 * static_cast<int64_t>(cu_count());
-  if (tiles >= want || steps < 4) return p;
-  int64_t ks = (want + tiles - 1) / tiles;
-  if (ks > steps / 2) ks = steps / 2;
-  if (ks > 16) ks = 16;
-  if (ks < 2) return p;
-  const int64_t per = (steps + ks - 1) / ks;
-  p.kchunk = static_cast<int>(per * kF32BK);
-  p.ksplit = static_cast<int>((steps + per - 1) / per);
+  const int64_t cus = cu_count();
+  if (steps < 4 || tiles <= 0) return p;
+  int64_t best = (tiles + cus - 1) / cus * steps, best_per = steps;
+  for (int64_t ks = 2; ks <= 16 && 2 * ks <= steps; ++ks) {
+    const int64_t per = (steps + ks - 1) / ks;
+    const int64_t n = (steps + per - 1) / per;
+    const int64_t cost = (tiles * n + cus - 1) / cus * per + kReduceSteps;
+    if (cost < best) {
+      best = cost;
+      best_per = per;
+    }
+  }
+  if (best_per == steps) return p;
+  p.kchunk = static_cast<int>(best_per * kF32BK);
+  p.ksplit = static_cast<int>((steps + best_per - 1) / best_per);
   p.ldw = (N + 3) / 4 * 4;
   p.bytes = static_cast<int64_t>(p.ksplit) * M * p.ldw * 4;
   return p;
@@ -1830,19 +1883,31 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     MOC_REQUIRE(grid.y <= 65535, "moc_gemm: M too large for the f32 grid");
     // tiled path: each operand contiguous along K or along M/N with 16-byte
-    // rows, both products with the same layouts, the first product's K a
-    // multiple of the K step when there is a second
-    auto f32_layout = [](const void* p, int64_t s_mn, int64_t s_k) -> int {
+    // rows and that extent (K, or M/N) a multiple of 4, both products with
+    // the same layouts, the first product's K a multiple of the K step when
+    // there is a second
+    auto f32_layout = [](const void* p, int64_t s_mn, int64_t s_k, int64_t mn, int64_t k) -> int {
       if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return -1;
-      if (s_k == 1 && s_mn % 4 == 0) return 1;  // KC
-      if (s_mn == 1 && s_k % 4 == 0) return 0;  // MN
+      if (s_k == 1 && s_mn % 4 == 0 && k % 4 == 0) return 1;  // KC
+      if (s_mn == 1 && s_k % 4 == 0 && mn % 4 == 0) return 0;  // MN
       return -1;
     };
-    int la = K > 0 ? f32_layout(A, a_sm, a_sk) : 1, lb = K > 0 ? f32_layout(B, b_sn, b_sk) : 1;
+    int la = K > 0 ? f32_layout(A, a_sm, a_sk, M, K) : 1, lb = K > 0 ? f32_layout(B, b_sn, b_sk, N, K) : 1;
     if (second) {
-      if (f32_layout(A2, a2_sm, a2_sk) != la || f32_layout(B2, b2_sn, b2_sk) != lb || K % kF32BK != 0)
+      if (f32_layout(A2, a2_sm, a2_sk, M, K2) != la || f32_layout(B2, b2_sn, b2_sk, N, K2) != lb ||
+          K % kF32BK != 0)
         la = -1;
     }
+    // and its bytes addressable by 32-bit buffer offsets below kOob
+    auto fits = [](int kc, int64_t mn, int64_t s_mn, int64_t s_k, int64_t k) {
+      if (mn <= 0 || k <= 0) return true;
+      const int64_t bytes = kc ? ((mn - 1) * s_mn + k) * 4 : ((k - 1) * s_k + mn) * 4;
+      return bytes < static_cast<int64_t>(kOob) - 16;
+    };
+    if (la >= 0 && lb >= 0 &&
+        !(fits(la, M, a_sm, a_sk, K) && fits(lb, N, b_sn, b_sk, K) &&
+          (!second || (fits(la, M, a2_sm, a2_sk, K2) && fits(lb, N, b2_sn, b2_sk, K2)))))
+      la = -1;
     if (la < 0 || lb < 0 || K + (second ? K2 : 0) == 0) {
       gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
       return check_launch("gemm_f32_kernel");
@@ -1861,7 +1926,7 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     const dim3 g3(grid.x, grid.y, static_cast<unsigned>(sp.ksplit));
     const int64_t stride = M * sp.ldw;
 #define MOC_F32T(AK, BK)                                                                          \
-  gemm_f32_tiled_kernel<AK, BK><<<g3, 256, 0, st>>>(a, sp.kchunk, ws, stride, sp.ldw)
+  gemm_f32_tiled_kernel<AK, BK><<<g3, 512, 0, st>>>(a, sp.kchunk, ws, stride, sp.ldw)
     if (la == 1 && lb == 1) MOC_F32T(true, true);
     else if (la == 1) MOC_F32T(true, false);
     else if (lb == 1) MOC_F32T(false, true);

@@ -336,11 +336,13 @@ def test_gemm_dual_product_and_f32():
 
 @pytest.mark.parametrize("layout", ["kckc", "kcmn", "mnkc", "mnmn"])
 @pytest.mark.parametrize("mnk", [(512, 1376, 512), (512, 512, 1376), (67, 45, 130), (1, 5, 7),
-                                 (300, 260, 64)])
+                                 (300, 260, 64), (68, 44, 132), (64, 128, 4096), (2048, 512, 512)])
 def test_gemm_f32_tiled(layout, mnk):
-    """The f32 GEMM (64x64 tiles, K split over f32 partials summed in a fixed
-    order when the tiles leave CUs idle) in all four operand layouts,
-    against float64; repeat calls are identical."""
+    """The f32 GEMM (fp32 MFMA, 64x64 tiles, K split over f32 partials summed
+    in a fixed order when that shortens the busiest CU's work) in all four
+    operand layouts, against float64; repeat calls are identical.  Extents
+    not a multiple of 4 along an operand's contiguous dimension take the
+    generic kernel (67, 45, 130 and 1, 5, 7 in the MN layouts)."""
     M, Nn, Kk = mnk
     g = gen(M * 7 + Nn + Kk)
     a, b = torch.randn(M, Kk, generator=g), torch.randn(Kk, Nn, generator=g)
