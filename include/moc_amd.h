@@ -218,6 +218,19 @@ int moc_ffn_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int 
                          void* idx, int idx_dtype, void* u_s, void* s_s, void* z_s, void* out, int64_t ldo,
                          void* workspace, int64_t workspace_bytes, void* stream);
 
+/* GEMM workspace bytes of moc_ffn_forward_f32 (0: none). */
+int64_t moc_ffn_forward_f32_workspace_size(int64_t rows, int64_t d, int64_t inter);
+
+/* moc_ffn_forward_bf16 with f32 operands and outputs (the reference's f32
+ * path, _MoCFunction.forward, moc/ffn.py:130-173): the same steps and
+ * arguments, every float pointer f32 with 16-byte aligned rows; G and U run
+ * on the fp32 MFMA as one launch where the split plan allows. */
+int moc_ffn_forward_f32(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection, const void* x,
+                        int64_t ldx, const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
+                        const void* wd, int64_t ldwd, void* g, void* u, int64_t ld_gu, void* vals,
+                        void* idx, int idx_dtype, void* u_s, void* s_s, void* z_s, void* out, int64_t ldo,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 /* GEMM workspace bytes of moc_ffn_backward_bf16 (0: none). */
 int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu, int stacked);
 

@@ -63,6 +63,10 @@ SIGNATURES: dict[str, tuple] = {
     "moc_ffn_forward_bf16": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
                                     _i64, _vp, _vp, _i64, _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp,
                                     _i64, _vp]),
+    "moc_ffn_forward_f32_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "moc_ffn_forward_f32": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
+                                   _i64, _vp, _vp, _i64, _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp,
+                                   _i64, _vp]),
     "moc_ffn_backward_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _int]),
     "moc_ffn_backward_bf16": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _vp,
                                      _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,

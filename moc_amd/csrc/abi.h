@@ -46,6 +46,11 @@ int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* w
                         int64_t inter, int64_t* idx, uint16_t* sz, hipStream_t st, uint16_t* ap = nullptr,
                         int64_t ld_ap = 0, uint32_t* meta = nullptr, int64_t meta_rows = 0);
 
+// f32 pair C1 = A W1^T, C2 = A W2^T as one launch (gemm.hip); 1: shapes not
+// taken (nothing launched).
+int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* W1,
+                  const float* W2, int64_t ldw, float* C1, float* C2, int64_t ldc, hipStream_t st);
+
 }  // namespace moc
 
 #define MOC_REQUIRE(cond, ...)        \

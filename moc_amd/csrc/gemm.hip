@@ -1248,6 +1248,11 @@ struct GemmArgsF32 {
   int64_t a1m, a1k, b1k, b1n, a2m, a2k, b2k, b2n;
   float* C;
   int64_t ldc;
+  // pair (ncat > 0, tiled kernel only): column tiles from ncat on compute
+  // Cp = A Bp^T with Bp laid out as B1
+  const float* Bp;
+  float* Cp;
+  int ncat;
 };
 
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgsF32 g) {
@@ -1383,7 +1388,13 @@ __global__ __launch_bounds__(512) void gemm_f32_tiled_kernel(GemmArgsF32 g, int 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2, blk = wave & 3;
-  const int m0 = blockIdx.y * kF32BM, n0 = blockIdx.x * kF32BM;
+  int bx = blockIdx.x;
+  if (g.ncat > 0 && bx >= g.ncat) {  // the pair's second product
+    bx -= g.ncat;
+    g.B1 = g.Bp;
+    g.C = g.Cp;
+  }
+  const int m0 = blockIdx.y * kF32BM, n0 = bx * kF32BM;
   const int bm = (blk >> 1) * 32, bn = (blk & 1) * 32;
   const int ktot = g.K1 + g.K2;
   const int klo = blockIdx.z * kchunk;
@@ -2052,3 +2063,33 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     return check_launch("splitk_reduce_kernel");
   }
 }
+
+namespace moc {
+
+// f32 pair C1 = A W1^T and C2 = A W2^T (W1, W2: [N, K] rows of ldw, C1, C2
+// rows of ldc, A [M, K] rows of lda) as one launch of the tiled kernel,
+// their column tiles side by side.  Returns 1 without launching when the
+// shapes do not suit it (a layout the tiled kernel does not take, or a pair
+// the split plan would cut over K); the caller then issues two GEMMs.
+int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* W1,
+                  const float* W2, int64_t ldw, float* C1, float* C2, int64_t ldc, hipStream_t st) {
+  auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (M <= 0 || N <= 0 || K <= 0 || M >= (1LL << 31) || N >= (1LL << 30) || K % 4 != 0 || lda % 4 != 0 ||
+      ldw % 4 != 0 || !al(A) || !al(W1) || !al(W2) || C1 == nullptr || C2 == nullptr)
+    return 1;
+  if (((M - 1) * lda + K) * 4 >= static_cast<int64_t>(kOob) - 16 ||
+      ((N - 1) * ldw + K) * 4 >= static_cast<int64_t>(kOob) - 16)
+    return 1;
+  const int64_t tn = (N + kF32BM - 1) / kF32BM, tm = (M + kF32BM - 1) / kF32BM;
+  if (tm > 65535 || plan_f32(M, 2 * tn * kF32BM, K, 0).ksplit != 1) return 1;
+  GemmArgsF32 a{(int)M, (int)N, (int)K, 0, A, W1, nullptr, nullptr, lda, 1, 1, ldw, 0, 0, 0, 0, C1, ldc};
+  a.Bp = W2;
+  a.Cp = C2;
+  a.ncat = static_cast<int>(tn);
+  const dim3 grid(static_cast<unsigned>(2 * tn), static_cast<unsigned>(tm), 1);
+  gemm_f32_tiled_kernel<true, true><<<grid, 512, 0, st>>>(a, static_cast<int>((K + kF32BK - 1) / kF32BK * kF32BK),
+                                                          nullptr, 0, 0);
+  return check_launch("gemm_f32_tiled_kernel (pair)");
+}
+
+}  // namespace moc

@@ -1,5 +1,5 @@
-// The MoC FFN layer's forward and backward as one C-ABI call each: the
-// launches of the bf16 single-stream path (moc/ffn.py:124-259 for `moc`,
+// The MoC FFN layer's forward (bf16 or f32) and backward (bf16) as one C-ABI
+// call each: the launches of the single-stream path (moc/ffn.py:124-259 for `moc`,
 // :262-369 for the 2:8 and post-SiLU selections, :372-497 for `moc_gcp`)
 // issued from here instead of one host call per kernel.  At the shapes
 // whose GEMMs fill the CUs about once (the 130m and 350m layers) the layer
@@ -14,15 +14,75 @@
 
 namespace {
 
-int64_t gemm_ws(int64_t M, int64_t N, int64_t K, int64_t K2) {
-  const int64_t b = moc_gemm_workspace_size(MOC_BF16, M, N, K, K2);
+int64_t gemm_ws(int64_t M, int64_t N, int64_t K, int64_t K2, int dt = MOC_BF16) {
+  const int64_t b = moc_gemm_workspace_size(dt, M, N, K, K2);
   return b > 0 ? b : 0;
 }
 
 int64_t effective_2of8(int64_t inter) { return (inter / 8) * 2 + std::min<int64_t>(2, inter % 8); }
 
-bool ld_ok(const void* p, int64_t ld, int64_t cols) {
-  return p != nullptr && moc::aligned16(p) && ld % 8 == 0 && ld >= cols;
+// 16-byte aligned rows of at least `cols` elements of `esz` bytes
+bool ld_ok(const void* p, int64_t ld, int64_t cols, int64_t esz = 2) {
+  return p != nullptr && moc::aligned16(p) && (ld * esz) % 16 == 0 && ld >= cols;
+}
+
+// The forward of moc_ffn_forward_bf16 / moc_ffn_forward_f32 in element type
+// dt: G and U (one launch), the selection, the sparse aux, D.
+int ffn_forward(int dt, const char* name, int64_t rows, int64_t d, int64_t inter, int64_t k, int selection,
+                const void* x, int64_t ldx, const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
+                const void* wd, int64_t ldwd, void* g, void* u, int64_t ld_gu, void* vals, void* idx,
+                int idx_dtype, void* u_s, void* s_s, void* z_s, void* out, int64_t ldo, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  const int64_t esz = dt == MOC_BF16 ? 2 : 4;
+  MOC_REQUIRE(rows >= 1 && d >= 1 && inter >= 1 && k >= 1 && k <= inter, "%s: bad shape", name);
+  MOC_REQUIRE(selection >= 0 && selection <= 2, "%s: selection 0 (Top-K), 1 (Top-K of |SiLU(G)|) or 2 (top-2 of 8)",
+              name);
+  MOC_REQUIRE(selection != 2 || k == effective_2of8(inter), "%s: the 2:8 selection keeps %lld channels", name,
+              (long long)effective_2of8(inter));
+  MOC_REQUIRE(ld_ok(x, ldx, d, esz) && ld_ok(wg, ldwg, d, esz) && ld_ok(wu, ldwu, d, esz) &&
+                  ld_ok(wd, ldwd, inter, esz) && ld_ok(g, ld_gu, inter, esz) && ld_ok(u, ld_gu, inter, esz) &&
+                  ld_ok(out, ldo, d, esz),
+              "%s: operands need 16-byte aligned rows (leading dimensions multiples of %lld)", name,
+              (long long)(16 / esz));
+  MOC_REQUIRE(vals && idx && u_s, "%s: null output", name);
+  const int64_t need = dt == MOC_BF16 ? moc_ffn_forward_workspace_size(rows, d, inter)
+                                      : moc_ffn_forward_f32_workspace_size(rows, d, inter);
+  MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+              "%s: workspace of %lld bytes required", name, (long long)need);
+  // G = x Wg^T and U = x Wu^T (one launch)
+  int rc;
+  if (dt == MOC_BF16) {
+    rc = moc_gemm_pair(rows, d, x, ldx, wg, ldwg, inter, g, ld_gu, wu, ldwu, inter, u, ld_gu, workspace,
+                       workspace_bytes, stream);
+  } else {
+    rc = ldwg == ldwu ? moc::f32_gemm_pair(rows, inter, d, static_cast<const float*>(x), ldx,
+                                           static_cast<const float*>(wg), static_cast<const float*>(wu), ldwg,
+                                           static_cast<float*>(g), static_cast<float*>(u), ld_gu,
+                                           moc::as_stream(stream))
+                      : 1;
+    if (rc == 1) {  // two launches
+      rc = moc_gemm_ws(dt, rows, inter, d, x, ldx, 1, wg, 1, ldwg, 0, nullptr, 0, 0, nullptr, 0, 0, g, ld_gu, dt,
+                       workspace, workspace_bytes, stream);
+      if (rc == MOC_OK)
+        rc = moc_gemm_ws(dt, rows, inter, d, x, ldx, 1, wu, 1, ldwu, 0, nullptr, 0, 0, nullptr, 0, 0, u, ld_gu,
+                         dt, workspace, workspace_bytes, stream);
+    }
+  }
+  if (rc != MOC_OK) return rc;
+  // the selection (indices in ascending channel order) and its gate values
+  if (selection == 2)
+    rc = moc_select_2of8(dt, g, rows, inter, ld_gu, vals, idx, idx_dtype, stream);
+  else
+    rc = moc_topk_rows(dt, g, rows, inter, ld_gu, k, selection, vals, idx, idx_dtype, nullptr, 0, stream);
+  if (rc != MOC_OK) return rc;
+  // U at the selection, SiLU, Z; the dense zero-filled Z goes into G's
+  // buffer, which nothing reads after the selection
+  rc = moc_sparse_forward_aux(dt, vals, idx, idx_dtype, u, ld_gu, rows, k, inter, u_s, s_s, z_s, g, ld_gu,
+                              stream);
+  if (rc != MOC_OK) return rc;
+  // D = Z W_down^T
+  return moc_gemm_ws(dt, rows, d, inter, g, ld_gu, 1, wd, 1, ldwd, 0, nullptr, 0, 0, nullptr, 0, 0, out, ldo, dt,
+                     workspace, workspace_bytes, stream);
 }
 
 }  // namespace
@@ -33,42 +93,33 @@ extern "C" int64_t moc_ffn_forward_workspace_size(int64_t rows, int64_t d, int64
   return std::max(gemm_ws(rows, inter, d, 0), gemm_ws(rows, d, inter, 0));
 }
 
+// GEMM workspace of moc_ffn_forward_f32: G and U when they run as two
+// launches, and D = Z W_down^T.
+extern "C" int64_t moc_ffn_forward_f32_workspace_size(int64_t rows, int64_t d, int64_t inter) {
+  if (rows <= 0 || d <= 0 || inter <= 0) return 0;
+  return std::max(gemm_ws(rows, inter, d, 0, MOC_F32), gemm_ws(rows, d, inter, 0, MOC_F32));
+}
+
 extern "C" int moc_ffn_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection,
                                     const void* x, int64_t ldx, const void* wg, int64_t ldwg,
                                     const void* wu, int64_t ldwu, const void* wd, int64_t ldwd, void* g,
                                     void* u, int64_t ld_gu, void* vals, void* idx, int idx_dtype,
                                     void* u_s, void* s_s, void* z_s, void* out, int64_t ldo,
                                     void* workspace, int64_t workspace_bytes, void* stream) {
-  MOC_REQUIRE(rows >= 1 && d >= 1 && inter >= 1 && k >= 1 && k <= inter, "moc_ffn_forward_bf16: bad shape");
-  MOC_REQUIRE(selection >= 0 && selection <= 2, "moc_ffn_forward_bf16: selection 0 (Top-K), 1 (Top-K of "
-              "|SiLU(G)|) or 2 (top-2 of 8)");
-  MOC_REQUIRE(selection != 2 || k == effective_2of8(inter),
-              "moc_ffn_forward_bf16: the 2:8 selection keeps %lld channels", (long long)effective_2of8(inter));
-  MOC_REQUIRE(ld_ok(x, ldx, d) && ld_ok(wg, ldwg, d) && ld_ok(wu, ldwu, d) && ld_ok(wd, ldwd, inter) &&
-                  ld_ok(g, ld_gu, inter) && ld_ok(u, ld_gu, inter) && ld_ok(out, ldo, d),
-              "moc_ffn_forward_bf16: operands need 16-byte aligned rows (leading dimensions multiples of 8)");
-  MOC_REQUIRE(vals && idx && u_s, "moc_ffn_forward_bf16: null output");
-  const int64_t need = moc_ffn_forward_workspace_size(rows, d, inter);
-  MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
-              "moc_ffn_forward_bf16: workspace of %lld bytes required", (long long)need);
-  // G = x Wg^T and U = x Wu^T (one launch)
-  int rc = moc_gemm_pair(rows, d, x, ldx, wg, ldwg, inter, g, ld_gu, wu, ldwu, inter, u, ld_gu, workspace,
-                         workspace_bytes, stream);
-  if (rc != MOC_OK) return rc;
-  // the selection (indices in ascending channel order) and its gate values
-  if (selection == 2)
-    rc = moc_select_2of8(MOC_BF16, g, rows, inter, ld_gu, vals, idx, idx_dtype, stream);
-  else
-    rc = moc_topk_rows(MOC_BF16, g, rows, inter, ld_gu, k, selection, vals, idx, idx_dtype, nullptr, 0, stream);
-  if (rc != MOC_OK) return rc;
-  // U at the selection, SiLU, Z; the dense zero-filled Z goes into G's
-  // buffer, which nothing reads after the selection
-  rc = moc_sparse_forward_aux(MOC_BF16, vals, idx, idx_dtype, u, ld_gu, rows, k, inter, u_s, s_s, z_s, g,
-                              ld_gu, stream);
-  if (rc != MOC_OK) return rc;
-  // D = Z W_down^T
-  return moc_gemm_ws(MOC_BF16, rows, d, inter, g, ld_gu, 1, wd, 1, ldwd, 0, nullptr, 0, 0, nullptr, 0, 0, out,
-                     ldo, MOC_BF16, workspace, workspace_bytes, stream);
+  return ffn_forward(MOC_BF16, "moc_ffn_forward_bf16", rows, d, inter, k, selection, x, ldx, wg, ldwg, wu, ldwu,
+                     wd, ldwd, g, u, ld_gu, vals, idx, idx_dtype, u_s, s_s, z_s, out, ldo, workspace,
+                     workspace_bytes, stream);
+}
+
+extern "C" int moc_ffn_forward_f32(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection,
+                                   const void* x, int64_t ldx, const void* wg, int64_t ldwg, const void* wu,
+                                   int64_t ldwu, const void* wd, int64_t ldwd, void* g, void* u, int64_t ld_gu,
+                                   void* vals, void* idx, int idx_dtype, void* u_s, void* s_s, void* z_s,
+                                   void* out, int64_t ldo, void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  return ffn_forward(MOC_F32, "moc_ffn_forward_f32", rows, d, inter, k, selection, x, ldx, wg, ldwg, wu, ldwu,
+                     wd, ldwd, g, u, ld_gu, vals, idx, idx_dtype, u_s, s_s, z_s, out, ldo, workspace,
+                     workspace_bytes, stream);
 }
 
 // GEMM workspace of moc_ffn_backward_bf16 (stacked: dWg and dWu as one GEMM

@@ -137,17 +137,19 @@ _LAYER_WS: dict = {}
 USE_NATIVE_LAYER = True
 
 
-def _layer_ok(x2, *weights) -> bool:
-    """True if the one-call native layer (moc_ffn_forward_bf16 /
-    moc_ffn_backward_bf16) takes these operands: bf16, several rows, every
-    row 16-byte aligned without a copy (hidden and intermediate sizes
-    multiples of 8, contiguous weights)."""
+def _layer_ok(x2, *weights, dtypes=(torch.bfloat16,)) -> bool:
+    """True if the one-call native layer (moc_ffn_forward_bf16 / _f32,
+    moc_ffn_backward_bf16) takes these operands: one of `dtypes`, all alike,
+    several rows, every row 16-byte aligned without a copy (hidden and
+    intermediate sizes multiples of 16 bytes, contiguous weights)."""
     # the GEMM timing probe brackets every GEMM launch from Python
-    if not USE_NATIVE_LAYER or K._GEMM_PROBE is not None or x2.dtype != torch.bfloat16 or x2.shape[0] < 2 or x2.shape[1] % 8 or x2.stride(1) != 1 \
-            or x2.stride(0) % 8 or x2.data_ptr() % 16:
+    if not USE_NATIVE_LAYER or K._GEMM_PROBE is not None or x2.dtype not in dtypes:
+        return False
+    per16 = 16 // x2.element_size()
+    if x2.shape[0] < 2 or x2.shape[1] % per16 or x2.stride(1) != 1 or x2.stride(0) % per16 or x2.data_ptr() % 16:
         return False
     for w in weights:
-        if w.dtype != torch.bfloat16 or not w.is_contiguous() or w.data_ptr() % 16 or w.shape[1] % 8:
+        if w.dtype != x2.dtype or not w.is_contiguous() or w.data_ptr() % 16 or w.shape[1] % per16:
             return False
     return True
 
@@ -164,22 +166,24 @@ def _layer_forward(x, x2, gate_w, up_w, down_w, k, selection: str, idx_dtype, sa
     rows, d = x2.shape
     inter = gate_w.shape[0]
     dev = x2.device
-    bf16 = torch.bfloat16
-    pitch = K.row_pitch(inter, bf16)
+    dt = x2.dtype
+    f32 = dt == torch.float32
+    pitch = K.row_pitch(inter, dt)
     kk = _moc_2_8_effective_k(inter) if selection == "2of8" else k
-    g = torch.empty((rows, pitch), dtype=bf16, device=dev)
-    u = torch.empty((rows, pitch), dtype=bf16, device=dev)
-    vals = torch.empty((rows, kk), dtype=bf16, device=dev)
+    g = torch.empty((rows, pitch), dtype=dt, device=dev)
+    u = torch.empty((rows, pitch), dtype=dt, device=dev)
+    vals = torch.empty((rows, kk), dtype=dt, device=dev)
     idx = torch.empty((rows, kk), dtype=idx_dtype, device=dev)
-    u_s = torch.empty((rows, kk), dtype=bf16, device=dev)
-    s_s = torch.empty((rows, kk), dtype=bf16, device=dev) if save_s else None
-    z_s = torch.empty((rows, kk), dtype=bf16, device=dev) if save_s else None
+    u_s = torch.empty((rows, kk), dtype=dt, device=dev)
+    s_s = torch.empty((rows, kk), dtype=dt, device=dev) if save_s else None
+    z_s = torch.empty((rows, kk), dtype=dt, device=dev) if save_s else None
     d_out = down_w.shape[0]
-    out = torch.empty((rows, d_out), dtype=bf16, device=dev)
-    nbytes = _layer_ws_bytes(("f", dev.index, rows, d, inter), "moc_ffn_forward_workspace_size",
-                             rows, d, inter)
+    out = torch.empty((rows, d_out), dtype=dt, device=dev)
+    query = "moc_ffn_forward_f32_workspace_size" if f32 else "moc_ffn_forward_workspace_size"
+    nbytes = _layer_ws_bytes(("f", f32, dev.index, rows, d, inter), query, rows, d, inter)
     ws = K._gemm_workspace(dev, nbytes) if nbytes > 0 else None
-    N.call("moc_ffn_forward_bf16", rows, d, inter, kk, _SELECTION_CODE[selection], x2.data_ptr(),
+    N.call("moc_ffn_forward_f32" if f32 else "moc_ffn_forward_bf16", rows, d, inter, kk,
+             _SELECTION_CODE[selection], x2.data_ptr(),
              x2.stride(0), gate_w.data_ptr(), d, up_w.data_ptr(), d, down_w.data_ptr(), inter,
              g.data_ptr(), u.data_ptr(), pitch, vals.data_ptr(), idx.data_ptr(), N.idx_code(idx_dtype),
              u_s.data_ptr(), N.ptr(s_s), N.ptr(z_s), out.data_ptr(), d_out, N.ptr(ws), nbytes,
@@ -205,7 +209,8 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     # which the backward reuses, then runs on the side stream beside the
     # selection.  f32: U on the side stream beside G and the selection.
     side = _side_for(x.device, rows, inter)
-    if side is None and not want_mask and down_w.shape[0] == d and _layer_ok(x2, gate_w, up_w, down_w):
+    if side is None and not want_mask and down_w.shape[0] == d and \
+            _layer_ok(x2, gate_w, up_w, down_w, dtypes=(torch.bfloat16, torch.float32)):
         # one native call for the whole single-stream forward (host-bound shapes)
         return _layer_forward(x, x2, gate_w, up_w, down_w, k, selection, idx_dtype, save_s)
     g = K.padded_empty(rows, inter, x.dtype, x.device)

@@ -375,6 +375,36 @@ def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
         assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
 
 
+@pytest.mark.parametrize("mode", ["moc", "moc_gcp", "moc_2_8", "moc_post_silu_abs"])
+@pytest.mark.parametrize("shape", [(512, 512, 1376, 256), (300, 132, 404, 100)])
+def test_native_layer_f32_forward_matches_per_kernel_path(mode, shape, monkeypatch):
+    """The f32 one-call forward (moc_ffn_forward_f32: G and U as one fp32
+    MFMA launch, then the selection, the sparse aux and D) equals the
+    per-kernel f32 path bit for bit, output and gradients (the f32 backward
+    runs per kernel either way).  (512, 512, 1376) is config 1's shape."""
+    from moc_amd import _native, ffn
+    rows, d, inter, k = shape
+    x, wg, wu, wd, go = make_inputs(rows, d, inter, torch.float32, seed=rows + inter)
+    calls = []
+    real_call = _native.call
+
+    def spy(name, *args):
+        calls.append(name)
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_native, "call", spy)
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", True)
+    a = run_module(mode, x, wg, wu, wd, go, k, index_save_dtype=None)
+    assert "moc_ffn_forward_f32" in calls and "moc_ffn_backward_bf16" not in calls
+    calls.clear()
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", False)
+    b = run_module(mode, x, wg, wu, wd, go, k, index_save_dtype=None)
+    assert "moc_ffn_forward_f32" not in calls
+    for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, b):
+        assert p.dtype == q.dtype == torch.float32 and p.shape == q.shape, name
+        assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
+
+
 def test_native_layer_f32_master_grads(monkeypatch):
     """Under autocast with f32 parameters the layer entry's weight
     gradients come out in f32, equal to the per-kernel path's."""
