@@ -2069,8 +2069,11 @@ namespace moc {
 // f32 pair C1 = A W1^T and C2 = A W2^T (W1, W2: [N, K] rows of ldw, C1, C2
 // rows of ldc, A [M, K] rows of lda) as one launch of the tiled kernel,
 // their column tiles side by side.  Returns 1 without launching when the
-// shapes do not suit it (a layout the tiled kernel does not take, or a pair
-// the split plan would cut over K); the caller then issues two GEMMs.
+// shapes do not suit it (a layout the tiled kernel does not take, or
+// products the split plan would cut over K on their own); the caller then
+// issues two GEMMs.  Where each product alone runs unsplit, the pair runs
+// unsplit too: the same steps per tile, two workgroups sharing a CU where
+// one product's tiles would leave CUs idle.
 int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* W1,
                   const float* W2, int64_t ldw, float* C1, float* C2, int64_t ldc, hipStream_t st) {
   auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
@@ -2081,7 +2084,7 @@ int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, 
       ((N - 1) * ldw + K) * 4 >= static_cast<int64_t>(kOob) - 16)
     return 1;
   const int64_t tn = (N + kF32BM - 1) / kF32BM, tm = (M + kF32BM - 1) / kF32BM;
-  if (tm > 65535 || plan_f32(M, 2 * tn * kF32BM, K, 0).ksplit != 1) return 1;
+  if (tm > 65535 || plan_f32(M, N, K, 0).ksplit != 1) return 1;
   GemmArgsF32 a{(int)M, (int)N, (int)K, 0, A, W1, nullptr, nullptr, lda, 1, 1, ldw, 0, 0, 0, 0, C1, ldc};
   a.Bp = W2;
   a.Cp = C2;
