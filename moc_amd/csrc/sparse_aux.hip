@@ -318,6 +318,73 @@ __global__ __launch_bounds__(kRowThreads) void forward_aux_rows_kernel(
   row_store<kRowThreads>(z_full + row * z_ld, zrow, z_ld);
 }
 
+// f32 form of forward_aux_rows_kernel (rows of at most kRowMaxLdF32 floats,
+// pitches multiples of 4): the element kernel's f32 arithmetic, the U row
+// staged in LDS and the dense Z row built there and written whole (no
+// zero-fill launch).
+constexpr int64_t kRowMaxLdF32 = 4096;
+
+template <typename IdxT>
+__global__ __launch_bounds__(kRowThreads) void forward_aux_rows_f32_kernel(
+    const float* __restrict__ vals, const IdxT* __restrict__ idx, const float* __restrict__ u_full,
+    int64_t u_ld, int k, int64_t inter, float* __restrict__ u_s, float* __restrict__ s_s,
+    float* __restrict__ z_s, float* __restrict__ z_full, int64_t z_ld) {
+  extern __shared__ __attribute__((aligned(16))) float fbuf[];
+  float* urow = fbuf;        // [u_ld]
+  float* zrow = fbuf + u_ld;  // [z_ld]
+  const int64_t row = blockIdx.x;
+  constexpr int kMax = static_cast<int>(kRowMaxLdF32 / 4 / kRowThreads);
+  // the first entries' loads, then the U row's, before any is used
+  int64_t ch[kRowPer];
+  float gv[kRowPer];
+#pragma unroll
+  for (int q = 0; q < kRowPer; ++q) {
+    const int e = threadIdx.x + kRowThreads * q;
+    ch[q] = e < k ? static_cast<int64_t>(idx[row * k + e]) : -1;
+    gv[q] = e < k ? vals[row * k + e] : 0.0f;
+  }
+  float4 v[kMax];
+#pragma unroll
+  for (int q = 0; q < kMax; ++q) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(kRowThreads) * q;
+    v[q] = c < u_ld / 4 ? reinterpret_cast<const float4*>(u_full + row * u_ld)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int q = 0; q < kMax; ++q) {
+    const int64_t c = threadIdx.x + static_cast<int64_t>(kRowThreads) * q;
+    if (c < u_ld / 4) reinterpret_cast<float4*>(urow)[c] = v[q];
+  }
+  for (int64_t c = threadIdx.x; c < z_ld / 4; c += kRowThreads)
+    reinterpret_cast<float4*>(zrow)[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+  for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
+    if (e0 > 0) {
+#pragma unroll
+      for (int q = 0; q < kRowPer; ++q) {
+        const int e = e0 + threadIdx.x + kRowThreads * q;
+        ch[q] = e < k ? static_cast<int64_t>(idx[row * k + e]) : -1;
+        gv[q] = e < k ? vals[row * k + e] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kRowPer; ++q) {
+      if (ch[q] < 0 || ch[q] >= inter) continue;  // malformed index or past k: never touch memory
+      const int64_t i = row * k + e0 + threadIdx.x + kRowThreads * q;
+      const float g = gv[q];
+      const float u = urow[ch[q]];
+      const float sv = g * sigmoid_f32(g);
+      const float z = sv * u;
+      if (u_s) u_s[i] = u;
+      if (s_s) s_s[i] = sv;
+      if (z_s) z_s[i] = z;
+      zrow[ch[q]] = z;
+    }
+  }
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < z_ld / 4; c += kRowThreads)
+    reinterpret_cast<float4*>(z_full + row * z_ld)[c] = reinterpret_cast<const float4*>(zrow)[c];
+}
+
 template <typename IdxT>
 __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     const IdxT* __restrict__ idx, const uint16_t* __restrict__ g_s,
@@ -422,6 +489,20 @@ extern "C" int moc_sparse_forward_aux(int dtype, const void* topk_vals, const vo
     MOC_IDX_DISPATCH(idx_dtype, MOC_FWDR);
 #undef MOC_FWDR
     return check_launch("forward_aux_rows_kernel");
+  }
+  auto f32_row_ok = [](const void* p, int64_t ld) {
+    return ld % 4 == 0 && ld <= kRowMaxLdF32 && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+  };
+  if (dtype == MOC_F32 && z_full != nullptr && rows < (1LL << 31) && f32_row_ok(z_full, z_ld) &&
+      f32_row_ok(u_full, u_ld)) {
+    const size_t lds = static_cast<size_t>(u_ld + z_ld) * 4;
+#define MOC_FWDRF(T)                                                                           \
+  forward_aux_rows_f32_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>( \
+      (const float*)topk_vals, (const T*)idx, (const float*)u_full, u_ld, (int)k, inter,        \
+      (float*)u_sparse, (float*)s_sparse, (float*)z_sparse, (float*)z_full, z_ld)
+    MOC_IDX_DISPATCH(idx_dtype, MOC_FWDRF);
+#undef MOC_FWDRF
+    return check_launch("forward_aux_rows_f32_kernel");
   }
   if (z_full) {
     const int rc = moc_fill_zero(z_full, rows * z_ld * static_cast<int64_t>(esz), stream);

@@ -161,7 +161,8 @@ int launch_topk_kernel(const void* scores, int64_t rows, int inter, int64_t ld, 
 }
 
 // One wave per row while a thread's share fits 128 (f32) or 256 (bf16)
-// channels in registers; wider f32 rows use two waves per row.
+// channels in registers; wider f32 rows, and f32 rows of more than 960
+// channels when there are fewer rows than SIMDs, use two waves per row.
 template <bool BF16>
 int launch_topk(const void* scores, int64_t rows, int inter, int64_t ld, int k, int transform,
                 void* vals, void* idx, int idx_dtype, uint32_t* mask, int64_t mask_ld,
@@ -180,6 +181,14 @@ int launch_topk(const void* scores, int64_t rows, int inter, int64_t ld, int k, 
     case 15: MOC_TOPK(NW, 120); default: MOC_TOPK(NW, 128);              \
   }
   const int per1 = (inter + 63) / 64;
+  if constexpr (!BF16) {
+    // few rows (under one row-wave per SIMD): two waves per row halve each
+    // row's dependent chain (same selection)
+    if (rows < 4LL * cu_count() && per1 >= 16) {
+      const int per2 = (inter + 127) / 128;
+      MOC_TOPK_L8(2, per2);
+    }
+  }
   if (per1 <= 128) {
     MOC_TOPK_L8(1, per1);
   }

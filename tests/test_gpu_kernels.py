@@ -447,8 +447,11 @@ def test_select_2of8_bitexact():
 
 # ------------------------------------------------------------- training aux
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_sparse_aux_forward_backward(dtype):
-    rows, inter, k = 300, 2048, 384
+@pytest.mark.parametrize("shape", [(300, 2048, 384), (64, 5461, 1024)])
+def test_sparse_aux_forward_backward(dtype, shape):
+    """Row kernels (bf16 pitches up to 8192, f32 up to 4096) and, for f32
+    rows past that, the element kernels with a zero-fill, against the oracle."""
+    rows, inter, k = shape
     g = gen(6)
     G = torch.randn(rows, inter, generator=g).to(dtype)
     U = torch.randn(rows, inter, generator=g).to(dtype)
