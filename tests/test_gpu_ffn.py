@@ -376,7 +376,8 @@ def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
 
 
 @pytest.mark.parametrize("mode", ["moc", "moc_gcp", "moc_2_8", "moc_post_silu_abs"])
-@pytest.mark.parametrize("shape", [(512, 512, 1376, 256), (300, 132, 404, 100)])
+@pytest.mark.parametrize("shape", [(512, 512, 1376, 256), (300, 132, 404, 100), (2, 64, 100, 1),
+                                   (3, 128, 132, 132)])
 def test_native_layer_f32_forward_matches_per_kernel_path(mode, shape, monkeypatch):
     """The f32 one-call forward (moc_ffn_forward_f32: G and U as one fp32
     MFMA launch, then the selection, the sparse aux and D) equals the
@@ -403,6 +404,27 @@ def test_native_layer_f32_forward_matches_per_kernel_path(mode, shape, monkeypat
     for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, b):
         assert p.dtype == q.dtype == torch.float32 and p.shape == q.shape, name
         assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
+
+
+@pytest.mark.parametrize("shape", [(2, 64, 100, 1), (3, 128, 132, 132), (300, 132, 404, 100)])
+def test_native_layer_f32_forward_edges_vs_oracle(shape):
+    """The f32 one-call forward at edge shapes (two rows, k = 1, k = I, I not
+    a multiple of 8) against the oracle on the device's own G: the Top-K
+    indices bit-exact, the output within 1e-5."""
+    from moc_amd.ffn import MoCSwiGLUFFN
+    rows, d, inter, k = shape
+    x, wg, wu, wd, _ = make_inputs(rows, d, inter, torch.float32, seed=rows * 7 + inter)
+    m = MoCSwiGLUFFN(d, inter, k, mode="moc", index_save_dtype=None).to(DEV)
+    with torch.no_grad():
+        m.gate_proj.weight.copy_(wg)
+        m.up_proj.weight.copy_(wu)
+        m.down_proj.weight.copy_(wd)
+        out = m(x.to(DEV))
+    fwd = O.ffn_forward(x, wg, wu, wd, k, "moc", g_override=device_gate(x, wg))
+    close(out, fwd["out"], 1e-5, 1e-5, "out")
+    from moc_amd import kernels as K
+    _, idx, _ = K.topk_rows(device_gate(x, wg).to(DEV), k)
+    assert np.array_equal(idx.cpu().numpy(), fwd["idx"])
 
 
 def test_native_layer_f32_master_grads(monkeypatch):
