@@ -285,6 +285,7 @@ def _operand(t: torch.Tensor, bf16: bool) -> tuple[torch.Tensor, int, int]:
 
 
 _GEMM_WS: dict = {}
+_GEMM_WS_RETIRED: list = []
 
 # Optional timing probe: when a list is installed with set_gemm_probe(), every
 # GEMM launch made through gemm() / linear_pair() is bracketed by two timing
@@ -320,11 +321,15 @@ def _gemm_workspace(device, nbytes: int) -> torch.Tensor:
     Its first 4 KB hold arrival counters that must be zero when a GEMM starts
     and that every GEMM leaves zero, so the buffer is created zeroed and then
     reused without clearing; one buffer per stream keeps GEMMs that run
-    concurrently on different streams apart."""
+    concurrently on different streams apart.  An outgrown buffer is kept
+    alive, not freed, as the decode workspace is."""
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _GEMM_WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        _GEMM_WS.pop(key, None)
+        if ws is not None:
+            # kept alive, not freed: a HIP graph captured with it keeps
+            # writing to it on every replay
+            _GEMM_WS_RETIRED.append(ws)
         ws = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
         _GEMM_WS[key] = ws
     return ws
