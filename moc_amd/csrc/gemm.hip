@@ -1494,7 +1494,7 @@ void launch_bf16(const GemmArgs& a, bool out_f32, hipStream_t st, bool short_m =
   const dim3 grid(static_cast<unsigned>(units)), block(kThreads);
   const bool dual = a.nk[1] > 0;
   if constexpr (A_KC) {
-    if (a.pp && short_m) {  // 128 x 256 tiles, whole (no split, no fix-up)
+    if (a.pp && short_m) {  // 128 x 256 tiles, whole or with the two-part fix-up (no split)
       const dim3 pblock(kPpThreads);
       if (out_f32) {
         if (dual) gemm_pp_kernel<A_KC, B_KC, true, true, false, false, false, true><<<grid, pblock, 0, st>>>(a);
@@ -1625,10 +1625,9 @@ struct FixPlan {
   int64_t bytes = 0;
 };
 
-FixPlan plan_fix(int64_t M, int64_t N, int nk) {
+FixPlan plan_fix_tiles(int64_t tiles, int nk) {
   constexpr int64_t kUnit = 5, kFix = 4, kStore = 3;
   FixPlan f;
-  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const int64_t cus = cu_count();
   if (tiles <= 0 || 3 * tiles <= cus || tiles >= cus || nk < 8 || tiles * 4 > kFixCounterBytes) return f;
   const int64_t w = (tiles + (cus - tiles) - 1) / (cus - tiles);
@@ -1646,6 +1645,25 @@ FixPlan plan_fix(int64_t M, int64_t N, int nk) {
   f.split = static_cast<int>(best_s);
   f.bytes = kFixCounterBytes + tiles * 2 * kPartBytes;
   return f;
+}
+
+FixPlan plan_fix(int64_t M, int64_t N, int nk) {
+  return plan_fix_tiles(((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN), nk);
+}
+
+// A product whose 256x256 tiles fill at most a third of the CUs (split-K
+// territory) but whose 128-row tiles fill more: the 128-row tiles with the
+// two-part fix-up instead, no f32 partial tiles of the whole K range and no
+// reduction launch (the fix-up's partials are one per split tile).  Up to
+// kShortFixMaxKTiles: a 128-row K tile moves the B tile of a 256-row one for
+// half its MFMA work, so over a longer K the K split and its reduction win
+// (350m layer: D, 43 K tiles, 39.3 against 33.4 + 11.2 us; dX, 86, 62.4
+// against 49.0 + 12.0 us).
+constexpr int kShortFixMaxKTiles = 64;
+FixPlan plan_fix_short(int64_t M, int64_t N, int nk) {
+  const int64_t tiles256 = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  if (3 * tiles256 > cu_count() || nk > kShortFixMaxKTiles) return FixPlan();
+  return plan_fix_tiles(((M + 127) / 128) * ((N + kBN - 1) / kBN), nk);
 }
 
 }  // namespace
@@ -1710,7 +1728,7 @@ extern "C" int64_t moc_gemm_workspace_size(int dtype, int64_t M, int64_t N, int6
   }
   if (dtype != MOC_BF16) return 0;
   const int nk = static_cast<int>((K + kBK - 1) / kBK + (K2 + kBK - 1) / kBK);
-  return std::max(plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes);
+  return std::max({plan_split(M, N, nk).bytes, plan_fix(M, N, nk).bytes, plan_fix_short(M, N, nk).bytes});
 }
 
 // MoC 2:8 compacted Down on the structured-sparse MFMA:
@@ -2013,8 +2031,13 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
   // 72 us split against 78 us).
   const int64_t cus = cu_count();
   const int64_t tiles256 = static_cast<int64_t>(a.tiles_m) * a.tiles_n;
-  const bool short_m = a.pp && la == 1 && 4 * tiles256 > cus && 2 * tiles256 <= cus &&
-                       a.nk[0] + a.nk[1] <= kShortMaxKTiles;
+  const bool short_whole = a.pp && la == 1 && 4 * tiles256 > cus && 2 * tiles256 <= cus &&
+                           a.nk[0] + a.nk[1] <= kShortMaxKTiles;
+  // 128-row tiles in two K parts instead of a K split (see plan_fix_short)
+  const FixPlan sfp = a.pp && la == 1 && !short_whole ? plan_fix_short(M, N, a.nk[0] + a.nk[1]) : FixPlan();
+  const bool short_fix = sfp.tail > 0 && workspace != nullptr && workspace_bytes >= sfp.bytes &&
+                         reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
+  const bool short_m = short_whole || short_fix;
   if (short_m) a.tiles_m = static_cast<int>((M + 127) / 128);
   a.ksplit = 1;
   a.kper = a.nk[0] + a.nk[1];
@@ -2032,7 +2055,7 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
     run.ldc = sp.ldw;
     run.vec_store = 1;
   }
-  const FixPlan fp = (split || short_m) ? FixPlan() : plan_fix(M, N, a.nk[0] + a.nk[1]);
+  const FixPlan fp = short_fix ? sfp : (split || short_m) ? FixPlan() : plan_fix(M, N, a.nk[0] + a.nk[1]);
   const bool fix = a.pp && fp.tail > 0 && workspace != nullptr && workspace_bytes >= fp.bytes &&
                    reinterpret_cast<uintptr_t>(workspace) % 256 == 0;
   if (fix) {

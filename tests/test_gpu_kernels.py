@@ -305,6 +305,45 @@ def test_gemm_short_tiles_dual():
     bf16_close(K().gemm(gg, wg, a2=gu, b2=wu), ref, ulps=1, atol=1e-3)
 
 
+@pytest.mark.parametrize("mnk", [(4096, 1024, 2736), (4000, 1000, 2736), (4096, 1024, 1001)])
+def test_gemm_short_tiles_fixup(mnk):
+    """Products whose 256x256 tiles fill at most a third of the CUs but whose
+    128x256 tiles fill more (the 350m layer's D: 4096 x 1024 x 2736) run the
+    128-row tiles in two K parts with the fix-up instead of a K split:
+    against the fp32 reference, bit for bit on repeats (the fix-up's sum of
+    two partials does not depend on which part finishes first)."""
+    M, Nn, Kk = mnk
+    tiles = ((M + 255) // 256) * ((Nn + 255) // 256)
+    cus = K().cu_count(torch.cuda.current_device())
+    assert 3 * tiles <= cus < 6 * tiles
+    g = torch.Generator(device=DEV).manual_seed(18)
+    a = K().aligned_rows(torch.randn(M, Kk, device=DEV, generator=g).to(torch.bfloat16))
+    w = K().aligned_rows((torch.randn(Nn, Kk, device=DEV, generator=g) * 0.05).to(torch.bfloat16))
+    first = K().gemm(a, w.t(), out_dtype=torch.float32)
+    ref = a.float() @ w.float().t()
+    close(first, ref, rtol=1e-4, atol=2e-3)
+    for _ in range(3):
+        assert torch.equal(first, K().gemm(a, w.t(), out_dtype=torch.float32))
+    bf16_close(K().gemm(a, w.t()), ref, ulps=1, atol=2e-3)
+
+
+def test_gemm_short_tiles_fixup_dual():
+    """A dX-shaped dual product (4096 x 1024 x (1024 + 1024)) on 128-row
+    tiles in two K parts, against the fp32 reference and bit for bit on
+    repeats."""
+    g = torch.Generator(device=DEV).manual_seed(19)
+    T, I, d = 4096, 1024, 1024
+    gg = K().aligned_rows(torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16))
+    gu = K().aligned_rows(torch.randn(T, I, device=DEV, generator=g).to(torch.bfloat16))
+    wg = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(I, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    out = K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32)
+    ref = gg.float() @ wg.float() + gu.float() @ wu.float()
+    close(out, ref, rtol=1e-4, atol=1e-3)
+    for _ in range(3):
+        assert torch.equal(out, K().gemm(gg, wg, a2=gu, b2=wu, out_dtype=torch.float32))
+
+
 def test_gemm_workspace_shared_by_split_and_fixup():
     """Split-K and fix-up launches take turns on the stream's one workspace:
     the split-K partials leave the fix-up's arrival counters untouched."""
