@@ -11,7 +11,9 @@
 //
 // select_threshold finds the k-th largest key T and how many T-valued
 // channels still have to be taken (krem) by an MSB-first radix select with
-// 8-bit digits (2 passes over the registers for 16-bit keys, 4 for 32-bit).
+// 8-bit digits (2 passes over the registers for 16-bit keys, 4 for 32-bit;
+// one wave with 16-bit keys first tries two passes over the 4096 keys below
+// the row's largest, select_threshold_window).
 // The group counts into one 256-bin LDS histogram kept in C copies (lane % C
 // picks the copy): LDS atomics serialise on lanes of one instruction that
 // hit the same address, and real scores pile into a few exponent bins, so
@@ -250,10 +252,124 @@ __device__ __forceinline__ void raw_to_keys(int n, int c0, int transform, KeyOf 
   }
 }
 
+// Scan of one histogram (C copies summed) from the top bin down: the bin pb
+// holding the krem-th largest counted key and the count gt of keys in the
+// bins above it.  Lane l owns bins 255 - 64 m - l (m = 0..3): every m a run
+// of 64 descending bins in lane order, so the reads are bank-conflict free.
+// Returns false (pb, gt untouched) when fewer than krem keys were counted.
+template <int C>
+__device__ __forceinline__ bool sel_scan_bins(const uint32_t* hist, int lane, uint32_t krem, uint32_t& pb,
+                                              uint32_t& gt) {
+  constexpr int kPitch = sel_copy_pitch<C>();
+  uint32_t s[4], ge[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int bin = kSelBins - 1 - 64 * m - lane;
+    uint32_t v = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) v += hist[c * kPitch + bin];
+    s[m] = v;
+  }
+  // keys in bins >= bin
+  uint32_t base = 0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t incl = wave_inclusive_scan(s[m]);
+    ge[m] = base + incl;
+    base += wave_read_lane(incl, 63);
+  }
+  int hit_m = -1;
+  uint32_t hit_gt = 0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t g = ge[m] - s[m];
+    if (g < krem && ge[m] >= krem) {
+      hit_m = m;
+      hit_gt = g;
+    }
+  }
+  const unsigned long long hits = __ballot(hit_m >= 0);
+  if (hits == 0ull) return false;
+  const int src = __ffsll(hits) - 1;
+  pb = kSelBins - 1 - 64 * wave_read_lane(static_cast<uint32_t>(hit_m), src) - src;
+  gt = wave_read_lane(hit_gt, src);
+  return true;
+}
+
+// Largest value over the 64 lanes, returned to every lane.
+__device__ __forceinline__ uint32_t sel_wave_max(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror: every lane holds its row's max
+  return max(max(wave_read_lane(v, 0), wave_read_lane(v, 16)), max(wave_read_lane(v, 32), wave_read_lane(v, 48)));
+}
+
+// One wave, 16-bit keys: the threshold in two passes over a window below the
+// row's largest key hi, when the k-th largest key lies in [hi - 4095, hi]
+// (32 binades below the largest value).  Pass 1 counts bins of 16 keys (a
+// sixteenth of a binade) over the window, pass 2 the 16 keys of the bin
+// found.  The top byte of a key (sign and seven exponent bits) puts two
+// binades in one bin, a quarter of a Gaussian row's keys, and the atomic
+// adds of the 16 lanes that share a copy serialise on that address; a
+// sixteenth of a binade spreads the same keys over 32 bins.  Keys outside
+// the counted range go to the lane's spare bin: as unsigned values,
+// (key - base) >> 4 in pass 1 and (key - base) << 4 in pass 2 (in-bin keys
+// on every 16th bin) are then at least 256 (no key lies above the window).
+// Returns false, with nothing decided, when fewer than k keys lie in the
+// window (the caller then runs the byte-digit passes).
+template <int C, int W>
+__device__ __forceinline__ bool select_threshold_window(const uint32_t (&w)[W], uint32_t k, uint32_t* hist,
+                                                        uint32_t& thr, uint32_t& krem) {
+  constexpr int kPitch = sel_copy_pitch<C>();
+  constexpr int kHist = C * kPitch;
+  const int lane = threadIdx.x & 63;
+  uint32_t* mine = hist + (lane % C) * kPitch;
+  const uint32_t spare = kSelBins + lane / C;
+  auto bump = [&](uint32_t bin) {
+    __hip_atomic_fetch_add(&mine[bin], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+  sel_u16x2 m2 = {0, 0};
+#pragma unroll
+  for (int j = 0; j < W; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(sel_u16x2, w[j]));
+  const uint32_t hi = sel_wave_max(max(static_cast<uint32_t>(m2.x), static_cast<uint32_t>(m2.y)));
+  // the lowest real key is 0x80; padding keys (0) fall below the window
+  const int lo = max(static_cast<int>(hi) - 4095, 1);
+  for (int i = lane; i < kHist; i += 64) hist[i] = 0;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    bump(min(static_cast<uint32_t>(static_cast<int>(w[j] & 0xFFFFu) - lo) >> 4, spare));
+    bump(min(static_cast<uint32_t>(static_cast<int>(w[j] >> 16) - lo) >> 4, spare));
+  }
+  __builtin_amdgcn_wave_barrier();
+  uint32_t pb, gt;
+  if (!sel_scan_bins<C>(hist, lane, k, pb, gt)) return false;
+  krem = k - gt;
+  const int kb = lo + 16 * static_cast<int>(pb);  // the bin holds keys [kb, kb + 16)
+  __builtin_amdgcn_wave_barrier();
+  for (int i = lane; i < kHist; i += 64) hist[i] = 0;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    bump(min(static_cast<uint32_t>(static_cast<int>(w[j] & 0xFFFFu) - kb) << 4, spare));
+    bump(min(static_cast<uint32_t>(static_cast<int>(w[j] >> 16) - kb) << 4, spare));
+  }
+  __builtin_amdgcn_wave_barrier();
+  sel_scan_bins<C>(hist, lane, krem, pb, gt);  // krem of the bin's keys lie in the bin
+  thr = static_cast<uint32_t>(kb) + (pb >> 4);
+  krem -= gt;
+  return true;
+}
+
 template <int NW, int C, int W, int KEY_BITS>
 __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_t k,
                                                  uint32_t* hist, uint32_t& thr, uint32_t& krem) {
   static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 histogram copies");
+  if constexpr (NW == 1 && KEY_BITS == 16) {
+    if (select_threshold_window<C, W>(w, k, hist, thr, krem)) return;
+    __builtin_amdgcn_wave_barrier();
+  }
   constexpr int kPitch = sel_copy_pitch<C>();
   constexpr int kHist = C * kPitch;
   const int t = (NW > 1) ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x & 63);
@@ -298,38 +414,9 @@ __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_
       }
     }
     group_sync();
-    // lane l owns bins 255 - 64 m - l (m = 0..3): every m a run of 64
-    // descending bins in lane order, so the reads are bank-conflict free
-    uint32_t s[4], ge[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int bin = kSelBins - 1 - 64 * m - lane;
-      uint32_t v = 0;
-#pragma unroll
-      for (int c = 0; c < C; ++c) v += hist[c * kPitch + bin];
-      s[m] = v;
-    }
-    // keys in bins >= bin
-    uint32_t base = 0;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint32_t incl = wave_inclusive_scan(s[m]);
-      ge[m] = base + incl;
-      base += wave_read_lane(incl, 63);
-    }
-    int hit_m = -1;
-    uint32_t hit_gt = 0;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const uint32_t gt = ge[m] - s[m];
-      if (gt < krem && ge[m] >= krem) {
-        hit_m = m;
-        hit_gt = gt;
-      }
-    }
-    const int src = __ffsll(static_cast<unsigned long long>(__ballot(hit_m >= 0))) - 1;
-    const uint32_t pb = kSelBins - 1 - 64 * wave_read_lane(static_cast<uint32_t>(hit_m), src) - src;
-    krem -= wave_read_lane(hit_gt, src);
+    uint32_t pb = 0, gt = 0;
+    sel_scan_bins<C>(hist, lane, krem, pb, gt);  // the keys counted include the krem-th
+    krem -= gt;
     prefix |= pb << shift;
   }
   thr = prefix;

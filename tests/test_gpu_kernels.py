@@ -441,6 +441,24 @@ def test_topk_bitexact_vs_oracle(dtype, rows, inter, k):
     assert np.array_equal(m, O.topk_mask(want, inter))
 
 
+@pytest.mark.parametrize("k", [1, 100, 1024, 2600, 4000, 5461])
+def test_topk_wide_range_rows_vs_oracle(k):
+    """bf16 rows whose values span ~140 binades (some rows all negative, some
+    holding NaN or inf), so the k-th largest key falls inside, at the edge of
+    and below the 4096-key window under each row's largest key."""
+    g = gen(k)
+    rows, inter = 48, 5461
+    mag = torch.exp2(torch.rand(rows, inter, generator=g) * 140 - 70)
+    sign = torch.where(torch.rand(rows, inter, generator=g) < 0.3, -1.0, 1.0)
+    s = (sign * mag).to(torch.bfloat16)
+    s[::4] = -s[::4].abs()                               # all-negative rows
+    s[1::6, 17] = float("nan")
+    s[2::6, 33] = float("inf")
+    s[3::6, 40:60] = 2.0 ** 60                           # a block of equal top keys
+    _, idx, _ = K().topk_rows(s.to(DEV), k)
+    assert np.array_equal(idx.cpu().numpy(), O.topk_indices(s, k))
+
+
 def test_topk_heavy_ties_and_index_dtypes():
     vals = torch.tensor(np.random.default_rng(3).choice([0.0, -0.0, 1.0, -2.0, 0.5, float("inf")],
                                                         size=(33, 700)), dtype=torch.float32)
