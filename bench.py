@@ -51,6 +51,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
 D1B, I1B, K1B = 2048, 5461, 1024
+PROBE_STEPS = 5
 BATCH1B, SEQ1B = 64, 256
 
 
@@ -81,14 +82,62 @@ def parse_args():
     p.add_argument("--roofline-only", action="store_true",
                    help="only the seven GEMM launches of the roofline (for rocprofv3 kernel "
                         "traces whose per-kernel averages match roofline.per_launch)")
-    p.add_argument("--pmc-target", choices=["gemm", "dx", "copy", "decode", "down28", "down28_dense"],
+    p.add_argument("--pmc-target", choices=["gemm", "dx", "copy", "decode", "down28", "down28_dense",
+                                            "topk"],
                    default=None,
                    help="only launch one workload a few times (for rocprofv3 --pmc runs): the G,U "
                         "pair GEMM of the 1b layer, its dX GEMM (two products), a plain 256 MiB "
                         "copy kernel (counter scale), the B=1 decode layer over 8 weight sets, or "
                         "config 4's 2:8 Down (down28: structured-sparse MFMA over the packed "
-                        "selection; down28_dense: the same selection scattered dense)")
+                        "selection; down28_dense: the same selection scattered dense), or the "
+                        "row Top-K of the 1b training rows (topk: G of the bench input, "
+                        "16384 x 5461 bf16, K 1024, three calls)")
     return p.parse_args()
+
+
+def cfg5_model_flop(cfg, batch: int, seq: int) -> float:
+    """Algorithmic FLOP of one training step of the decoder (forward +
+    backward = 3 x forward): 2 FLOP per token per parameter of every matmul
+    (q/k/v and output projections, gate/up/down, LM head; not the embedding
+    lookup) plus the attention products QK^T and PV (2 x 2 x S^2 x d per
+    sequence and layer, over the full square).  The MoC FFN's nine GEMMs are
+    dense products in the reference (moc/ffn.py:389-494), so the count is
+    the same for both FFN types."""
+    L, d, inter, v = cfg.num_hidden_layers, cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    tokens = batch * seq
+    fwd = 2 * tokens * (L * (4 * d * d + 3 * d * inter) + v * d) + L * 2 * 2 * batch * seq * seq * d
+    return 3.0 * fwd
+
+
+def gpu_busy_ms(step, steps: int = 3):
+    """GPU-busy time per call of step(): the union of the device kernel and
+    copy intervals recorded by torch.profiler over `steps` calls, divided by
+    `steps` (host time, gaps between kernels, excluded).  None if the
+    profiler records no device activity here."""
+    import torch
+    from torch.autograd import DeviceType
+    from torch.profiler import ProfilerActivity, profile
+    try:
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+        iv = sorted((e.time_range.start, e.time_range.end) for e in prof.events()
+                    if e.device_type == DeviceType.CUDA and e.time_range.end > e.time_range.start)
+    except Exception as exc:  # the profiler is a measurement aid, not the product
+        log(f"gpu_busy_ms: torch.profiler failed ({exc!r})")
+        return None
+    if not iv:
+        return None
+    tot, cs, ce = 0.0, iv[0][0], iv[0][1]
+    for a, b in iv[1:]:
+        if a > ce:
+            tot += ce - cs
+            cs, ce = a, b
+        else:
+            ce = max(ce, b)
+    tot += ce - cs
+    return tot / 1e3 / steps  # time_range is in microseconds
 
 
 def cfg5_bench(steps: int) -> dict:
@@ -98,15 +147,20 @@ def cfg5_bench(steps: int) -> dict:
     tokens; 5 warmup steps (the reference harness's default,
     benchmark_training_throughput.py:135), then `steps` timed steps; peak
     memory over the timed steps (the method of
-    benchmark_training_throughput.py:51-114 and benchmark_memory.py:51-107).  Attention, norms and embeddings are stock
-    PyTorch; the FFN is this build's."""
+    benchmark_training_throughput.py:51-114 and benchmark_memory.py:51-107).
+    Attention, norms and embeddings are stock PyTorch; the FFN is this
+    build's.  Beside the wall-clock step: the GPU-busy time of a step (the
+    step is partly host-bound at this size, so the wall clock does not
+    separate the two FFNs), the model's algorithmic FLOP over both, and one
+    FFN layer of the step's shape timed on its own."""
     import torch
     from moc_amd import PRESETS, build_model
     from dataclasses import replace
     out = {}
+    cfg = replace(PRESETS["350m"], vocab_size=32100, max_seq_len=256)
+    flop = cfg5_model_flop(cfg, 16, 256)
     for ffn_type in ("moc_gcp", "dense"):
         torch.manual_seed(1234)
-        cfg = replace(PRESETS["350m"], vocab_size=32100, max_seq_len=256)
         model = build_model(cfg, ffn_type=ffn_type).to("cuda", torch.bfloat16)
         opt = torch.optim.AdamW(model.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0,
                                 fused=False)
@@ -130,13 +184,55 @@ def cfg5_bench(steps: int) -> dict:
             loss = step().detach()
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
-        out[ffn_type] = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),
-                         "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 3),
-                         "loss_first": round(float(loss0), 4), "loss_last": round(float(loss), 4)}
+        peak = torch.cuda.max_memory_allocated()
+        busy = gpu_busy_ms(step)
+        tf = flop / dt / 1e12
+        res = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),
+               "peak_mem_gib": round(peak / 2**30, 3),
+               "loss_first": round(float(loss0), 4), "loss_last": round(float(loss), 4),
+               "gpu_busy_ms_per_step": None if busy is None else round(busy, 2),
+               "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                            "algorithmic_tflop_per_step": round(flop / 1e12, 3)}}
+        if busy is not None:
+            tfb = flop / (busy * 1e-3) / 1e12
+            res["roofline"]["gpu_busy"] = {"achieved": round(tfb, 1),
+                                           "frac": round(tfb / BF16_PEAK_TFLOPS, 4)}
+        out[ffn_type] = res
         log(f"cfg5 {ffn_type}: {out[ffn_type]}")
         del model, opt
         torch.cuda.empty_cache()
+    out["ffn_layer"] = cfg5_ffn_layer()
+    log(f"cfg5 ffn layer: {out['ffn_layer']}")
     return out
+
+
+def cfg5_ffn_layer(steps: int = 20, warmup: int = 5) -> dict:
+    """One FFN layer of config 5's shape (16 x 256 tokens, d 1024, I 2736,
+    K 512), fwd+bwd on its own: moc_gcp (this build) against the dense
+    SwiGLU FFN (stock PyTorch, hipBLASLt), same seeded inputs; the nine
+    dense-equivalent GEMMs' FLOP over the step."""
+    import torch
+    from moc_amd import build_ffn
+    t, d, inter, k = 16 * 256, 1024, 2736, 512
+    x, wg, wu, wd, go = seeded_inputs(t, d, inter)
+    xd = x.reshape(16, 256, d).cuda().requires_grad_(True)
+    god = go.reshape(16, 256, d).cuda()
+    flop = 9 * 2.0 * t * d * inter
+    res = {}
+    for ffn_type in ("moc_gcp", "dense"):
+        m = build_ffn(d, inter, ffn_type, k=k).to("cuda", torch.bfloat16).train()
+        with torch.no_grad():
+            for p_, w in zip((m.gate_proj.weight, m.up_proj.weight, m.down_proj.weight), (wg, wu, wd)):
+                p_.copy_(w)
+        ms, f, b = time_train_layer(m, xd, god, steps, warmup)
+        tf = flop / (ms * 1e-3) / 1e12
+        res[ffn_type] = {"us": round(ms * 1e3, 1), "fwd_us": round(f["median"] * 1e3, 1),
+                         "bwd_us": round(b["median"] * 1e3, 1), "achieved": round(tf, 1),
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        del m
+    res["algorithmic_gflop"] = round(flop / 1e9, 1)
+    return res
 
 
 def pmc_target(which: str) -> None:
@@ -180,6 +276,17 @@ def pmc_target(which: str) -> None:
         for _ in range(3):
             for wg, wu, wdt in layers:
                 K.global_decode(x, wg, wu, wdt, K1B, workspace=ws, out=y)
+    elif which == "topk":
+        # the 1b layer's selection: G = X Wg^T of the bench input (one GEMM
+        # launch first), then the row Top-K three times, as the layer calls it
+        x, wg, _, _, _ = seeded_inputs(BATCH1B * SEQ1B, D1B, I1B)
+        g = K.padded_empty(x.shape[0], I1B, torch.bfloat16, "cuda")
+        K.linear(x.cuda(), wg.cuda(), out=g)
+        for _ in range(3):
+            K.topk_rows(g, K1B, idx_dtype=torch.int16)
+        torch.cuda.synchronize()
+        log("pmc target topk: 3 Top-K launches done")
+        return
     elif which in ("down28", "down28_dense"):
         # config 4's Down: 4096 tokens, the 1b shape padded to 5464 channels;
         # the 2:4-packed selection on the structured-sparse MFMA, or the same
@@ -896,10 +1003,12 @@ def main():
     m = build_layer(D1B, I1B, K1B, [w.cuda() for w in ws])
     xd = x.reshape(BATCH1B, SEQ1B, D1B).cuda().requires_grad_(True)
     god = go.reshape(BATCH1B, SEQ1B, D1B).cuda()
-    rec, starts = [], []
-    ms_step, fwd, bwd = time_train_layer(m, xd, god, args.steps, args.warmup, probe=rec,
-                                         step_starts=starts)
+    ms_step, fwd, bwd = time_train_layer(m, xd, god, args.steps, args.warmup)
     log(f"fwd+bwd {ms_step:.3f} ms/step (fwd {fwd['median']:.3f}, bwd {bwd['median']:.3f})")
+    # the GEMM launches' in-step time comes from separate probed steps (the
+    # probe adds two timing events per launch, so it stays out of `value`)
+    rec, starts = [], []
+    time_train_layer(m, xd, god, PROBE_STEPS, 1, probe=rec, step_starts=starts)
     inst = in_step_gemm(rec, starts)
     iso = gemm_roofline(t, D1B, I1B, K1B, ws, xd.detach(), god)
     log(f"GEMMs in the timed steps {inst['gemm_ms_per_step']:.3f} ms ({inst['achieved']} TFLOP/s), "
@@ -907,14 +1016,17 @@ def main():
     roof = {"bound": "mfma", "achieved": inst["achieved"], "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": inst["frac"], "traffic": iso.pop("traffic"),
             "traffic_note": iso.pop("traffic_note"), "kernel": iso.pop("kernel"),
-            "method": "algorithmic FLOP of the step's nine GEMMs (7 launches) / the time the GPU spent "
-                      "in them inside the timed steps (union of the launch intervals, timing events "
-                      "on each launch's own stream; per_launch: mean bracketed duration, which "
-                      "includes the slowdown of launches that overlap another stream's); "
-                      "`isolated`: the same launches timed back to back",
+            "method": f"algorithmic FLOP of the step's nine GEMMs (7 launches) / the time the GPU "
+                      f"spent in them inside {PROBE_STEPS} fwd+bwd steps run after the timed ones with "
+                      "every GEMM launch bracketed by timing events on its own stream (union of the "
+                      "launch intervals; per_launch: mean bracketed duration, which includes the "
+                      "slowdown of launches that overlap another stream's); `isolated`: the same "
+                      "launches timed back to back; `layer_step`: the same FLOP over the whole "
+                      "timed fwd+bwd step (`value`)",
             "algorithmic_flop_per_step": inst["algorithmic_flop_per_step"],
             "gemm_ms_per_step": inst["gemm_ms_per_step"], "per_launch": inst["per_launch"],
-            "isolated": {k: iso[k] for k in ("achieved", "frac", "gemm_ms_per_step", "per_launch")}}
+            "isolated": {k: iso[k] for k in ("achieved", "frac", "gemm_ms_per_step", "per_launch")},
+            "layer_step": layer_step_roofline(inst["algorithmic_flop_per_step"], ms_step)}
     gath = gather_report(xd.detach(), m.gate_proj.weight.detach(), K1B)
     log(f"gather report: union share {gath['union_share_of_channels']}")
     del m, xd, god
@@ -972,6 +1084,13 @@ def main():
         "device": torch.cuda.get_device_name(0),
     }
     print(json.dumps(out), flush=True)
+
+
+def layer_step_roofline(flop: float, ms_step: float) -> dict:
+    """The step's GEMM FLOP over the whole fwd+bwd step time (Top-K, sparse
+    aux kernels and stream joins included)."""
+    tf = flop / (ms_step * 1e-3) / 1e12
+    return {"achieved": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4), "ms": round(ms_step, 4)}
 
 
 def summarize_round(s):

@@ -343,8 +343,12 @@ int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void
  * device memory (code under HIP graph capture without an allocator, tight
  * serving loops).  The workspace is the library's fixed device scratch array
  * of MOC_NOALLOC_SCRATCH_BYTES per GPU; shapes that need more are rejected
- * (MOC_ERR_INVALID).  The stream must belong to the current device.  All
- * calls on one GPU share its array: calls that overlap on one GPU race. */
+ * (MOC_ERR_INVALID).  The stream must belong to the current device.  The
+ * first call on a device clears the array's counters and waits for the clear
+ * (so later calls on any stream find them zero); it must not be made under
+ * HIP graph capture (MOC_ERR_INVALID), later calls may be captured and
+ * replayed.  All calls on one GPU share its array: calls that overlap on one
+ * GPU race. */
 int moc_global_after_gate_noalloc_bf16(const void* x, const void* gate_scores, int64_t nb,
                                        int64_t inter, int64_t hidden, const void* w_up,
                                        const void* w_down_t, int64_t k, const void* residual,

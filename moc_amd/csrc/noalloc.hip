@@ -4,10 +4,14 @@
 // is only a stand-in: the array's device address on a GPU comes from
 // hipGetSymbolAddress, taken once per device with that device current, and
 // only that address is handed to kernels.  Layout as the caller workspace of
-// moc_global_after_gate_bf16: arrival counters (cleared once when the device's
-// address is taken; every call leaves them zero), partial sums, dense U.
+// moc_global_after_gate_bf16: arrival counters, partial sums, dense U.  The
+// counters are cleared once, by the first call on a device, which then waits
+// for the clear to finish before it goes on (so every later call, on any
+// stream, finds them zero; every call leaves them zero).  That first call must
+// therefore not be made while its stream is being captured into a HIP graph:
+// it returns an error instead; calls after it may be captured and replayed.
 // Every call on a GPU shares that GPU's array, so calls that overlap on one
-// GPU (two streams, two threads) race.
+// GPU (two streams, two threads, graph replays beside eager calls) race.
 
 #include <mutex>
 
@@ -50,9 +54,27 @@ int scratch_of_current_device(void** out, void* stream) {
                 hipGetErrorString(e));
       return MOC_ERR_HIP;
     }
-    // the arrival counters must be zero before the first call
+    // the arrival counters must be zero before the first call: cleared on
+    // this stream and waited for, so that no later call on another stream
+    // can run ahead of the clear (and never recorded into a graph)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(as_stream(stream), &cap);
+    if (e != hipSuccess) {
+      set_error("moc_global_after_gate_noalloc_bf16: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+      return MOC_ERR_HIP;
+    }
+    MOC_REQUIRE(cap == hipStreamCaptureStatusNone,
+                "moc_global_after_gate_noalloc_bf16: the first call on a device clears the scratch "
+                "counters and waits for it, so it cannot run under HIP graph capture; make one call "
+                "outside the capture first");
     const int rc = moc_fill_zero(p, kAfterGateCounterBytes, stream);
     if (rc != MOC_OK) return rc;
+    e = hipStreamSynchronize(as_stream(stream));
+    if (e != hipSuccess) {
+      set_error("moc_global_after_gate_noalloc_bf16: waiting for the scratch clear failed: %s",
+                hipGetErrorString(e));
+      return MOC_ERR_HIP;
+    }
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];

@@ -74,14 +74,17 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         # freeze_for_compile(): the [inter, hidden] copy of W_down that the
         # selected Down kernels stream row by row (with the weight version it
         # was made from), flat channel offsets of the 2:8 groups for the
-        # masked reference, and the after-gate kernel's workspaces (one per
-        # batch size, owned by this module so that a HIP graph captured with
-        # one never sees it freed or shared with another module).
+        # masked reference, the decode kernels' workspaces (one per batch
+        # size of at most 16 tokens, owned by this module so that a HIP graph
+        # captured with one never sees it freed or shared with another
+        # module), and the 2:8 prefill buffers (one grow-only set per device).
         self._down_weight_t: torch.Tensor | None = None
         self._down_weight_t_key: tuple | None = None
         self._group_offsets: dict = {}
         self._after_gate_ws: dict = {}
+        self._decode_ws: dict = {}
         self._packed28: dict = {}
+        self._packed28_captured: list = []
         self._compile_frozen: bool = False
 
     # -- derived state (the caches of inference_ffn.py:78-129)
@@ -117,17 +120,41 @@ class InferenceMoCSwiGLUFFN(nn.Module):
             self._after_gate_ws[(device, nb)] = ws
         return ws
 
-    def _packed28_state(self, nb: int, device: torch.device):
-        """This module's 2:4-packed operand buffers and zeroed Down workspace
-        for nb tokens (MoC 2:8 prefill)."""
-        st = self._packed28.get((device, nb))
-        if st is None:
+    def _global_decode_workspace(self, nb: int, device: torch.device) -> torch.Tensor:
+        """This module's zeroed gate GEMV + after-gate workspace for nb <= 16
+        tokens."""
+        ws = self._decode_ws.get((device, nb))
+        if ws is None:
             c = self.config
-            ap, meta = K.packed28_buffers(nb, c.intermediate_size, device)
-            ws = K.sparse28_down_workspace(nb, c.intermediate_size, c.hidden_size, device)
-            st = (ap, meta, ws)
-            self._packed28[(device, nb)] = st
-        return st
+            ws = K.global_decode_workspace(nb, c.intermediate_size, c.k, c.hidden_size, device)
+            self._decode_ws[(device, nb)] = ws
+        return ws
+
+    def _packed28_state(self, nb: int, device: torch.device):
+        """Row views for nb tokens of this module's 2:4-packed operand
+        buffers and zeroed sparse-Down workspace (MoC 2:8 prefill).  One set
+        per device, sized for the largest batch seen so far (rounded up to
+        256 rows, the positions' row block) and replaced only when a larger
+        batch comes; a set used while a HIP graph was being captured is kept
+        alive when it is replaced (the graph still uses it)."""
+        st = self._packed28.get(device)
+        c = self.config
+        if st is None or st["rows"] < nb:
+            if st is not None and st["captured"]:
+                self._packed28_captured.append(st)
+            rows = K.round_up(max(nb, 1), 256)
+            ap, meta = K.packed28_buffers(rows, c.intermediate_size, device)
+            ws = K.sparse28_down_workspace(rows, c.intermediate_size, c.hidden_size, device)
+            st = {"rows": rows, "ap": ap, "meta": meta, "ws": ws, "captured": False}
+            self._packed28[device] = st
+        need = K.sparse28_down_workspace_bytes(nb, c.intermediate_size, c.hidden_size)
+        if st["ws"].numel() < need:
+            if st["captured"]:
+                self._packed28_captured.append(dict(st))
+            st["ws"] = K.sparse28_down_workspace(nb, c.intermediate_size, c.hidden_size, device)
+        if torch.cuda.is_current_stream_capturing():
+            st["captured"] = True
+        return st["ap"][:nb], st["meta"], st["ws"]
 
     def freeze_for_compile(self, device: torch.device | None = None) -> None:
         """Build the derived state now and stop updating it inside forward."""
@@ -192,7 +219,8 @@ class InferenceMoCSwiGLUFFN(nn.Module):
             # the gate GEMV and the after-gate kernel through one layer
             # entry (same results as the two steps below)
             y = K.global_decode(x_2d, self.gate_proj.weight, self.up_proj.weight,
-                                self._down_weight_t, self.config.k)
+                                self._down_weight_t, self.config.k,
+                                workspace=self._global_decode_workspace(x_2d.shape[0], x_2d.device))
             return self._restore_output_shape(y, shp)
         if x_2d.shape[0] <= 16:
             gate_full = K.gemv(x_2d, self.gate_proj.weight)

@@ -284,8 +284,43 @@ def _operand(t: torch.Tensor, bf16: bool) -> tuple[torch.Tensor, int, int]:
     return tt, (tt.stride(0) if r > 1 else round_up(max(c, 1), 8)), 1
 
 
+# Per-stream workspaces (GEMM fix-up/split-K partials, decode partial sums).
+# Both start with arrival counters that must be zero when a kernel starts and
+# that every kernel leaves zero, so a buffer is created zeroed and reused
+# without clearing; one buffer per (device, stream) keeps kernels that run
+# concurrently on different streams apart.
+_STREAM_WS_LIMIT = 8        # cached streams per device and cache; the oldest goes first
 _GEMM_WS: dict = {}
-_GEMM_WS_RETIRED: list = []
+_WS_CACHE: dict = {}
+# buffers a captured HIP graph still uses: kept alive until the process ends
+# (one per captured buffer that was later outgrown or evicted)
+_WS_CAPTURED: list = []
+
+
+def _stream_workspace(cache: dict, device, nbytes: int, minimum: int = 1) -> torch.Tensor:
+    """The zeroed workspace of the current stream on `device` from `cache`,
+    grown on demand.  A buffer handed out during a HIP graph capture is
+    marked: when it is outgrown or evicted it is kept alive (the graph keeps
+    writing to it on every replay); any other outgrown buffer is freed (the
+    caching allocator orders its reuse after the work queued on its
+    stream).  At most _STREAM_WS_LIMIT streams per device keep a buffer."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ent = cache.pop(key, None)  # re-inserted below: the dict's order is least-recent first
+    if ent is None or ent[0].numel() < nbytes:
+        if ent is not None and ent[1]:
+            _WS_CAPTURED.append(ent[0])
+        ent = [torch.zeros((max(nbytes, minimum),), dtype=torch.uint8, device=device), False]
+    if torch.cuda.is_current_stream_capturing():
+        ent[1] = True
+    cache[key] = ent
+    same_dev = [k for k in cache if k[0] == device.index]
+    for old in same_dev[:max(0, len(same_dev) - _STREAM_WS_LIMIT)]:
+        gone = cache.pop(old)
+        if gone[1]:
+            _WS_CAPTURED.append(gone[0])
+    return ent[0]
+
 
 # Optional timing probe: when a list is installed with set_gemm_probe(), every
 # GEMM launch made through gemm() / linear_pair() is bracketed by two timing
@@ -317,22 +352,9 @@ def _probe_end(ev, name: str, flop: float) -> None:
 
 
 def _gemm_workspace(device, nbytes: int) -> torch.Tensor:
-    """The GEMM workspace of the current stream on `device`, grown on demand.
-    Its first 4 KB hold arrival counters that must be zero when a GEMM starts
-    and that every GEMM leaves zero, so the buffer is created zeroed and then
-    reused without clearing; one buffer per stream keeps GEMMs that run
-    concurrently on different streams apart.  An outgrown buffer is kept
-    alive, not freed, as the decode workspace is."""
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    ws = _GEMM_WS.get(key)
-    if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            # kept alive, not freed: a HIP graph captured with it keeps
-            # writing to it on every replay
-            _GEMM_WS_RETIRED.append(ws)
-        ws = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
-        _GEMM_WS[key] = ws
-    return ws
+    """The GEMM workspace of the current stream on `device` (its first 4 KB
+    hold the fix-up's arrival counters), grown on demand."""
+    return _stream_workspace(_GEMM_WS, device, nbytes)
 
 
 def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
@@ -504,25 +526,10 @@ def global_after_gate_workspace_bytes(nb: int, inter: int, k: int, hidden: int) 
     return N.query("moc_global_after_gate_workspace_size", nb, inter, int(k), hidden)
 
 
-_WS_CACHE: dict = {}
-_WS_RETIRED: list = []
-
-
 def _decode_workspace(device, nbytes: int) -> torch.Tensor:
     """The after-gate workspace of the current stream on `device`, grown on
-    demand.  The kernel's arrival counters must start at zero and every call
-    leaves them zero, so a buffer is created zeroed and then reused without
-    clearing.  One buffer per stream keeps calls on different streams apart.
-    A buffer that is outgrown is kept alive, not freed: a HIP graph captured
-    with it keeps writing to it on every replay."""
-    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
-    ws = _WS_CACHE.get(key)
-    if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            _WS_RETIRED.append(ws)
-        ws = torch.zeros((max(nbytes, 256),), dtype=torch.uint8, device=device)
-        _WS_CACHE[key] = ws
-    return ws
+    demand (callers without a workspace of their own: the moc_native op)."""
+    return _stream_workspace(_WS_CACHE, device, nbytes, minimum=256)
 
 
 def global_after_gate_workspace(nb: int, inter: int, k: int, hidden: int, device) -> torch.Tensor:
@@ -672,16 +679,29 @@ def grouped_top2_up_silu_packed(x, gate_weight, up_weight, ap, meta) -> None:
     if wg.shape != wu.shape or wg.shape[1] != hidden:
         raise ValueError(f"H mismatch: x={tuple(x.shape)}, gate={tuple(wg.shape)}, up={tuple(wu.shape)}")
     nt, ld_ap, meta_rows = packed28_layout(nb, inter)
-    if ap.shape != (nb, ld_ap) or meta.shape != (nt, meta_rows, 2):
-        raise ValueError("packed buffers do not match packed28_layout")
+    _check_packed28(ap, meta, nb, nt, ld_ap, meta_rows)
     N.call("moc_grouped_top2_up_silu_packed_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(),
-           wu.data_ptr(), inter, ap.data_ptr(), ld_ap, meta.data_ptr(), meta_rows, N.stream_of(x))
+           wu.data_ptr(), inter, ap.data_ptr(), ld_ap, meta.data_ptr(), meta.shape[1], N.stream_of(x))
+
+
+def _check_packed28(ap, meta, nb: int, nt: int, ld_ap: int, meta_rows: int) -> None:
+    """ap: [nb, ld_ap] rows (a row view of a larger buffer is fine); meta:
+    [nt, R, 2] with R >= meta_rows (the tile stride may be a larger
+    batch's)."""
+    if (ap.shape != (nb, ld_ap) or ap.stride() != (ld_ap, 1) or meta.dim() != 3
+            or meta.shape[0] != nt or meta.shape[2] != 2 or meta.shape[1] < meta_rows
+            or meta.shape[1] % 256 or not meta.is_contiguous()):
+        raise ValueError("packed buffers do not match packed28_layout")
+
+
+def sparse28_down_workspace_bytes(nb: int, inter: int, hidden: int) -> int:
+    return N.query("moc_sparse28_down_workspace_size", nb, inter, hidden)
 
 
 def sparse28_down_workspace(nb: int, inter: int, hidden: int, device) -> torch.Tensor:
     """A zeroed workspace for sparse28_down (its counters start at zero and
     every call leaves them zero, so it is reused without clearing)."""
-    b = N.query("moc_sparse28_down_workspace_size", nb, inter, hidden)
+    b = sparse28_down_workspace_bytes(nb, inter, hidden)
     return torch.zeros((max(b, 1),), dtype=torch.uint8, device=device)
 
 
@@ -695,13 +715,14 @@ def sparse28_down(ap, meta, inter: int, down_weight_t, *, workspace, out=None) -
         raise ValueError("down_weight_t must be a bf16 [inter, hidden] tensor")
     hidden = wdt.shape[1]
     nt, ld_ap, meta_rows = packed28_layout(nb, inter)
+    _check_packed28(ap, meta, nb, nt, ld_ap, meta_rows)
     y = _empty((nb, hidden), torch.bfloat16, ap.device) if out is None else out
     if y.shape != (nb, hidden) or not y.is_contiguous():
         raise ValueError(f"out shape must be ({nb},{hidden})")
     ws_bytes = N.query("moc_sparse28_down_workspace_size", nb, inter, hidden)
     if workspace.numel() < ws_bytes:
         raise ValueError(f"sparse28_down needs a workspace of {ws_bytes} bytes")
-    N.call("moc_sparse28_down_bf16", ap.data_ptr(), ld_ap, meta.data_ptr(), meta_rows, nb, inter,
+    N.call("moc_sparse28_down_bf16", ap.data_ptr(), ld_ap, meta.data_ptr(), meta.shape[1], nb, inter,
            wdt.data_ptr(), wdt.stride(0), 0, hidden, y.data_ptr(), y.stride(0), workspace.data_ptr(),
            ws_bytes, N.stream_of(ap))
     return y

@@ -56,29 +56,8 @@ def torch_from_bf16_bits(bits: np.ndarray) -> torch.Tensor:
 
 
 # --------------------------------------------------------------- order keys
-def order_keys(scores) -> np.ndarray:
-    """Unsigned keys whose order is the numeric order of the scores.
-
-    bf16 tensors give 16-bit keys, float32 tensors 32-bit keys, following the
-    sign-flip encoding of bf16_order_key (optimized_global_moc_ext.cu:26-29)
-    with -0 folded onto +0 and NaN mapped to the largest key."""
-    if isinstance(scores, torch.Tensor):
-        if scores.dtype == torch.bfloat16:
-            bits = torch_bf16_bits(scores).astype(np.uint32)
-            nbits = 16
-        elif scores.dtype == torch.float32:
-            bits = scores.detach().cpu().contiguous().numpy().view(np.uint32).astype(np.uint32)
-            nbits = 32
-        else:
-            raise ValueError(f"unsupported dtype {scores.dtype}")
-    else:
-        arr = np.asarray(scores)
-        if arr.dtype == np.uint16:
-            bits, nbits = arr.astype(np.uint32), 16
-        elif arr.dtype == np.float32:
-            bits, nbits = arr.view(np.uint32).astype(np.uint32), 32
-        else:
-            raise ValueError(f"unsupported array dtype {arr.dtype}")
+def _keys_from_bits(bits: np.ndarray, nbits: int) -> np.ndarray:
+    """Order keys of raw IEEE bit patterns of width nbits (16: bf16, 32: f32)."""
     sign = np.uint32(1 << (nbits - 1))
     full = np.uint32((1 << nbits) - 1)
     expmask = np.uint32(((1 << (nbits - 1)) - 1))
@@ -87,6 +66,31 @@ def order_keys(scores) -> np.ndarray:
     keys = np.where(bits & sign, (~bits) & full, bits | sign).astype(np.uint32)
     keys = np.where((bits & expmask) > inf, full, keys)
     return keys.astype(np.uint32)
+
+
+# the key of every bf16 bit pattern: a bf16 tensor's keys are one table lookup
+_BF16_KEYS = _keys_from_bits(np.arange(1 << 16, dtype=np.uint32), 16)
+
+
+def order_keys(scores) -> np.ndarray:
+    """Unsigned keys whose order is the numeric order of the scores.
+
+    bf16 tensors give 16-bit keys, float32 tensors 32-bit keys, following the
+    sign-flip encoding of bf16_order_key (optimized_global_moc_ext.cu:26-29)
+    with -0 folded onto +0 and NaN mapped to the largest key."""
+    if isinstance(scores, torch.Tensor):
+        if scores.dtype == torch.bfloat16:
+            return _BF16_KEYS[torch_bf16_bits(scores)]
+        if scores.dtype == torch.float32:
+            bits = scores.detach().cpu().contiguous().numpy().view(np.uint32).astype(np.uint32)
+            return _keys_from_bits(bits, 32)
+        raise ValueError(f"unsupported dtype {scores.dtype}")
+    arr = np.asarray(scores)
+    if arr.dtype == np.uint16:
+        return _BF16_KEYS[arr]
+    if arr.dtype == np.float32:
+        return _keys_from_bits(arr.view(np.uint32).astype(np.uint32), 32)
+    raise ValueError(f"unsupported array dtype {arr.dtype}")
 
 
 def silu_abs_scores(g: torch.Tensor) -> torch.Tensor:
@@ -101,14 +105,26 @@ def topk_indices(scores: torch.Tensor, k: int) -> np.ndarray:
 
     Follows torch.topk(g, k, dim=-1, largest=True, sorted=False)
     (moc/ffn.py:144,392; inference_ffn.py:147-153) with the stable-descending
-    tie rule of the CUB kernel (optimized_global_moc_ext.cu:59-82)."""
+    tie rule of the CUB kernel (optimized_global_moc_ext.cu:59-82): the first
+    k of a stable sort by descending key.  That set is every key above the
+    row's k-th largest key plus, of the keys equal to it, the ones of lowest
+    channel index; it is formed that way here (a partition finds the k-th
+    key), in blocks of rows, so that rows of a full training batch take
+    seconds instead of a full sort each."""
     keys = order_keys(scores.reshape(-1, scores.shape[-1]))
     rows, inter = keys.shape
     if not 1 <= k <= inter:
         raise ValueError(f"k={k} must be in [1, {inter}]")
-    # stable sort of -key keeps equal keys in ascending index order
-    order = np.argsort(-(keys.astype(np.int64)), axis=1, kind="stable")[:, :k]
-    return np.sort(order, axis=1).astype(np.int64)
+    out = np.empty((rows, k), dtype=np.int64)
+    for r0 in range(0, rows, 1024):
+        kb = keys[r0:r0 + 1024]
+        kth = np.partition(kb, inter - k, axis=1)[:, inter - k][:, None]
+        above = kb > kth
+        tied = kb == kth
+        need = (k - above.sum(axis=1, dtype=np.int64))[:, None]
+        take = above | (tied & (np.cumsum(tied, axis=1, dtype=np.int32) <= need))
+        out[r0:r0 + 1024] = np.nonzero(take)[1].reshape(-1, k)
+    return out
 
 
 def topk_mask(idx: np.ndarray, inter: int) -> np.ndarray:

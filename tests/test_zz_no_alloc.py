@@ -83,3 +83,39 @@ def test_noalloc_matches_workspace_entry_point():
             assert torch.equal(io, io_ref), f"selection differs at nb={nb}"
             assert torch.equal(y, y_ref), f"y differs at nb={nb}"
             assert int(io.min()) >= 0
+
+
+@pytest.mark.gpu
+def test_noalloc_captured_in_graph_matches_workspace_entry_point():
+    """The entry point captured in a HIP graph (after an eager first call,
+    which clears the scratch counters), replayed three times with new inputs
+    copied into the captured buffers and eager calls of the workspace entry
+    point between the replays: every replay equals that entry point on the
+    same input bit for bit (output and selection)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    N.load()
+    d, inter, k, nb = 2048, 5461, 1024, 4
+    x, gate, wu, wdt, res = _inputs(nb, d, inter, 950)
+    _no_alloc(x, gate, wu, wdt, k, res)  # the first call on the device is eager
+    torch.cuda.synchronize()
+    xs, gs, rs = x.clone(), gate.clone(), res.clone()
+    y = torch.empty(nb, d, dtype=torch.bfloat16, device=DEV)
+    io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):  # captures on torch's own capture stream
+        N.call("moc_global_after_gate_noalloc_bf16", xs.data_ptr(), gs.data_ptr(), nb, inter, d,
+               wu.data_ptr(), wdt.data_ptr(), k, rs.data_ptr(), y.data_ptr(), io.data_ptr(),
+               N.stream_of(xs))
+    for rep in range(3):
+        xn, gn, _, _, rn = _inputs(nb, d, inter, 960 + rep)
+        xs.copy_(xn)
+        gs.copy_(gn)
+        rs.copy_(rn)
+        print(f"[no-alloc] graph replay {rep}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        y_ref, io_ref = _with_workspace(xn, gn, wu, wdt, k, rn)
+        torch.cuda.synchronize()
+        assert torch.equal(io, io_ref), f"selection differs on replay {rep}"
+        assert torch.equal(y, y_ref), f"y differs on replay {rep}"
