@@ -74,6 +74,10 @@ def parse_args():
                    help="only the 350m-model training step (config 5): tokens/s and peak "
                         "memory, moc_gcp vs dense, one JSON line")
     p.add_argument("--cfg5-steps", type=int, default=10)
+    p.add_argument("--no-gpu-busy", action="store_true",
+                   help="skip config 5's GPU-only timing (steps queued behind a sleep kernel)")
+    p.add_argument("--cfg5-row", choices=["moc_gcp", "dense", "moc_gcp_unfused"], default=None,
+                   help="with --cfg5: only this row, and no FFN-layer timing (for kernel traces)")
     p.add_argument("--only", choices=["cfg1", "cfg2", "cfg4"], default=None,
                    help="run one config's GPU leg alone (for kernel traces) and print its JSON")
     p.add_argument("--decode-e2e", action="store_true",
@@ -109,38 +113,35 @@ def cfg5_model_flop(cfg, batch: int, seq: int) -> float:
     return 3.0 * fwd
 
 
-def gpu_busy_ms(step, steps: int = 3):
-    """GPU-busy time per call of step(): the union of the device kernel and
-    copy intervals recorded by torch.profiler over `steps` calls, divided by
-    `steps` (host time, gaps between kernels, excluded).  None if the
-    profiler records no device activity here."""
+def gpu_only_ms(step, host_ms: float, n: int = 5):
+    """GPU time per call of step() with the host out of the loop: a bounded
+    sleep kernel holds the stream while the host queues n calls, so the GPU
+    then runs them back to back; the time between events around the n calls
+    is pure GPU time (kernels and the gaps the GPU itself needs between
+    them).  Returns (ms per call, True) if the host had queued all n calls
+    before the GPU reached them, else (ms, False): the host did not keep
+    ahead and the number includes host time."""
     import torch
-    from torch.autograd import DeviceType
-    from torch.profiler import ProfilerActivity, profile
-    try:
-        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
-            for _ in range(steps):
-                step()
-            torch.cuda.synchronize()
-        iv = sorted((e.time_range.start, e.time_range.end) for e in prof.events()
-                    if e.device_type == DeviceType.CUDA and e.time_range.end > e.time_range.start)
-    except Exception as exc:  # the profiler is a measurement aid, not the product
-        log(f"gpu_busy_ms: torch.profiler failed ({exc!r})")
-        return None
-    if not iv:
-        return None
-    tot, cs, ce = 0.0, iv[0][0], iv[0][1]
-    for a, b in iv[1:]:
-        if a > ce:
-            tot += ce - cs
-            cs, ce = a, b
-        else:
-            ce = max(ce, b)
-    tot += ce - cs
-    return tot / 1e3 / steps  # time_range is in microseconds
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    torch.cuda._sleep(1 << 22)
+    b.record()
+    torch.cuda.synchronize()
+    cycles_per_ms = (1 << 22) / max(a.elapsed_time(b), 1e-3)
+    hold = int(cycles_per_ms * (2.0 * n * host_ms + 100.0))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(hold)
+    e0.record()
+    for _ in range(n):
+        step()
+    e1.record()
+    ahead = not e0.query()  # the GPU was still asleep when the last call was queued
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n, ahead
 
 
-def cfg5_bench(steps: int) -> dict:
+def cfg5_bench(steps: int, gpu_busy: bool = True, only: str | None = None) -> dict:
     """Config 5: a 350m LLaMA training step (24 layers, d=1024, I=2736,
     K=512), bf16 parameters, AdamW (0.9/0.999, wd 0, fused=False, lr 1e-3),
     tokens [16, 256] uniform over the 32100-token vocabulary with labels =
@@ -149,17 +150,25 @@ def cfg5_bench(steps: int) -> dict:
     memory over the timed steps (the method of
     benchmark_training_throughput.py:51-114 and benchmark_memory.py:51-107).
     Attention, norms and embeddings are stock PyTorch; the FFN is this
-    build's.  Beside the wall-clock step: the GPU-busy time of a step (the
-    step is partly host-bound at this size, so the wall clock does not
-    separate the two FFNs), the model's algorithmic FLOP over both, and one
-    FFN layer of the step's shape timed on its own."""
+    build's.  Beside the wall-clock step: the GPU-only time of a step (steps
+    queued behind a sleep kernel, so host time drops out: at this size the
+    host's launch time is close to the GPU's work, and the wall clock mixes
+    both), the model's algorithmic FLOP over both, and one FFN layer of the
+    step's shape timed on its own.  Rows: moc_gcp (the FFN's pre-norm and
+    residual add fused around it), dense, and moc_gcp with that fusion
+    switched off."""
     import torch
     from moc_amd import PRESETS, build_model
     from dataclasses import replace
     out = {}
     cfg = replace(PRESETS["350m"], vocab_size=32100, max_seq_len=256)
     flop = cfg5_model_flop(cfg, 16, 256)
-    for ffn_type in ("moc_gcp", "dense"):
+    from moc_amd import ffn as F
+    for row in ("moc_gcp", "dense", "moc_gcp_unfused") if only is None else (only,):
+        # moc_gcp_unfused: the same model with the FFN's pre-norm and residual
+        # add as stock PyTorch ops around the FFN (the fusion switched off)
+        ffn_type = "moc_gcp" if row == "moc_gcp_unfused" else row
+        F.FUSE_BLOCK_FFN = row != "moc_gcp_unfused"
         torch.manual_seed(1234)
         model = build_model(cfg, ffn_type=ffn_type).to("cuda", torch.bfloat16)
         opt = torch.optim.AdamW(model.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=0.0,
@@ -185,23 +194,28 @@ def cfg5_bench(steps: int) -> dict:
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         peak = torch.cuda.max_memory_allocated()
-        busy = gpu_busy_ms(step)
+        busy, ahead = gpu_only_ms(step, dt * 1e3) if gpu_busy else (None, False)
+        if not ahead:
+            busy = None
         tf = flop / dt / 1e12
         res = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),
                "peak_mem_gib": round(peak / 2**30, 3),
                "loss_first": round(float(loss0), 4), "loss_last": round(float(loss), 4),
-               "gpu_busy_ms_per_step": None if busy is None else round(busy, 2),
+               "gpu_only_ms_per_step": None if busy is None else round(busy, 2),
                "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                             "algorithmic_tflop_per_step": round(flop / 1e12, 3)}}
         if busy is not None:
             tfb = flop / (busy * 1e-3) / 1e12
-            res["roofline"]["gpu_busy"] = {"achieved": round(tfb, 1),
+            res["roofline"]["gpu_only"] = {"achieved": round(tfb, 1),
                                            "frac": round(tfb / BF16_PEAK_TFLOPS, 4)}
-        out[ffn_type] = res
-        log(f"cfg5 {ffn_type}: {out[ffn_type]}")
+        out[row] = res
+        log(f"cfg5 {row}: {out[row]}")
         del model, opt
         torch.cuda.empty_cache()
+    F.FUSE_BLOCK_FFN = True
+    if only is not None:
+        return out
     out["ffn_layer"] = cfg5_ffn_layer()
     log(f"cfg5 ffn layer: {out['ffn_layer']}")
     return out
@@ -991,7 +1005,8 @@ def main():
         return
     if args.cfg5:
         print(json.dumps({"config": "350m LLaMA training step (config 5), 16x256 tokens, bf16",
-                          "steps": args.cfg5_steps, "result": cfg5_bench(args.cfg5_steps)}))
+                          "steps": args.cfg5_steps,
+                          "result": cfg5_bench(args.cfg5_steps, not args.no_gpu_busy, args.cfg5_row)}))
         return
     from moc_amd import _native
     _native.load()  # the HIP library must be there: no fallback
@@ -1054,7 +1069,7 @@ def main():
         log("config 4: 2:8 prefill")
         configs["4_moc28_prefill_4096"] = moc28_prefill_bench()
         log("config 5: 350m training step")
-        configs["5_350m_step"] = cfg5_bench(args.cfg5_steps)
+        configs["5_350m_step"] = cfg5_bench(args.cfg5_steps, not args.no_gpu_busy)
         if cpu_on:
             log("cpu baselines of configs 1-5")
             configs["1_60m_moc_fwd_f32"]["cpu_baseline"] = cpu_cfg1()

@@ -182,6 +182,17 @@ int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64
                 void* C, int64_t ldc, int c_dtype, void* workspace, int64_t workspace_bytes,
                 void* stream);
 
+/* C = bf16(bf16(A B) + R) for bf16 A, B, C: moc_gemm_ws (single product,
+ * same strides, workspace rules and results) with the residual R [M, N]
+ * (16-byte aligned rows, ldres a multiple of 8) added where C is written.
+ * The decoder block's residual add around the FFN, x + ffn(ffn_norm(x))
+ * (moc/model.py:85), in the Down projection's epilogue: D is rounded to
+ * bf16 first, then added to R and rounded again, the rounding of the
+ * reference's bf16 add of two bf16 tensors.  C may be R itself. */
+int moc_gemm_residual_bf16(int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm, int64_t a_sk,
+                           const void* B, int64_t b_sk, int64_t b_sn, void* C, int64_t ldc, const void* res,
+                           int64_t ldres, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* C1[M,N1] = A W1^T and C2[M,N2] = A W2^T (bf16) in one launch: A [M,K]
  * row-major (lda), W1 [N1,K] and W2 [N2,K] nn.Linear weights (ldw1, ldw2),
  * C1/C2 row-major (ldc1, ldc2).  The gate and up projections of the MoC FFN
@@ -249,6 +260,61 @@ int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, con
                           void* gg, void* gu, int64_t ld_ggu, int stacked, void* s_tmp, void* dx, int64_t lddx,
                           void* dwg, void* dwu, int64_t ld_dw, void* dwd, int64_t lddwd, int grad_dtype,
                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------- pre-norm and FFN block */
+/* RMSNorm of rows of bf16 activations, the FFN's pre-norm (RMSNorm.forward,
+ * moc/model.py:20-28): r = 1 / sqrt(mean(x^2) + eps) in f32 per row,
+ * y = bf16(bf16(x * r) * w) with w bf16 [d]; rstd (f32 [rows], may be NULL)
+ * receives r.  d a multiple of 8 up to 8192, rows 16-byte aligned. */
+int moc_rmsnorm_rows_bf16(const void* x, int64_t ldx, int64_t rows, int64_t d, const void* w, float eps,
+                          void* y, int64_t ldy, float* rstd, void* stream);
+
+/* Workspace bytes of moc_rmsnorm_backward_bf16 (f32 partial rows of dw). */
+int64_t moc_rmsnorm_backward_workspace_size(int64_t rows, int64_t d);
+
+/* Backward of moc_rmsnorm_rows_bf16 (the autograd of moc/model.py:26-28)
+ * with a second gradient dres reaching x around the norm (the block's
+ * residual branch, moc/model.py:85; NULL: none):
+ *   dx = dres + r (dy w) - (r^3 / d) x sum_j(dy_j w_j x_j)   (bf16 [rows, d])
+ *   dw = sum over rows of dy bf16(x r)                        (dw_dtype [d])
+ * in f32, each rounded once.  dw is summed in a fixed order (no atomics).
+ * d a multiple of 8 up to 4096. */
+int moc_rmsnorm_backward_bf16(const void* x, int64_t ldx, int64_t rows, int64_t d, const void* w,
+                              const float* rstd, const void* dy, int64_t lddy, const void* dres, int64_t ldres,
+                              void* dx, int64_t lddx, void* dw, int dw_dtype, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/* The FFN half of a pre-norm decoder block, out = h + FFN(RMSNorm(h))
+ * (TransformerBlock.forward, moc/model.py:83-86, with the FFN of
+ * moc/ffn.py:124-497), as one call: moc_rmsnorm_rows_bf16 into xn (the
+ * FFN's input, [rows, d] scratch the caller may free afterwards) and rstd,
+ * then moc_ffn_forward_bf16 on xn (same arguments and outputs) with h
+ * added in the Down GEMM's epilogue.  Workspace: that of
+ * moc_ffn_forward_bf16. */
+int moc_ffn_block_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection, const void* h,
+                               int64_t ldh, const void* norm_w, float eps, void* xn, int64_t ldxn, float* rstd,
+                               const void* wg, int64_t ldwg, const void* wu, int64_t ldwu, const void* wd,
+                               int64_t ldwd, void* g, void* u, int64_t ld_gu, void* vals, void* idx, int idx_dtype,
+                               void* u_s, void* s_s, void* z_s, void* out, int64_t ldo, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of moc_ffn_block_backward_bf16. */
+int64_t moc_ffn_block_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu, int stacked);
+
+/* Backward of moc_ffn_block_forward_bf16 given dout: recomputes xn from h
+ * (the forward's row pass, same bits) into xn, runs moc_ffn_backward_bf16
+ * on it (same arguments; its dX lands in xn's buffer), then
+ * moc_rmsnorm_backward_bf16 with dres = dout: dh (bf16 [rows, d]) and the
+ * norm weight's gradient dnorm_w (dnorm_dtype [d]). */
+int moc_ffn_block_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* dout, int64_t ldgo,
+                                const void* h, int64_t ldh, const void* norm_w, float eps, const float* rstd,
+                                void* xn, int64_t ldxn, const void* idx, int idx_dtype, const void* g_s,
+                                const void* u_s, const void* s_s, const void* z_s, const void* wg, int64_t ldwg,
+                                const void* wu, int64_t ldwu, const void* wd, int64_t ldwd, void* zbuf,
+                                int64_t ldz, void* gg, void* gu, int64_t ld_ggu, int stacked, void* s_tmp, void* dh,
+                                int64_t lddh, void* dwg, void* dwu, int64_t ld_dw, void* dwd, int64_t lddwd,
+                                int grad_dtype, void* dnorm_w, int dnorm_dtype, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- decode */
 /* y[b, r] = bf16(sum_h x[b,h] W[r,h]) for b < nb <= 16 tokens: the decode

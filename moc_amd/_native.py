@@ -59,6 +59,21 @@ SIGNATURES: dict[str, tuple] = {
     "moc_gemm_ws": (_int, [_int, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                            _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp, _i64, _vp]),
     "moc_gemm_workspace_size": (_i64, [_int, _i64, _i64, _i64, _i64]),
+    "moc_gemm_residual_bf16": (_int, [_i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                                      _vp, _i64, _vp, _i64, _vp]),
+    "moc_rmsnorm_rows_bf16": (_int, [_vp, _i64, _i64, _i64, _vp, ctypes.c_float, _vp, _i64, _vp, _vp]),
+    "moc_rmsnorm_backward_workspace_size": (_i64, [_i64, _i64]),
+    "moc_rmsnorm_backward_bf16": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
+                                         _i64, _vp, _int, _vp, _i64, _vp]),
+    "moc_ffn_block_forward_bf16": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, ctypes.c_float,
+                                          _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64,
+                                          _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "moc_ffn_block_backward_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _int]),
+    "moc_ffn_block_backward_bf16": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp,
+                                           ctypes.c_float, _vp, _vp, _i64, _vp, _int, _vp, _vp, _vp, _vp,
+                                           _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64,
+                                           _int, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _int, _vp,
+                                           _int, _vp, _i64, _vp]),
     "moc_ffn_forward_workspace_size": (_i64, [_i64, _i64, _i64]),
     "moc_ffn_forward_bf16": (_int, [_i64, _i64, _i64, _i64, _int, _vp, _i64, _vp, _i64, _vp, _i64, _vp,
                                     _i64, _vp, _vp, _i64, _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _vp,

@@ -132,6 +132,11 @@ struct GemmArgs {
   int64_t gu_ld_ap;
   uint32_t* gu_meta;
   int gu_meta_rows, gu_nt;
+  // bf16 output plus a residual: C = bf16(bf16(A B) + R), R [M, N] bf16 with
+  // rows ldres apart (16-byte aligned rows); null: plain C = bf16(A B).  The
+  // decoder block's x + ffn(...) in the Down GEMM's epilogue.
+  const uint16_t* res;
+  int64_t ldres;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -350,6 +355,31 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
+// Eight bf16 values of C (a 16-byte segment) plus the residual's eight at
+// r (n < 8: only the first n are read), each bf16(c + r).
+__device__ __forceinline__ uint4 add_residual8(uint4 v, const uint16_t* r, int n) {
+  uint32_t rw[4];
+  if (n >= 8) {
+    const uint4 t = *reinterpret_cast<const uint4*>(r);
+    rw[0] = t.x;
+    rw[1] = t.y;
+    rw[2] = t.z;
+    rw[3] = t.w;
+  } else {
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t lo = 2 * q < n ? r[2 * q] : 0u, hi = 2 * q + 1 < n ? r[2 * q + 1] : 0u;
+      rw[q] = lo | (hi << 16);
+    }
+  }
+  const uint32_t cw[4] = {v.x, v.y, v.z, v.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    o[q] = pack_bf16x2(__uint_as_float(cw[q] << 16) + __uint_as_float(rw[q] << 16),
+                       __uint_as_float(cw[q] & 0xFFFF0000u) + __uint_as_float(rw[q] & 0xFFFF0000u));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <bool OUT_F32, int NJ, int MI = 4>
 __device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const f32x16_t (&acc)[MI][NJ],
                                              int row0, int col0, int wm, int wn, int wave, int lane) {
@@ -384,10 +414,13 @@ __device__ __forceinline__ void store_tile_w(const GemmArgs& g, char* lds, const
     for (int it = 0; it < kIters; ++it) {
       const int e = it * 64 + lane;
       const int row = e / kSegs, seg = e % kSegs;
-      const uint4 v = *reinterpret_cast<const uint4*>(reg + row * kPitch + seg * 16);
+      uint4 v = *reinterpret_cast<const uint4*>(reg + row * kPitch + seg * 16);
       const int grow = row0 + wm + 32 * i + row;
       const int gcol = col0 + wn + seg * (16 / kEsz);
       if (grow >= g.M || gcol >= g.N) continue;
+      if constexpr (!OUT_F32) {
+        if (g.res != nullptr) v = add_residual8(v, g.res + static_cast<int64_t>(grow) * g.ldres + gcol, g.N - gcol);
+      }
       char* dst = static_cast<char*>(g.C) + (static_cast<int64_t>(grow) * g.ldc + gcol) * kEsz;
       if (vec && gcol + 16 / kEsz <= g.N) {
         *reinterpret_cast<uint4*>(dst) = v;
@@ -438,10 +471,13 @@ __device__ __forceinline__ void store_tile_t(const GemmArgs& g, char* lds, const
     for (int it = 0; it < kIters; ++it) {
       const int e = it * 64 + lane;
       const int row = e / kSegs, seg = e % kSegs;
-      const uint4 v = *reinterpret_cast<const uint4*>(reg + row * kPitch + seg * 16);
+      uint4 v = *reinterpret_cast<const uint4*>(reg + row * kPitch + seg * 16);
       const int grow = row0 + wm + 32 * i + row;
       const int gcol = col0 + wn + seg * (16 / kEsz);
       if (grow >= g.M || gcol >= g.N) continue;
+      if constexpr (!OUT_F32) {
+        if (g.res != nullptr) v = add_residual8(v, g.res + static_cast<int64_t>(grow) * g.ldres + gcol, g.N - gcol);
+      }
       char* dst = static_cast<char*>(g.C) + (static_cast<int64_t>(grow) * g.ldc + gcol) * kEsz;
       if (vec && gcol + 16 / kEsz <= g.N) {
         *reinterpret_cast<uint4*>(dst) = v;
@@ -1203,7 +1239,9 @@ void gemm_pp_kernel(GemmArgs g) {
 template <bool OUT_F32>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t stride,
                                                             int ksplit, int M, int N, int64_t ldw,
-                                                            void* __restrict__ C, int64_t ldc, int vec) {
+                                                            void* __restrict__ C, int64_t ldc, int vec,
+                                                            const uint16_t* __restrict__ res = nullptr,
+                                                            int64_t ldres = 0) {
   const int qpr = (N + 3) / 4;
   const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (q >= static_cast<int64_t>(M) * qpr) return;
@@ -1217,7 +1255,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     s.z += v.z;
     s.w += v.w;
   }
-  const float r[4] = {s.x, s.y, s.z, s.w};
+  float r[4] = {s.x, s.y, s.z, s.w};
+  if (!OUT_F32 && res != nullptr) {
+    // bf16(bf16(sum) + residual), the rounding of x + bf16 GEMM output
+    const uint16_t* rp = res + row * ldres + c;
+    for (int e = 0; e < 4; ++e)
+      if (c + e < N)
+        r[e] = __uint_as_float(pack_bf16x2(r[e], 0.0f) << 16) + __uint_as_float(static_cast<uint32_t>(rp[e]) << 16);
+  }
   if (OUT_F32) {
     float* dst = static_cast<float*>(C) + row * ldc + c;
     if (vec && c + 4 <= N) {
@@ -1886,12 +1931,19 @@ extern "C" int moc_gemm(int dtype, int64_t M, int64_t N, int64_t K, const void* 
                      b2_sn, C, ldc, c_dtype, nullptr, 0, stream);
 }
 
-extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
-                           int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
-                           const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
-                           int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+namespace {
+
+// moc_gemm_ws with an optional bf16 residual R added to a bf16 C (res may be
+// null): C = bf16(bf16(A B (+ A2 B2)) + R).
+int gemm_ws_impl(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm, int64_t a_sk,
+                 const void* B, int64_t b_sk, int64_t b_sn, int64_t K2, const void* A2, int64_t a2_sm,
+                 int64_t a2_sk, const void* B2, int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
+                 void* workspace, int64_t workspace_bytes, void* stream, const void* res, int64_t ldres) {
   MOC_REQUIRE(dtype == MOC_BF16 || dtype == MOC_F32, "moc_gemm: dtype must be bf16 or f32");
+  MOC_REQUIRE(res == nullptr || (dtype == MOC_BF16 && c_dtype == MOC_BF16 && aligned16(res) && ldres % 8 == 0 &&
+                                 ldres >= N),
+              "moc_gemm: a residual needs bf16 operands and output and 16-byte aligned rows (ldres a multiple "
+              "of 8, >= N)");
   MOC_REQUIRE(M >= 0 && N >= 0 && K >= 0 && K2 >= 0, "moc_gemm: negative extent");
   MOC_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && K2 < (1LL << 31),
               "moc_gemm: extent too large");
@@ -2009,6 +2061,8 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
   a.N = static_cast<int>(N);
   a.C = C;
   a.ldc = ldc;
+  a.res = static_cast<const uint16_t*>(res);
+  a.ldres = ldres;
   a.vec_store = (reinterpret_cast<uintptr_t>(C) % 16 == 0 &&
                  (ldc * (c_dtype == MOC_F32 ? 4 : 2)) % 16 == 0) ? 1 : 0;
   a.tiles_m = static_cast<int>((M + kBM - 1) / kBM);
@@ -2082,9 +2136,32 @@ extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const voi
                                                        C, ldc, a.vec_store);
     else
       splitk_reduce_kernel<false><<<grid, 256, 0, st>>>(parts, run.ws_stride, sp.ksplit, (int)M, (int)N, sp.ldw,
-                                                        C, ldc, a.vec_store);
+                                                        C, ldc, a.vec_store, a.res, a.ldres);
     return check_launch("splitk_reduce_kernel");
   }
+}
+
+}  // namespace
+
+extern "C" int moc_gemm_ws(int dtype, int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm,
+                           int64_t a_sk, const void* B, int64_t b_sk, int64_t b_sn, int64_t K2,
+                           const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2,
+                           int64_t b2_sk, int64_t b2_sn, void* C, int64_t ldc, int c_dtype,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  return gemm_ws_impl(dtype, M, N, K, A, a_sm, a_sk, B, b_sk, b_sn, K2, A2, a2_sm, a2_sk, B2, b2_sk, b2_sn, C,
+                      ldc, c_dtype, workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+// C = bf16(bf16(A B) + R): moc_gemm_ws for bf16 operands and output with the
+// residual R [M, N] (rows ldres apart) added in the epilogue (the decoder
+// block's x + Down(z) in one pass).
+extern "C" int moc_gemm_residual_bf16(int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm, int64_t a_sk,
+                                      const void* B, int64_t b_sk, int64_t b_sn, void* C, int64_t ldc,
+                                      const void* res, int64_t ldres, void* workspace, int64_t workspace_bytes,
+                                      void* stream) {
+  MOC_REQUIRE(res != nullptr, "moc_gemm_residual_bf16: null residual");
+  return gemm_ws_impl(MOC_BF16, M, N, K, A, a_sm, a_sk, B, b_sk, b_sn, 0, nullptr, 0, 0, nullptr, 0, 0, C, ldc,
+                      MOC_BF16, workspace, workspace_bytes, stream, res, ldres);
 }
 
 namespace moc {

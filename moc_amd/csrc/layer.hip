@@ -32,7 +32,7 @@ int ffn_forward(int dt, const char* name, int64_t rows, int64_t d, int64_t inter
                 const void* x, int64_t ldx, const void* wg, int64_t ldwg, const void* wu, int64_t ldwu,
                 const void* wd, int64_t ldwd, void* g, void* u, int64_t ld_gu, void* vals, void* idx,
                 int idx_dtype, void* u_s, void* s_s, void* z_s, void* out, int64_t ldo, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, const void* res = nullptr, int64_t ldres = 0) {
   const int64_t esz = dt == MOC_BF16 ? 2 : 4;
   MOC_REQUIRE(rows >= 1 && d >= 1 && inter >= 1 && k >= 1 && k <= inter, "%s: bad shape", name);
   MOC_REQUIRE(selection >= 0 && selection <= 2, "%s: selection 0 (Top-K), 1 (Top-K of |SiLU(G)|) or 2 (top-2 of 8)",
@@ -80,7 +80,10 @@ int ffn_forward(int dt, const char* name, int64_t rows, int64_t d, int64_t inter
   rc = moc_sparse_forward_aux(dt, vals, idx, idx_dtype, u, ld_gu, rows, k, inter, u_s, s_s, z_s, g, ld_gu,
                               stream);
   if (rc != MOC_OK) return rc;
-  // D = Z W_down^T
+  // D = Z W_down^T (with a residual: res + D from the same epilogue)
+  if (res != nullptr)
+    return moc_gemm_residual_bf16(rows, d, inter, g, ld_gu, 1, wd, 1, ldwd, out, ldo, res, ldres, workspace,
+                                  workspace_bytes, stream);
   return moc_gemm_ws(dt, rows, d, inter, g, ld_gu, 1, wd, 1, ldwd, 0, nullptr, 0, 0, nullptr, 0, 0, out, ldo, dt,
                      workspace, workspace_bytes, stream);
 }
@@ -198,4 +201,75 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
   // dX = gG Wg + gU Wu (:491-497)
   return moc_gemm_ws(MOC_BF16, rows, d, inter, gg, ld_ggu, 1, wg, ldwg, 1, inter, gu, ld_ggu, 1, wu, ldwu, 1, dx,
                      lddx, MOC_BF16, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The FFN half of a pre-norm decoder block, h + FFN(RMSNorm(h))
+// (moc/model.py:20-28,83-86), as one call per pass: the norm as a row pass,
+// the FFN's launches, the residual add in the Down GEMM's epilogue; the
+// backward recomputes the norm's output (same kernel, same bits) instead of
+// keeping it, runs the FFN backward and then the norm's backward with the
+// residual branch's gradient added.
+
+extern "C" int moc_ffn_block_forward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, int selection,
+                                          const void* h, int64_t ldh, const void* norm_w, float eps, void* xn,
+                                          int64_t ldxn, float* rstd, const void* wg, int64_t ldwg, const void* wu,
+                                          int64_t ldwu, const void* wd, int64_t ldwd, void* g, void* u,
+                                          int64_t ld_gu, void* vals, void* idx, int idx_dtype, void* u_s,
+                                          void* s_s, void* z_s, void* out, int64_t ldo, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(rstd != nullptr, "moc_ffn_block_forward_bf16: null rstd");
+  MOC_REQUIRE(ld_ok(h, ldh, d), "moc_ffn_block_forward_bf16: h needs 16-byte aligned rows");
+  int rc = moc_rmsnorm_rows_bf16(h, ldh, rows, d, norm_w, eps, xn, ldxn, rstd, stream);
+  if (rc != MOC_OK) return rc;
+  return ffn_forward(MOC_BF16, "moc_ffn_block_forward_bf16", rows, d, inter, k, selection, xn, ldxn, wg, ldwg, wu,
+                     ldwu, wd, ldwd, g, u, ld_gu, vals, idx, idx_dtype, u_s, s_s, z_s, out, ldo, workspace,
+                     workspace_bytes, stream, h, ldh);
+}
+
+namespace {
+// Where the norm backward's partial rows start in the block backward's
+// workspace: after the FFN backward's GEMM workspace, and never inside the
+// GEMM arrival counters at its start (which must stay zero between calls).
+int64_t block_rms_offset(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu, int stacked) {
+  const int64_t f = (moc_ffn_backward_workspace_size(rows, d, inter, ld_ggu, stacked) + 255) / 256 * 256;
+  return std::max<int64_t>(f, MOC_GEMM_WS_COUNTER_BYTES);
+}
+}  // namespace
+
+extern "C" int64_t moc_ffn_block_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, int64_t ld_ggu,
+                                                         int stacked) {
+  if (rows <= 0 || d <= 0 || inter <= 0) return 0;
+  return block_rms_offset(rows, d, inter, ld_ggu, stacked) + moc_rmsnorm_backward_workspace_size(rows, d);
+}
+
+extern "C" int moc_ffn_block_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* dout,
+                                           int64_t ldgo, const void* h, int64_t ldh, const void* norm_w, float eps,
+                                           const float* rstd, void* xn, int64_t ldxn, const void* idx,
+                                           int idx_dtype, const void* g_s, const void* u_s, const void* s_s,
+                                           const void* z_s, const void* wg, int64_t ldwg, const void* wu,
+                                           int64_t ldwu, const void* wd, int64_t ldwd, void* zbuf, int64_t ldz,
+                                           void* gg, void* gu, int64_t ld_ggu, int stacked, void* s_tmp,
+                                           void* dh, int64_t lddh, void* dwg, void* dwu, int64_t ld_dw, void* dwd,
+                                           int64_t lddwd, int grad_dtype, void* dnorm_w, int dnorm_dtype,
+                                           void* workspace, int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(rows >= 1 && d >= 1, "moc_ffn_block_backward_bf16: bad shape");
+  const int64_t need = moc_ffn_block_backward_workspace_size(rows, d, inter, ld_ggu, stacked);
+  MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need && moc::aligned16(workspace),
+              "moc_ffn_block_backward_bf16: workspace of %lld bytes required", (long long)need);
+  MOC_REQUIRE(ld_ok(h, ldh, d) && ld_ok(xn, ldxn, d) && ld_ok(dh, lddh, d) && rstd != nullptr,
+              "moc_ffn_block_backward_bf16: h, xn and dh need 16-byte aligned rows");
+  const int64_t f = block_rms_offset(rows, d, inter, ld_ggu, stacked);
+  // the FFN's input again (the forward's row pass: same bits)
+  int rc = moc_rmsnorm_rows_bf16(h, ldh, rows, d, norm_w, eps, xn, ldxn, nullptr, stream);
+  if (rc != MOC_OK) return rc;
+  // FFN backward; its dX (the norm output's gradient) goes into xn's buffer:
+  // xn is last read by the weight-gradient GEMMs, which run before dX
+  rc = moc_ffn_backward_bf16(rows, d, inter, k, dout, ldgo, xn, ldxn, idx, idx_dtype, g_s, u_s, s_s, z_s, wg,
+                             ldwg, wu, ldwu, wd, ldwd, zbuf, ldz, gg, gu, ld_ggu, stacked, s_tmp, xn, ldxn, dwg,
+                             dwu, ld_dw, dwd, lddwd, grad_dtype, workspace, f, stream);
+  if (rc != MOC_OK) return rc;
+  // dh = dout (the residual branch) + the norm's backward of dX
+  return moc_rmsnorm_backward_bf16(h, ldh, rows, d, norm_w, rstd, xn, ldxn, dout, ldgo, dh, lddh, dnorm_w,
+                                   dnorm_dtype, static_cast<char*>(workspace) + f, workspace_bytes - f, stream);
 }

@@ -194,11 +194,12 @@ def _layer_forward(x, x2, gate_w, up_w, down_w, k, selection: str, idx_dtype, sa
 
 
 def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_s: bool,
-                    want_mask: bool = False):
+                    want_mask: bool = False, residual=None):
     """Shared MoC forward: G -> select -> U -> sparse aux -> D.
 
     Follows _MoCFunction.forward (moc/ffn.py:130-173) and the variants at
-    :266-308 (2:8), :322-367 (post-SiLU) and :378-421 (GCP)."""
+    :266-308 (2:8), :322-367 (post-SiLU) and :378-421 (GCP).  With
+    `residual` ([rows, d] bf16), returns residual + D from D's epilogue."""
     d = x.shape[-1]
     inter = gate_w.shape[0]
     x2 = K.aligned_rows(x.reshape(-1, d))
@@ -209,7 +210,7 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
     # which the backward reuses, then runs on the side stream beside the
     # selection.  f32: U on the side stream beside G and the selection.
     side = _side_for(x.device, rows, inter)
-    if side is None and not want_mask and down_w.shape[0] == d and \
+    if side is None and not want_mask and residual is None and down_w.shape[0] == d and \
             _layer_ok(x2, gate_w, up_w, down_w, dtypes=(torch.bfloat16, torch.float32)):
         # one native call for the whole single-stream forward (host-bound shapes)
         return _layer_forward(x, x2, gate_w, up_w, down_w, k, selection, idx_dtype, save_s)
@@ -244,7 +245,7 @@ def _forward_common(x, gate_w, up_w, down_w, k, selection: str, idx_dtype, save_
         torch.cuda.current_stream(x.device).wait_stream(side)
     u_s, s_s, z_s, z_full = K.sparse_forward_aux(vals, idx, u, inter, want_s=save_s, want_z=save_s)
     del u
-    out = K.gemm(z_full, wd.t())
+    out = K.gemm(z_full, wd.t(), residual=residual)
     del z_full
     kk = idx.shape[-1]
     shp = (*x.shape[:-1], kk)
@@ -530,6 +531,187 @@ class MoCSwiGLUFFN(nn.Module):
         else:
             fn = _MoCFunction
         return fn.apply(x, wg, wu, wd, self.k, self.index_save_dtype, aux)
+
+
+# ------------------------------------------------------------ decoder block
+# The FFN half of a pre-norm block, h + FFN(RMSNorm(h)) (TransformerBlock.
+# forward, moc/model.py:83-86; RMSNorm :20-28), with the norm as one row
+# kernel in front of the FFN and the residual add in the Down GEMM's
+# epilogue; the backward runs the FFN backward on the recomputed norm output
+# and then the norm's backward with the residual gradient added.  The
+# library's own fusion of the FFN's neighbours (no reference counterpart:
+# the reference runs stock PyTorch ops around its FFN).
+FUSE_BLOCK_FFN = True
+
+_SELECTION_OF_MODE = {"moc": ("topk", False), "moc_triton_aux": ("topk", False),
+                      "moc_gcp": ("topk", True), "moc_gcp_triton_aux": ("topk", True),
+                      "moc_2_8": ("2of8", False), "moc_2_8_triton_aux": ("2of8", False),
+                      "moc_post_silu_abs": ("post_silu_abs", False),
+                      "moc_post_silu_abs_triton_aux": ("post_silu_abs", False)}
+
+
+def block_ffn_ok(h, norm_weight, ffn) -> bool:
+    """True if block_ffn takes this block: a MoC FFN, bf16 activations,
+    norm weight and FFN weights on the device, no autocast, hidden a
+    multiple of 8 up to 4096."""
+    if not FUSE_BLOCK_FFN or not isinstance(ffn, MoCSwiGLUFFN) or ffn.mode not in _SELECTION_OF_MODE:
+        return False
+    if not h.is_cuda or h.dtype != torch.bfloat16 or norm_weight.dtype != torch.bfloat16:
+        return False
+    if _autocast_dtype(h) is not None:
+        return False
+    d = h.shape[-1]
+    if d % 8 or d > 4096:
+        return False
+    return all(w.dtype == torch.bfloat16 and w.is_cuda for w in
+               (ffn.gate_proj.weight, ffn.up_proj.weight, ffn.down_proj.weight))
+
+
+def block_ffn(h, norm_weight, eps: float, ffn) -> torch.Tensor:
+    """h + ffn(RMSNorm(h)) with the norm (weight norm_weight, eps) and the
+    residual fused around the MoC FFN `ffn` (block_ffn_ok must hold)."""
+    selection, gcp = _SELECTION_OF_MODE[ffn.mode]
+    return _MoCBlockFunction.apply(h, norm_weight, ffn.gate_proj.weight, ffn.up_proj.weight,
+                                   ffn.down_proj.weight, float(eps), ffn.k, ffn.index_save_dtype,
+                                   ffn.mode.endswith("_triton_aux"), selection, gcp)
+
+
+def _block_native(h2, wg, wu, wd) -> bool:
+    """The one-call block entry points take this shape (single-stream)."""
+    return _side_for(h2.device, h2.shape[0], wg.shape[0]) is None and h2.shape[1] == wd.shape[0] and \
+        _layer_ok(h2, wg, wu, wd)
+
+
+class _MoCBlockFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, h, norm_w, gate_w, up_w, down_w, eps, k, index_save_dtype, use_triton_aux, selection,
+                gcp):
+        _check_inputs(h, gate_w, up_w, down_w, use_triton_aux, index_save_dtype)
+        d = h.shape[-1]
+        inter = gate_w.shape[0]
+        h2 = K.aligned_rows(h.reshape(-1, d))
+        rows = h2.shape[0]
+        idx_dtype = _pack_topk_idx_dtype(index_save_dtype, inter)
+        bitmask = index_save_dtype == INDEX_SAVE_BITMASK
+        mask = None
+        if not bitmask and _block_native(h2, gate_w, up_w, down_w):
+            out, idx, vals, u_s, s_s, z_s, rstd = _block_forward_native(
+                h2, norm_w, eps, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=not gcp)
+        else:
+            xn, rstd = K.rmsnorm_rows(h2, norm_w, eps)
+            out, idx, vals, u_s, s_s, z_s, *mk = _forward_common(
+                xn, gate_w, up_w, down_w, k, selection, idx_dtype, save_s=not gcp, want_mask=bitmask,
+                residual=h2)
+            mask = mk[0] if mk else None
+            del xn
+        sel = _saved_index(idx, mask, bitmask)
+        if gcp:
+            ctx.save_for_backward(h2, rstd, norm_w, sel, vals, u_s, gate_w, up_w, down_w)
+        else:
+            ctx.save_for_backward(h2, rstd, norm_w, sel, vals, u_s, s_s, z_s, gate_w, up_w, down_w)
+        ctx.k = idx.shape[-1]
+        ctx.inter = inter
+        ctx.bitmask = bitmask
+        ctx.gcp = gcp
+        ctx.eps = eps
+        ctx.h_shape = h.shape
+        return out.reshape(h.shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        if ctx.gcp:
+            h2, rstd, norm_w, saved, g_s, u_s, wg, wu, wd = ctx.saved_tensors
+            s_s = z_s = None
+        else:
+            h2, rstd, norm_w, saved, g_s, u_s, s_s, z_s, wg, wu, wd = ctx.saved_tensors
+        idx = _restore_index(ctx, saved)
+        d = h2.shape[1]
+        go = K.aligned_rows(dout.reshape(-1, d).to(h2.dtype))
+        if _block_native(h2, wg, wu, wd) and _layer_ok(go) and \
+                (not ctx.gcp or K.row_pitch(ctx.inter, h2.dtype) <= 8192):
+            dh, dnw, dwg, dwu, dwd = _block_backward_native(ctx, go, h2, rstd, norm_w, idx, g_s, u_s, s_s,
+                                                            z_s, wg, wu, wd)
+        else:
+            xn, _ = K.rmsnorm_rows(h2, norm_w, ctx.eps, want_rstd=False)
+            dxn, dwg, dwu, dwd = _backward_common(go, xn, idx, g_s, u_s, s_s, z_s, wg, wu, wd, gcp=ctx.gcp)
+            del xn
+            dh, dnw = K.rmsnorm_backward(h2, norm_w, rstd, dxn.reshape(-1, d), dres=go)
+        return (dh.reshape(ctx.h_shape), dnw, dwg, dwu, dwd, None, None, None, None, None, None)
+
+
+def _block_forward_native(h2, norm_w, eps, gate_w, up_w, down_w, k, selection, idx_dtype, save_s):
+    """moc_ffn_block_forward_bf16: the norm, the FFN and the residual add in
+    one call (the launches of the unfused path in the same order)."""
+    rows, d = h2.shape
+    inter = gate_w.shape[0]
+    dev = h2.device
+    dt = h2.dtype
+    pitch = K.row_pitch(inter, dt)
+    kk = _moc_2_8_effective_k(inter) if selection == "2of8" else k
+    xn = torch.empty((rows, d), dtype=dt, device=dev)
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    g = torch.empty((rows, pitch), dtype=dt, device=dev)
+    u = torch.empty((rows, pitch), dtype=dt, device=dev)
+    vals = torch.empty((rows, kk), dtype=dt, device=dev)
+    idx = torch.empty((rows, kk), dtype=idx_dtype, device=dev)
+    u_s = torch.empty((rows, kk), dtype=dt, device=dev)
+    s_s = torch.empty((rows, kk), dtype=dt, device=dev) if save_s else None
+    z_s = torch.empty((rows, kk), dtype=dt, device=dev) if save_s else None
+    out = torch.empty((rows, d), dtype=dt, device=dev)
+    nbytes = _layer_ws_bytes(("f", False, dev.index, rows, d, inter), "moc_ffn_forward_workspace_size",
+                             rows, d, inter)
+    ws = K._gemm_workspace(dev, nbytes) if nbytes > 0 else None
+    N.call("moc_ffn_block_forward_bf16", rows, d, inter, kk, _SELECTION_CODE[selection], h2.data_ptr(),
+           h2.stride(0), norm_w.contiguous().data_ptr(), float(eps), xn.data_ptr(), d, rstd.data_ptr(),
+           gate_w.data_ptr(), d, up_w.data_ptr(), d, down_w.data_ptr(), inter, g.data_ptr(), u.data_ptr(),
+           pitch, vals.data_ptr(), idx.data_ptr(), N.idx_code(idx_dtype), u_s.data_ptr(), N.ptr(s_s),
+           N.ptr(z_s), out.data_ptr(), d, N.ptr(ws), nbytes, N.stream_of(h2))
+    return out, idx, vals, u_s, s_s, z_s, rstd
+
+
+def _block_backward_native(ctx, go, h2, rstd, norm_w, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w):
+    """moc_ffn_block_backward_bf16: norm recompute, FFN backward and the
+    norm's backward with the residual gradient in one call."""
+    rows, d = h2.shape
+    inter = gate_w.shape[0]
+    dev = h2.device
+    bf16 = torch.bfloat16
+    pitch = K.row_pitch(inter, bf16)
+    idx2 = idx.reshape(rows, -1)
+    kk = idx2.shape[1]
+    g2, u2 = g_s.reshape(rows, kk), u_s.reshape(rows, kk)
+    s2 = None if ctx.gcp else s_s.reshape(rows, kk)
+    z2 = None if ctx.gcp else z_s.reshape(rows, kk)
+    for t in (idx2, g2, u2, s2, z2):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("saved selection tensors must be contiguous")
+    grad_dtype = down_w.dtype
+    stacked = _stack_weight_grads(dev, inter, d, pitch, bf16)
+    xn = torch.empty((rows, d), dtype=bf16, device=dev)
+    zbuf = torch.empty((rows, pitch), dtype=bf16, device=dev)
+    ggu = torch.empty((rows, 2 * pitch), dtype=bf16, device=dev)
+    s_tmp = torch.empty((rows, kk), dtype=bf16, device=dev) if ctx.gcp else None
+    dh = torch.empty((rows, d), dtype=bf16, device=dev)
+    if stacked:
+        dw = torch.empty((2 * pitch, d), dtype=grad_dtype, device=dev)
+        dwg, dwu = dw[:inter], dw[pitch:pitch + inter]
+    else:
+        dwg = torch.empty((inter, d), dtype=grad_dtype, device=dev)
+        dwu = torch.empty((inter, d), dtype=grad_dtype, device=dev)
+    dwd = torch.empty((d, inter), dtype=grad_dtype, device=dev)
+    dnw = torch.empty(d, dtype=norm_w.dtype, device=dev)
+    nbytes = _layer_ws_bytes(("bb", dev.index, rows, d, inter, stacked), "moc_ffn_block_backward_workspace_size",
+                             rows, d, inter, 2 * pitch, int(stacked))
+    ws = K._gemm_workspace(dev, nbytes)
+    gg = ggu.data_ptr()
+    N.call("moc_ffn_block_backward_bf16", rows, d, inter, kk, go.data_ptr(), go.stride(0), h2.data_ptr(),
+           h2.stride(0), norm_w.contiguous().data_ptr(), float(ctx.eps), rstd.data_ptr(), xn.data_ptr(), d,
+           idx2.data_ptr(), N.idx_code(idx2.dtype), g2.data_ptr(), u2.data_ptr(), N.ptr(s2), N.ptr(z2),
+           gate_w.data_ptr(), d, up_w.data_ptr(), d, down_w.data_ptr(), inter, zbuf.data_ptr(), pitch, gg,
+           gg + 2 * pitch, 2 * pitch, int(stacked), N.ptr(s_tmp), dh.data_ptr(), d, dwg.data_ptr(),
+           dwu.data_ptr(), d, dwd.data_ptr(), inter, N.dtype_code(grad_dtype), dnw.data_ptr(),
+           N.dtype_code(norm_w.dtype), ws.data_ptr(), nbytes, N.stream_of(h2))
+    return dh, dnw, dwg, dwu, dwd
 
 
 def build_ffn(hidden_size: int, intermediate_size: int, ffn_type: str = "dense", k=None):

@@ -359,8 +359,12 @@ def _gemm_workspace(device, nbytes: int) -> torch.Tensor:
 
 def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
          b2: torch.Tensor | None = None, out: torch.Tensor | None = None,
-         out_dtype: torch.dtype | None = None) -> torch.Tensor:
-    """C = a @ b (+ a2 @ b2) on the MFMA engine; a: [M, K], b: [K, N]."""
+         out_dtype: torch.dtype | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """C = a @ b (+ a2 @ b2) on the MFMA engine; a: [M, K], b: [K, N].  With
+    `residual` (bf16 [M, N], bf16 operands, one product): C = residual +
+    a @ b, added in the GEMM's epilogue (bf16(bf16(a @ b) + residual))."""
+    if residual is not None:
+        return _gemm_residual(a, b, residual, out)
     N.require_device(a, b, a2, b2, out)
     if a.dtype != b.dtype or (a2 is not None and (a2.dtype != a.dtype or b2.dtype != a.dtype)):
         raise ValueError("moc gemm operands must share one dtype")
@@ -401,6 +405,76 @@ def gemm(a: torch.Tensor, b: torch.Tensor, *, a2: torch.Tensor | None = None,
            N.dtype_code(out_dtype), N.ptr(ws), ws_bytes, N.stream_of(a))
     _probe_end(probe, f"gemm {M}x{Nn}x{K}" + (f"+{K2}" if K2 else ""), 2.0 * M * Nn * (K + K2))
     return out
+
+
+def _gemm_residual(a, b, residual, out):
+    N.require_device(a, b, residual, out)
+    if not (a.dtype == b.dtype == residual.dtype == torch.bfloat16):
+        raise ValueError("gemm with a residual takes bf16 operands and a bf16 residual")
+    M, Kd = a.shape
+    K_, Nn = b.shape
+    if Kd != K_ or residual.shape != (M, Nn):
+        raise ValueError(f"gemm shape mismatch {tuple(a.shape)} @ {tuple(b.shape)} + {tuple(residual.shape)}")
+    if out is None:
+        out = _empty((M, Nn), torch.bfloat16, a.device)
+    if out.shape != (M, Nn) or out.dtype != torch.bfloat16 or (out.stride(1) != 1 and Nn > 1):
+        raise ValueError("gemm out must be bf16 [M, N] with unit column stride")
+    r = aligned_rows(residual)
+    aa, as0, as1 = _operand(a, True)
+    bb, bs0, bs1 = _operand(b, True)
+    ws_bytes = 0
+    if gemm_tiles(M, Nn) < cu_count(a.get_device()):
+        ws_bytes = N.query("moc_gemm_workspace_size", N.MOC_BF16, M, Nn, Kd, 0)
+    ws = _gemm_workspace(a.device, ws_bytes) if ws_bytes > 0 else None
+    probe = _probe_begin()
+    N.call("moc_gemm_residual_bf16", M, Nn, Kd, aa.data_ptr(), as0, as1, bb.data_ptr(), bs0, bs1,
+           out.data_ptr(), out.stride(0) if M > 1 else max(Nn, 1), r.data_ptr(),
+           r.stride(0) if M > 1 else round_up(max(Nn, 1), 8), N.ptr(ws), ws_bytes, N.stream_of(a))
+    _probe_end(probe, f"gemm {M}x{Nn}x{Kd} +res", 2.0 * M * Nn * Kd)
+    return out
+
+
+def rmsnorm_rows(x2d: torch.Tensor, weight: torch.Tensor, eps: float, *, out: torch.Tensor | None = None,
+                 want_rstd: bool = True):
+    """(y, rstd): the pre-norm y = bf16(bf16(x / rms(x)) * weight) of every
+    row of a bf16 [rows, d] tensor (RMSNorm.forward of moc/model.py:26-28),
+    rstd = 1 / rms(x) per row in f32 (None unless want_rstd)."""
+    N.require_device(x2d, weight, out)
+    if x2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("rmsnorm_rows takes bf16 rows and a bf16 weight")
+    xa = aligned_rows(x2d)
+    rows, d = xa.shape
+    w = weight.contiguous()
+    if w.shape != (d,):
+        raise ValueError(f"norm weight must be [{d}]")
+    y = padded_empty(rows, d, torch.bfloat16, x2d.device) if out is None else out
+    rstd = torch.empty(rows, dtype=torch.float32, device=x2d.device) if want_rstd else None
+    N.call("moc_rmsnorm_rows_bf16", xa.data_ptr(), xa.stride(0) if rows > 1 else round_up(d, 8), rows, d,
+           w.data_ptr(), float(eps), y.data_ptr(), y.stride(0) if rows > 1 else round_up(d, 8),
+           N.ptr(rstd), N.stream_of(x2d))
+    return y, rstd
+
+
+def rmsnorm_backward(x2d: torch.Tensor, weight: torch.Tensor, rstd: torch.Tensor, dy: torch.Tensor,
+                     dres: torch.Tensor | None = None, dw_dtype=None):
+    """(dx, dw) of rmsnorm_rows given dy, plus dres (the gradient of a
+    residual branch around the norm, added to dx)."""
+    N.require_device(x2d, weight, rstd, dy, dres)
+    xa, ga = aligned_rows(x2d), aligned_rows(dy)
+    ra = None if dres is None else aligned_rows(dres)
+    rows, d = xa.shape
+    w = weight.contiguous()
+    dw_dtype = dw_dtype or weight.dtype
+    dx = padded_empty(rows, d, torch.bfloat16, x2d.device)
+    dw = torch.empty(d, dtype=dw_dtype, device=x2d.device)
+    nbytes = N.query("moc_rmsnorm_backward_workspace_size", rows, d)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=x2d.device)
+    ld = lambda t: t.stride(0) if rows > 1 else round_up(d, 8)  # noqa: E731
+    N.call("moc_rmsnorm_backward_bf16", xa.data_ptr(), ld(xa), rows, d, w.data_ptr(),
+           rstd.contiguous().data_ptr(), ga.data_ptr(), ld(ga), N.ptr(ra), 0 if ra is None else ld(ra),
+           dx.data_ptr(), ld(dx), dw.data_ptr(), N.dtype_code(dw_dtype), ws.data_ptr(), ws.numel(),
+           N.stream_of(x2d))
+    return dx, dw
 
 
 def linear(x2d: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor | None = None,

@@ -117,3 +117,111 @@ def test_decode_fused_ffn_neighbours_match_unfused(row):
     lf = fused.forward_step(tf[:, :1], pos).float()
     lp = plain.forward_step(tf[:, :1], pos).float()
     assert torch.allclose(lf, lp, atol=5e-2, rtol=5e-2)
+
+
+class _FFNRecorder:
+    """Records every FFN call of a decode model: ("ffn", x, y) for the
+    module's forward (x is the FFN input after ffn_norm) and ("fused", x, y,
+    norm weight, eps) for fused_decode_residual (x before the norm, y = x +
+    FFN(norm(x))).  With graph_only, only calls made while a HIP graph is
+    being captured are kept: their clones are written again by every replay,
+    so after a replay they hold that replay's FFN inputs and outputs."""
+
+    def __init__(self, model, graph_only: bool):
+        self.calls = []
+        self.graph_only = graph_only
+        for i, layer in enumerate(model.layers):
+            layer.ffn.register_forward_hook(
+                lambda mod, args, out, _i=i: self._add(_i, "ffn", args[0], out))
+            orig = layer.ffn.fused_decode_residual
+
+            def fused(x, w, eps, _orig=orig, _i=i):
+                y = _orig(x, w, eps)
+                self._add(_i, "fused", x, y, w, eps)
+                return y
+
+            layer.ffn.fused_decode_residual = fused
+
+    def _add(self, i, kind, x, y, w=None, eps=None):
+        if self.graph_only and not torch.cuda.is_current_stream_capturing():
+            return
+        self.calls.append((i, kind, x.detach().clone(), y.detach().clone(), w, eps))
+
+
+def _ffn_oracle(ffn, row, x):
+    """The FFN of one decode layer on the CPU oracle, for FFN input x [n, h]
+    (bf16 on the device): global MoC is masked_reference with the device's
+    own gate scores (the same GEMV/GEMM the layer runs, so the selection is
+    compared on identical inputs); MoC 2:8 is kernel A (grouped top-2 + up
+    SiLU) then kernel B (selected Down) of the reference's Triton path."""
+    from moc_amd import kernels as K
+    from oracle import moc_oracle as O
+    wg, wu, wd = (w.detach() for w in (ffn.gate_proj.weight, ffn.up_proj.weight, ffn.down_proj.weight))
+    if row == "global_moc":
+        g = (K.gemv(x, wg) if x.shape[0] <= 16 else K.linear(x, wg)).cpu()
+        y, _, _ = O.masked_reference(x.cpu(), wg.cpu(), wu.cpu(), wd.cpu(), ffn.config.k, g_override=g)
+        return y
+    idx, sz, _ = O.grouped_top2_up_silu(x.cpu(), wg.cpu(), wu.cpu())
+    return O.selected_down(sz, idx, wd.t().contiguous().cpu())
+
+
+def _check_calls(calls, model, row):
+    from oracle import moc_oracle as O
+    assert calls, "no FFN call was recorded"
+    for i, kind, x, y, w, eps in calls:
+        ffn = model.layers[i].ffn
+        if kind == "ffn":
+            ref = _ffn_oracle(ffn, row, x)
+        else:
+            xf = x.float()
+            xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
+            if row == "global_moc":
+                from moc_amd import kernels as K
+                _, xn = K.gemv_rmsnorm(x, w, eps, ffn.gate_proj.weight)  # the device's own x_norm
+            ref = (x.cpu().float() + _ffn_oracle(ffn, row, xn).float()).to(x.dtype)
+        a, b = y.float().cpu().reshape(ref.shape), ref.float()
+        err = (a - b).abs()
+        bad = err > 2e-2 + 2e-2 * b.abs()
+        assert not bool(bad.any()), (i, kind, tuple(x.shape), err.max().item())
+        assert O is not None
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fuse", [True, False])
+@pytest.mark.parametrize("row", ["global_moc", "moc_2_8"])
+def test_decode_ffn_calls_match_oracle_eager(row, fuse):
+    """Every FFN call of a 2-layer decode (the 24-token prompt through the
+    >16-token op forms, then 4 greedy single-token steps) against the
+    oracle on that call's own input: out within 2e-2."""
+    cfg = DecodeConfig(layers=2, max_seq=40)
+    m = DecoderModel(row, cfg, fuse=fuse).to(DEV, torch.bfloat16).init_weights(11)
+    m.allocate_cache()
+    rec = _FFNRecorder(m, graph_only=False)
+    prompt = torch.randint(0, cfg.vocab, (1, 24), generator=torch.Generator().manual_seed(12)).to(DEV)
+    run_decode(m, prompt, 4, make_step(m, "eager"))
+    torch.cuda.synchronize()
+    kinds = {k for _, k, *_ in rec.calls}
+    assert kinds == ({"ffn", "fused"} if fuse else {"ffn"}), kinds
+    _check_calls(rec.calls, m, row)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fuse", [True, False])
+@pytest.mark.parametrize("row", ["global_moc", "moc_2_8"])
+def test_decode_ffn_calls_match_oracle_whole_graph(row, fuse):
+    """The whole-step HIP graph (the scope of the decode benchmark's rows):
+    after each of three replays, every layer's FFN input and output as that
+    replay computed them, against the oracle."""
+    cfg = DecodeConfig(layers=2, max_seq=40)
+    m = DecoderModel(row, cfg, fuse=fuse).to(DEV, torch.bfloat16).init_weights(13)
+    m.allocate_cache()
+    rec = _FFNRecorder(m, graph_only=True)
+    prompt = torch.randint(0, cfg.vocab, (1, 24), generator=torch.Generator().manual_seed(14)).to(DEV)
+    step = make_step(m, "whole_graph")
+    assert len(rec.calls) == cfg.layers
+    m.reset_cache()
+    cur = m.forward_prompt(prompt)[:, -1:, :].argmax(dim=-1)
+    for i in range(3):
+        cur = step(cur, 24 + i).argmax(dim=-1)
+        torch.cuda.synchronize()
+        _check_calls(rec.calls, m, row)

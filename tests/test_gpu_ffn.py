@@ -481,10 +481,14 @@ def test_model_350m_two_layers_ffn_parity():
     tokens: every FFN's output and its gradients (dX, dWg, dWu, dWd) match the
     oracle run on that FFN's own input and upstream gradient."""
     from moc_amd import MoCConfig, build_model
+    from moc_amd import ffn as F
     cfg = MoCConfig(hidden_size=1024, intermediate_size=2736, num_hidden_layers=2,
                     num_attention_heads=16, vocab_size=32100, max_seq_len=256, k=512)
     torch.manual_seed(7)
     model = build_model(cfg, ffn_type="moc_gcp").to(DEV, torch.bfloat16)
+    # the FFN module's own call (its hooks see its input and gradients); the
+    # fused block form is tested in test_gpu_block.py
+    F.FUSE_BLOCK_FFN = False
     seen = {}
 
     def fwd_hook(mod, inp, out):
@@ -500,8 +504,11 @@ def test_model_350m_two_layers_ffn_parity():
         f.register_full_backward_hook(bwd_hook)
     tok = torch.randint(0, cfg.vocab_size, (16, 256), device=DEV,
                         generator=torch.Generator(device=DEV).manual_seed(3))
-    _, loss = model(tok, labels=tok)
-    loss.backward()
+    try:
+        _, loss = model(tok, labels=tok)
+        loss.backward()
+    finally:
+        F.FUSE_BLOCK_FFN = True
     assert torch.isfinite(loss).item()
     for f in ffns:
         rec = seen[f]

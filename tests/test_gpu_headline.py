@@ -53,11 +53,11 @@ def bench_inputs():
 @pytest.fixture(scope="module")
 def oracle_1b():
     """Inputs, the oracle's forward/backward on the device's own G, U, gZ."""
-    from moc_amd import kernels as K
+    from moc_amd import kernels as KR
     x, wg, wu, wd, go = bench_inputs()
     xd = x.to(DEV)
-    g, u = K.linear_pair(xd, wg.to(DEV), wu.to(DEV))
-    gz = K.gemm(K.aligned_rows(go.to(DEV)), K.aligned_rows(wd.to(DEV)))
+    g, u = KR.linear_pair(xd, wg.to(DEV), wu.to(DEV))
+    gz = KR.gemm(KR.aligned_rows(go.to(DEV)), KR.aligned_rows(wd.to(DEV)))
     g, u, gz = g.cpu(), u.cpu(), gz.cpu()
     torch.set_num_threads(min(16, max(1, torch.get_num_threads())))
     fwd = O.ffn_forward(x, wg, wu, wd, K, "moc_gcp", g_override=g, u_override=u)
