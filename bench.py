@@ -74,8 +74,15 @@ def parse_args():
                    help="only the 350m-model training step (config 5): tokens/s and peak "
                         "memory, moc_gcp vs dense, one JSON line")
     p.add_argument("--cfg5-steps", type=int, default=10)
-    p.add_argument("--no-gpu-busy", action="store_true",
-                   help="skip config 5's GPU-only timing (steps queued behind a sleep kernel)")
+    p.add_argument("--trace-summary", metavar="DIR", default=None,
+                   help="no GPU work: summarise a rocprofv3 --kernel-trace --stats --output-format csv "
+                        "output directory (per-kernel totals; with --trace-headline, the GEMM "
+                        "launches of the headline's timed steps) as markdown")
+    p.add_argument("--trace-steps", type=float, default=1.0,
+                   help="with --trace-summary: steps the traced run made (per-step columns)")
+    p.add_argument("--trace-headline", action="store_true",
+                   help="with --trace-summary: the trace is of `bench.py --skip-extra`; report the "
+                        "seven GEMM launches of its timed fwd+bwd steps")
     p.add_argument("--cfg5-row", choices=["moc_gcp", "dense", "moc_gcp_unfused"], default=None,
                    help="with --cfg5: only this row, and no FFN-layer timing (for kernel traces)")
     p.add_argument("--only", choices=["cfg1", "cfg2", "cfg4"], default=None,
@@ -113,35 +120,7 @@ def cfg5_model_flop(cfg, batch: int, seq: int) -> float:
     return 3.0 * fwd
 
 
-def gpu_only_ms(step, host_ms: float, n: int = 5):
-    """GPU time per call of step() with the host out of the loop: a bounded
-    sleep kernel holds the stream while the host queues n calls, so the GPU
-    then runs them back to back; the time between events around the n calls
-    is pure GPU time (kernels and the gaps the GPU itself needs between
-    them).  Returns (ms per call, True) if the host had queued all n calls
-    before the GPU reached them, else (ms, False): the host did not keep
-    ahead and the number includes host time."""
-    import torch
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    a.record()
-    torch.cuda._sleep(1 << 22)
-    b.record()
-    torch.cuda.synchronize()
-    cycles_per_ms = (1 << 22) / max(a.elapsed_time(b), 1e-3)
-    hold = int(cycles_per_ms * (2.0 * n * host_ms + 100.0))
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(hold)
-    e0.record()
-    for _ in range(n):
-        step()
-    e1.record()
-    ahead = not e0.query()  # the GPU was still asleep when the last call was queued
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / n, ahead
-
-
-def cfg5_bench(steps: int, gpu_busy: bool = True, only: str | None = None) -> dict:
+def cfg5_bench(steps: int, only: str | None = None) -> dict:
     """Config 5: a 350m LLaMA training step (24 layers, d=1024, I=2736,
     K=512), bf16 parameters, AdamW (0.9/0.999, wd 0, fused=False, lr 1e-3),
     tokens [16, 256] uniform over the 32100-token vocabulary with labels =
@@ -150,11 +129,10 @@ def cfg5_bench(steps: int, gpu_busy: bool = True, only: str | None = None) -> di
     memory over the timed steps (the method of
     benchmark_training_throughput.py:51-114 and benchmark_memory.py:51-107).
     Attention, norms and embeddings are stock PyTorch; the FFN is this
-    build's.  Beside the wall-clock step: the GPU-only time of a step (steps
-    queued behind a sleep kernel, so host time drops out: at this size the
-    host's launch time is close to the GPU's work, and the wall clock mixes
-    both), the model's algorithmic FLOP over both, and one FFN layer of the
-    step's shape timed on its own.  Rows: moc_gcp (the FFN's pre-norm and
+    build's.  Beside the wall-clock step: the model's algorithmic FLOP over
+    it, and one FFN layer of the step's shape timed on its own (GPU-bound,
+    so the two FFNs compare without the host's launch time, which at this
+    size is close to the GPU's work).  Rows: moc_gcp (the FFN's pre-norm and
     residual add fused around it), dense, and moc_gcp with that fusion
     switched off."""
     import torch
@@ -194,21 +172,13 @@ def cfg5_bench(steps: int, gpu_busy: bool = True, only: str | None = None) -> di
         torch.cuda.synchronize()
         dt = (time.perf_counter() - t0) / steps
         peak = torch.cuda.max_memory_allocated()
-        busy, ahead = gpu_only_ms(step, dt * 1e3) if gpu_busy else (None, False)
-        if not ahead:
-            busy = None
         tf = flop / dt / 1e12
         res = {"ms_per_step": round(dt * 1e3, 2), "tokens_per_s": round(16 * 256 / dt, 1),
                "peak_mem_gib": round(peak / 2**30, 3),
                "loss_first": round(float(loss0), 4), "loss_last": round(float(loss), 4),
-               "gpu_only_ms_per_step": None if busy is None else round(busy, 2),
                "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                             "algorithmic_tflop_per_step": round(flop / 1e12, 3)}}
-        if busy is not None:
-            tfb = flop / (busy * 1e-3) / 1e12
-            res["roofline"]["gpu_only"] = {"achieved": round(tfb, 1),
-                                           "frac": round(tfb / BF16_PEAK_TFLOPS, 4)}
         out[row] = res
         log(f"cfg5 {row}: {out[row]}")
         del model, opt
@@ -956,8 +926,78 @@ def cpu_cfg5():
                       f"{cfg.num_hidden_layers} x block"}
 
 
+def trace_summary(d: str, steps: float, headline: bool) -> None:
+    """Markdown summary of a rocprofv3 CSV output directory: the kernels by
+    total time (from *kernel_stats.csv), and with `headline` the GEMM
+    launches of the timed steps of `bench.py --skip-extra` (from
+    *kernel_trace.csv): per launch the mean and median duration over the
+    timed steps, and the union of a step's GEMM intervals."""
+    import csv
+    import glob
+    stats = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+    if stats:
+        rows = list(csv.DictReader(open(stats[0])))
+        tot = sum(float(r["TotalDurationNs"]) for r in rows)
+        print(f"Kernels: {len(rows)}; total kernel time {tot / 1e6:.3f} ms; per step ({steps:g} steps) "
+              f"{tot / 1e6 / steps:.3f} ms\n")
+        print("| kernel | calls | total ms | ms per step | mean us |\n|---|---:|---:|---:|---:|")
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:30]:
+            name = r["Name"] if len(r["Name"]) < 100 else r["Name"][:97] + "..."
+            print(f"| `{name}` | {r['Calls']} | {float(r['TotalDurationNs']) / 1e6:.3f} | "
+                  f"{float(r['TotalDurationNs']) / 1e6 / steps:.3f} | {float(r['AverageNs']) / 1e3:.2f} |")
+    if not headline:
+        return
+    trace = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    ev = []
+    for r in csv.DictReader(open(trace[0])):
+        if "gemm_pp_kernel" in r["Kernel_Name"]:
+            # grid sizes are in work-items: workgroups = grid / workgroup size
+            grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
+            wg = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 1)
+            ev.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), grid // wg, r["Kernel_Name"]))
+    ev.sort()
+    per_step = 7
+    warm, timed = 5, 20  # bench.py's headline: 5 warmup steps, then the timed ones
+    names = ["G, U pair", "D = Z Wd^T", "dWd = dD^T Z", "gZ = dD Wd", "dWg = gG^T X", "dWu = gU^T X",
+             "dX = gG Wg + gU Wu"]
+    by_launch = {n: [] for n in names}
+    unions = []
+    for st in range(warm, warm + timed):
+        step = ev[st * per_step:(st + 1) * per_step]
+        # forward: pair then D; backward: dWd (side stream) and gZ overlap, then dWg, dWu, dX
+        fwd = step[:2]
+        bwd = sorted(step[2:], key=lambda e: (e[2] != 352, e[0]))  # the 352-workgroup launches first
+        w352 = [e for e in bwd if e[2] == 352]
+        other = [e for e in bwd if e[2] != 352]
+        gz = [e for e in other if e[2] != 512][0]
+        dx = [e for e in other if e[2] == 512][0]
+        for n, e in zip(names, [fwd[0], fwd[1], w352[0], gz, w352[1], w352[2], dx]):
+            by_launch[n].append((e[1] - e[0]) / 1e3)
+        iv = sorted((e[0], e[1]) for e in step)
+        tot, cs, ce = 0, iv[0][0], iv[0][1]
+        for a, b in iv[1:]:
+            if a > ce:
+                tot += ce - cs
+                cs, ce = a, b
+            else:
+                ce = max(ce, b)
+        unions.append((tot + ce - cs) / 1e3)
+    print("\n| GEMM launch | trace mean us | trace median us |\n|---|---:|---:|")
+    for n in names:
+        v = by_launch[n]
+        print(f"| {n} | {statistics.mean(v):.1f} | {statistics.median(v):.1f} |")
+    u = statistics.median(unions)
+    flop = 9 * 2.0 * BATCH1B * SEQ1B * D1B * I1B
+    print(f"\nUnion of a timed step's GEMM intervals (median of {timed} steps): {u:.1f} us -> "
+          f"{flop / 1e12:.3f} TFLOP / {u:.1f} us = {flop / (u * 1e-6) / 1e12:.0f} TFLOP/s = "
+          f"{flop / (u * 1e-6) / 1e12 / BF16_PEAK_TFLOPS:.3f} of 2.5 PFLOP/s")
+
+
 def main():
     args = parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.trace_steps, args.trace_headline)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the MoC FFN path has no "
                                    "multi-GPU mode (bench.py --gpus 1)", "n_gpus": args.gpus}))
@@ -1006,7 +1046,7 @@ def main():
     if args.cfg5:
         print(json.dumps({"config": "350m LLaMA training step (config 5), 16x256 tokens, bf16",
                           "steps": args.cfg5_steps,
-                          "result": cfg5_bench(args.cfg5_steps, not args.no_gpu_busy, args.cfg5_row)}))
+                          "result": cfg5_bench(args.cfg5_steps, args.cfg5_row)}))
         return
     from moc_amd import _native
     _native.load()  # the HIP library must be there: no fallback
@@ -1069,7 +1109,7 @@ def main():
         log("config 4: 2:8 prefill")
         configs["4_moc28_prefill_4096"] = moc28_prefill_bench()
         log("config 5: 350m training step")
-        configs["5_350m_step"] = cfg5_bench(args.cfg5_steps, not args.no_gpu_busy)
+        configs["5_350m_step"] = cfg5_bench(args.cfg5_steps)
         if cpu_on:
             log("cpu baselines of configs 1-5")
             configs["1_60m_moc_fwd_f32"]["cpu_baseline"] = cpu_cfg1()

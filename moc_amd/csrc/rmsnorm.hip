@@ -16,8 +16,8 @@
 // reduction.  The backward keeps each wave's dw contribution for its lane's
 // columns in registers across the rows it handles, adds the four waves of a
 // workgroup through LDS and writes one f32 partial row per workgroup; a
-// second kernel sums the partial rows column by column in workgroup order,
-// so dw does not depend on timing.  HBM-bound: the forward moves 2 d bytes
+// second kernel sums the partial rows column by column in a fixed order, so
+// dw does not depend on timing.  HBM-bound: the forward moves 2 d bytes
 // in and 2 d + 4 bytes out per row, the backward 6 d in and 2 d out.
 #include <algorithm>
 
@@ -166,16 +166,36 @@ __global__ __launch_bounds__(64 * kRmsWaves) void rmsnorm_bwd_rows_kernel(
   }
 }
 
-// dw[col] = sum over the partial rows in order, in w's dtype.
+// dw[col] = sum over the partial rows, in w's dtype.  A workgroup of 16 waves
+// takes 64 columns: wave w adds partial rows w, w + 16, ... for its lane's
+// column (each step one coalesced 256-byte row segment; eight loads in
+// flight), then the 16 wave sums are added in wave order through LDS, so
+// the result is the same on every run.
+constexpr int kDwWaves = 16;
 template <bool OUT_F32>
-__global__ __launch_bounds__(256) void rmsnorm_dw_reduce_kernel(const float* __restrict__ part, int nblocks,
-                                                                int d, void* __restrict__ dw) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= d) return;
-  float t = 0.f;
-  for (int b = 0; b < nblocks; ++b) t += part[static_cast<int64_t>(b) * d + col];
-  if (OUT_F32) static_cast<float*>(dw)[col] = t;
-  else static_cast<uint16_t*>(dw)[col] = bf16_rne(t);
+__global__ __launch_bounds__(64 * kDwWaves) void rmsnorm_dw_reduce_kernel(const float* __restrict__ part,
+                                                                          int nblocks, int d, void* __restrict__ dw) {
+  __shared__ float red[kDwWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
+  float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (col < d) {
+    int b = wave;
+    for (; b + 7 * kDwWaves < nblocks; b += 8 * kDwWaves) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] += part[static_cast<int64_t>(b + u * kDwWaves) * d + col];
+    }
+    for (; b < nblocks; b += kDwWaves) t[0] += part[static_cast<int64_t>(b) * d + col];
+  }
+  red[wave][lane] = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+  __syncthreads();
+  if (wave == 0 && col < d) {
+    float s = red[0][lane];
+#pragma unroll
+    for (int v = 1; v < kDwWaves; ++v) s += red[v][lane];
+    if (OUT_F32) static_cast<float*>(dw)[col] = s;
+    else static_cast<uint16_t*>(dw)[col] = bf16_rne(s);
+  }
 }
 
 int rms_blocks(int64_t rows) {
@@ -259,8 +279,8 @@ extern "C" int moc_rmsnorm_backward_bf16(const void* x, int64_t ldx, int64_t row
 #undef MOC_RMS_BWD
   int rc = check_launch("rmsnorm_bwd_rows_kernel");
   if (rc != MOC_OK) return rc;
-  const dim3 grid(static_cast<unsigned>((d + 255) / 256));
-  if (dw_dtype == MOC_F32) rmsnorm_dw_reduce_kernel<true><<<grid, 256, 0, st>>>(part, blocks, (int)d, dw);
-  else rmsnorm_dw_reduce_kernel<false><<<grid, 256, 0, st>>>(part, blocks, (int)d, dw);
+  const dim3 grid(static_cast<unsigned>((d + 63) / 64));
+  if (dw_dtype == MOC_F32) rmsnorm_dw_reduce_kernel<true><<<grid, 64 * kDwWaves, 0, st>>>(part, blocks, (int)d, dw);
+  else rmsnorm_dw_reduce_kernel<false><<<grid, 64 * kDwWaves, 0, st>>>(part, blocks, (int)d, dw);
   return check_launch("rmsnorm_dw_reduce_kernel");
 }
