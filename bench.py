@@ -74,6 +74,9 @@ def parse_args():
                    help="only the 350m-model training step (config 5): tokens/s and peak "
                         "memory, moc_gcp vs dense, one JSON line")
     p.add_argument("--cfg5-steps", type=int, default=10)
+    p.add_argument("--gemm-k-sweep", action="store_true",
+                   help="only time C[16384, N] = A B for N 5461 and 2048 over K 256 ... 8192 "
+                        "(padded outputs) and fit the per-round fixed cost and per-K-tile cost")
     p.add_argument("--trace-summary", metavar="DIR", default=None,
                    help="no GPU work: summarise a rocprofv3 --kernel-trace --stats --output-format csv "
                         "output directory (per-kernel totals; with --trace-headline, the GEMM "
@@ -926,6 +929,47 @@ def cpu_cfg5():
                       f"{cfg.num_hidden_layers} x block"}
 
 
+def gemm_k_sweep() -> dict:
+    """Time C[16384, N] = A[16384, K] B[K, N] (bf16, padded 16-byte aligned
+    outputs) for N in (5461, 2048) and K from 256 to 8192; per N, fit the
+    time per round of 256 tiles as t0 + nK tk (nK = K / 64 K tiles)."""
+    import torch
+    from moc_amd import kernels as K
+    g = torch.Generator(device="cuda").manual_seed(1)
+    m, res = 16384, {}
+    for n in (5461, 2048):
+        out = K.padded_empty(m, n, torch.bfloat16, "cuda")
+        a_all = torch.randn(m, 8192, device="cuda", generator=g).to(torch.bfloat16)
+        w_all = (torch.randn(n, 8192, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        tiles = ((m + 255) // 256) * ((n + 255) // 256)
+        rounds = -(-tiles // K.cu_count(torch.cuda.current_device()))
+        pts = []
+        for kk in (256, 512, 1024, 2048, 4096, 8192):
+            a, w = a_all[:, :kk], w_all[:, :kk]
+            fn = lambda: K.gemm(a, w.t(), out=out)  # noqa: E731
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(15)]
+            for e0, e1 in ev:
+                e0.record()
+                fn()
+                e1.record()
+            torch.cuda.synchronize()
+            us = statistics.median(e0.elapsed_time(e1) for e0, e1 in ev) * 1e3
+            pts.append((kk, us))
+        xs = [kk / 64 for kk, _ in pts]
+        ys = [us / rounds for _, us in pts]
+        mx, my = statistics.mean(xs), statistics.mean(ys)
+        tk = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        res[f"N{n}"] = {"tiles": tiles, "rounds": rounds,
+                        "us_by_K": {str(kk): round(us, 1) for kk, us in pts},
+                        "fit_t0_us_per_round": round(my - tk * mx, 2), "fit_us_per_K_tile": round(tk, 3)}
+        log(f"gemm K sweep N={n}: {res[f'N{n}']}")
+    return res
+
+
 def trace_summary(d: str, steps: float, headline: bool) -> None:
     """Markdown summary of a rocprofv3 CSV output directory: the kernels by
     total time (from *kernel_stats.csv), and with `headline` the GEMM
@@ -1029,6 +1073,11 @@ def main():
                           "reference_a800_ms_per_token": {"dense": 4.310, "global_moc": 4.003,
                                                           "moc_2_8": 3.586},
                           "rows": rows}), flush=True)
+        return
+    if args.gemm_k_sweep:
+        from moc_amd import _native
+        _native.load()
+        print(json.dumps({"gemm_k_sweep": gemm_k_sweep()}), flush=True)
         return
     if args.roofline_only:
         from moc_amd import _native
