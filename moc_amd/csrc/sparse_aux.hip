@@ -212,26 +212,66 @@ __device__ __forceinline__ float rnd(float f) { return bf16_rnd(f); }
 // memory latencies overlap.
 constexpr int kRowPer = 4;
 
-template <typename IdxT, int NT>
+// VEC: the thread's kRowPer entries are consecutive (e0 + kRowPer threadIdx.x
+// + q), so each sparse tensor arrives in one 8-byte load (the indices in
+// kRowPer sizeof(IdxT) bytes) instead of kRowPer 2-byte ones; the caller
+// guarantees k % kRowPer == 0 and aligned rows.  Otherwise the entries are
+// e0 + threadIdx.x + NT q (element loads, any k).
+template <typename IdxT, int NT, bool VEC = false>
 struct RowEntries {
   int64_t ch[kRowPer];
   uint16_t a[kRowPer], b[kRowPer], c[kRowPer];
-  // entries e0 + threadIdx.x + NT q of row `row`; a/b/c from up to
-  // three sparse [rows, k] tensors (null: not loaded)
+  __device__ __forceinline__ static int entry(int e0, int q) {
+    return VEC ? e0 + kRowPer * static_cast<int>(threadIdx.x) + q : e0 + static_cast<int>(threadIdx.x) + NT * q;
+  }
+  __device__ __forceinline__ static void load4(const uint16_t* p, int64_t i, bool ok, uint16_t (&v)[kRowPer]) {
+    const uint2 w = (ok && p) ? *reinterpret_cast<const uint2*>(p + i) : make_uint2(0, 0);
+    v[0] = static_cast<uint16_t>(w.x);
+    v[1] = static_cast<uint16_t>(w.x >> 16);
+    v[2] = static_cast<uint16_t>(w.y);
+    v[3] = static_cast<uint16_t>(w.y >> 16);
+  }
+  // entries of row `row` from entry(e0, .); a/b/c from up to three sparse
+  // [rows, k] tensors (null: not loaded)
   __device__ __forceinline__ void load(const IdxT* idx, const uint16_t* pa, const uint16_t* pb,
                                        const uint16_t* pc, int64_t row, int k, int e0) {
-#pragma unroll
-    for (int q = 0; q < kRowPer; ++q) {
-      const int e = e0 + threadIdx.x + NT * q;
+    if constexpr (VEC) {
+      static_assert(kRowPer == 4, "vector entry loads take four entries");
+      const int e = entry(e0, 0);
       const int64_t i = row * k + e;
       const bool ok = e < k;
-      ch[q] = ok ? static_cast<int64_t>(idx[i]) : -1;
-      a[q] = (ok && pa) ? pa[i] : uint16_t(0);
-      b[q] = (ok && pb) ? pb[i] : uint16_t(0);
-      c[q] = (ok && pc) ? pc[i] : uint16_t(0);
+      load4(pa, i, ok, a);
+      load4(pb, i, ok, b);
+      load4(pc, i, ok, c);
+      if constexpr (sizeof(IdxT) == 2) {
+        uint16_t t[kRowPer];
+        load4(reinterpret_cast<const uint16_t*>(idx), i, ok, t);
+#pragma unroll
+        for (int q = 0; q < kRowPer; ++q) ch[q] = ok ? static_cast<int64_t>(static_cast<int16_t>(t[q])) : -1;
+      } else {
+#pragma unroll
+        for (int q = 0; q < kRowPer; ++q) ch[q] = ok ? static_cast<int64_t>(idx[i + q]) : -1;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kRowPer; ++q) {
+        const int e = entry(e0, q);
+        const int64_t i = row * k + e;
+        const bool ok = e < k;
+        ch[q] = ok ? static_cast<int64_t>(idx[i]) : -1;
+        a[q] = (ok && pa) ? pa[i] : uint16_t(0);
+        b[q] = (ok && pb) ? pb[i] : uint16_t(0);
+        c[q] = (ok && pc) ? pc[i] : uint16_t(0);
+      }
     }
   }
 };
+
+// Stores kRowPer bf16 values of consecutive entries e .. e + 3 (VEC form).
+__device__ __forceinline__ void store4(uint16_t* p, const uint16_t (&v)[kRowPer]) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(v[0] | (static_cast<uint32_t>(v[1]) << 16),
+                                            v[2] | (static_cast<uint32_t>(v[3]) << 16));
+}
 
 template <typename IdxT>
 __global__ __launch_bounds__(kRowThreads) void scatter_rows_kernel(
@@ -256,33 +296,35 @@ __global__ __launch_bounds__(kRowThreads) void scatter_rows_kernel(
 // GCP recompute fused with the scatter of z: s = bf16(SiLU(g)),
 // z = bf16(s * u) per selected entry (torch's F.silu and product on bf16
 // tensors), s to s_s, z into the dense row.
-template <typename IdxT>
+template <typename IdxT, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void gcp_scatter_rows_kernel(
     const uint16_t* __restrict__ g_s, const uint16_t* __restrict__ u_s,
     const IdxT* __restrict__ idx, int k, int64_t inter, uint16_t* __restrict__ s_s,
     uint16_t* __restrict__ z_full, int64_t ld) {
   extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
   const int64_t row = blockIdx.x;
-  RowEntries<IdxT, kRowThreads> r;
+  RowEntries<IdxT, kRowThreads, VEC> r;
   r.load(idx, g_s, u_s, nullptr, row, k, 0);
   row_zero<kRowThreads>(rbuf, ld);
   __syncthreads();
   for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
     if (e0 > 0) r.load(idx, g_s, u_s, nullptr, row, k, e0);
+    uint16_t sv[kRowPer];
 #pragma unroll
     for (int q = 0; q < kRowPer; ++q) {
-      const int e = e0 + threadIdx.x + kRowThreads * q;
-      if (e >= k) continue;
+      const int e = r.entry(e0, q);
       const float s = rnd(silu_f32(bf16_to_f32(r.a[q])));
-      if (s_s) s_s[row * k + e] = to_bf16(s);
+      sv[q] = to_bf16(s);
+      if (!VEC && s_s && e < k) s_s[row * k + e] = sv[q];
       if (r.ch[q] >= 0 && r.ch[q] < inter) rbuf[r.ch[q]] = to_bf16(s * bf16_to_f32(r.b[q]));
     }
+    if (VEC && s_s && r.entry(e0, 0) < k) store4(s_s + row * k + r.entry(e0, 0), sv);
   }
   __syncthreads();
   row_store<kRowThreads>(z_full + row * ld, rbuf, ld);
 }
 
-template <typename IdxT>
+template <typename IdxT, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void forward_aux_rows_kernel(
     const uint16_t* __restrict__ vals, const IdxT* __restrict__ idx,
     const uint16_t* __restrict__ u_full, int64_t u_ld, int k, int64_t inter,
@@ -292,26 +334,55 @@ __global__ __launch_bounds__(kRowThreads) void forward_aux_rows_kernel(
   uint16_t* urow = rbuf;        // [u_ld]
   uint16_t* zrow = rbuf + u_ld;  // [z_ld]
   const int64_t row = blockIdx.x;
-  RowEntries<IdxT, kRowThreads> r;
+  RowEntries<IdxT, kRowThreads, VEC> r;
   r.load(idx, vals, nullptr, nullptr, row, k, 0);
   row_load<kRowThreads>(urow, u_full + row * u_ld, u_ld);
   row_zero<kRowThreads>(zrow, z_ld);
   __syncthreads();
   for (int e0 = 0; e0 < k; e0 += kRowThreads * kRowPer) {
     if (e0 > 0) r.load(idx, vals, nullptr, nullptr, row, k, e0);
+    uint16_t uv[kRowPer], sv[kRowPer], zv[kRowPer];
+    bool all = true;  // every entry of the group valid (VEC: vector stores)
 #pragma unroll
     for (int q = 0; q < kRowPer; ++q) {
       const int64_t ch = r.ch[q];
-      if (ch < 0 || ch >= inter) continue;  // malformed index or past k: never touch memory
-      const int64_t i = row * k + e0 + threadIdx.x + kRowThreads * q;
+      uv[q] = sv[q] = zv[q] = 0;
+      if (ch < 0 || ch >= inter) {  // malformed index or past k: never touch memory
+        all = false;
+        continue;
+      }
+      const int64_t i = row * k + r.entry(e0, q);
       const float g = bf16_to_f32(r.a[q]);
       const uint16_t u_raw = urow[ch];
       const float s = rnd(g * sigmoid_f32(g));
       const uint16_t z = to_bf16(s * bf16_to_f32(u_raw));
-      if (u_s) u_s[i] = u_raw;
-      if (s_s) s_s[i] = to_bf16(s);
-      if (z_s) z_s[i] = z;
+      uv[q] = u_raw;
+      sv[q] = to_bf16(s);
+      zv[q] = z;
+      if (!VEC) {
+        if (u_s) u_s[i] = u_raw;
+        if (s_s) s_s[i] = sv[q];
+        if (z_s) z_s[i] = z;
+      }
       zrow[ch] = z;
+    }
+    if (VEC) {
+      const int e = r.entry(e0, 0);
+      if (all) {
+        const int64_t i = row * k + e;
+        if (u_s) store4(u_s + i, uv);
+        if (s_s) store4(s_s + i, sv);
+        if (z_s) store4(z_s + i, zv);
+      } else {
+#pragma unroll
+        for (int q = 0; q < kRowPer; ++q) {
+          if (r.ch[q] < 0 || r.ch[q] >= inter) continue;
+          const int64_t i = row * k + e + q;
+          if (u_s) u_s[i] = uv[q];
+          if (s_s) s_s[i] = sv[q];
+          if (z_s) z_s[i] = zv[q];
+        }
+      }
     }
   }
   __syncthreads();
@@ -385,7 +456,7 @@ __global__ __launch_bounds__(kRowThreads) void forward_aux_rows_f32_kernel(
     reinterpret_cast<float4*>(z_full + row * z_ld)[c] = reinterpret_cast<const float4*>(zrow)[c];
 }
 
-template <typename IdxT>
+template <typename IdxT, bool VEC>
 __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     const IdxT* __restrict__ idx, const uint16_t* __restrict__ g_s,
     const uint16_t* __restrict__ u_s, const uint16_t* __restrict__ s_s,
@@ -399,7 +470,7 @@ __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
   uint16_t* ggrow = rbuf + gz_ld;          // [width]
   uint16_t* gurow = rbuf + gz_ld + width;  // [width]
   const int64_t row = blockIdx.x;
-  RowEntries<IdxT, kRowThreadsBwd> r;
+  RowEntries<IdxT, kRowThreadsBwd, VEC> r;
   r.load(idx, g_s, u_s, s_s, row, k, 0);
   row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_ld);
   row_zero<kRowThreadsBwd>(ggrow, width);
@@ -448,6 +519,15 @@ inline dim3 grid_for(int64_t n) { return dim3(static_cast<unsigned>((n + 255) / 
 
 bool idx_ok(int d) { return d == MOC_I16 || d == MOC_I32 || d == MOC_I64; }
 
+// The row kernels' vector entry loads: k a multiple of kRowPer, the bf16
+// sparse tensors 8-byte aligned (a row of k entries then starts aligned
+// too) and the indices aligned to kRowPer of their width.
+bool entries_vec_ok(int64_t k, int idx_dtype, const void* idx, const void* a, const void* b, const void* c) {
+  const uintptr_t isz = idx_dtype == MOC_I16 ? 2 : idx_dtype == MOC_I32 ? 4 : 8;
+  auto al = [](const void* p, uintptr_t n) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % n == 0; };
+  return k % kRowPer == 0 && al(idx, kRowPer * isz) && al(a, 8) && al(b, 8) && al(c, 8);
+}
+
 }  // namespace
 }  // namespace moc
 
@@ -482,10 +562,18 @@ extern "C" int moc_sparse_forward_aux(int dtype, const void* topk_vals, const vo
   if (dtype == MOC_BF16 && z_full != nullptr && rows < (1LL << 31) && row_form_ok(z_full, z_ld) &&
       row_form_ok(u_full, u_ld)) {
     const size_t lds = static_cast<size_t>(u_ld + z_ld) * 2;
-#define MOC_FWDR(T)                                                                           \
-  forward_aux_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(     \
-      (const uint16_t*)topk_vals, (const T*)idx, (const uint16_t*)u_full, u_ld, (int)k, inter, \
-      (uint16_t*)u_sparse, (uint16_t*)s_sparse, (uint16_t*)z_sparse, (uint16_t*)z_full, z_ld)
+    // vector entry loads and stores: the inputs and every sparse output aligned
+    const bool vec = entries_vec_ok(k, idx_dtype, idx, topk_vals, u_sparse, s_sparse) &&
+                     entries_vec_ok(k, idx_dtype, nullptr, z_sparse, nullptr, nullptr);
+#define MOC_FWDR(T)                                                                                   \
+  if (vec)                                                                                            \
+    forward_aux_rows_kernel<T, true><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(    \
+        (const uint16_t*)topk_vals, (const T*)idx, (const uint16_t*)u_full, u_ld, (int)k, inter,     \
+        (uint16_t*)u_sparse, (uint16_t*)s_sparse, (uint16_t*)z_sparse, (uint16_t*)z_full, z_ld);      \
+  else                                                                                                \
+    forward_aux_rows_kernel<T, false><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(   \
+        (const uint16_t*)topk_vals, (const T*)idx, (const uint16_t*)u_full, u_ld, (int)k, inter,     \
+        (uint16_t*)u_sparse, (uint16_t*)s_sparse, (uint16_t*)z_sparse, (uint16_t*)z_full, z_ld)
     MOC_IDX_DISPATCH(idx_dtype, MOC_FWDR);
 #undef MOC_FWDR
     return check_launch("forward_aux_rows_kernel");
@@ -615,11 +703,18 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
       row_form_ok(grad_g, out_ld) && row_form_ok(grad_u, out_ld)) {
     hipStream_t st = as_stream(stream);
     const size_t lds = static_cast<size_t>(gz_ld + 2 * out_row_width(inter, out_ld)) * 2;
-#define MOC_BWDR(T)                                                                          \
-  backward_aux_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
-      (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                   \
-      (const uint16_t*)s_sparse, (const uint16_t*)gz_full, gz_ld, (int)k, inter,              \
-      (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld)
+    const bool vec = entries_vec_ok(k, idx_dtype, idx, g_sparse, u_sparse, s_sparse);
+#define MOC_BWDR(T)                                                                                 \
+  if (vec)                                                                                          \
+    backward_aux_rows_kernel<T, true><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>(  \
+        (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                       \
+        (const uint16_t*)s_sparse, (const uint16_t*)gz_full, gz_ld, (int)k, inter,                  \
+        (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld);                                              \
+  else                                                                                              \
+    backward_aux_rows_kernel<T, false><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
+        (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse,                       \
+        (const uint16_t*)s_sparse, (const uint16_t*)gz_full, gz_ld, (int)k, inter,                  \
+        (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld)
     MOC_IDX_DISPATCH(idx_dtype, MOC_BWDR);
 #undef MOC_BWDR
     return check_launch("backward_aux_rows_kernel");
@@ -673,10 +768,16 @@ extern "C" int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const 
               "and <= %lld", (long long)kRowMaxLd);
   hipStream_t st = as_stream(stream);
   const size_t lds = static_cast<size_t>(ld) * 2;
-#define MOC_GCPS(T)                                                                           \
-  gcp_scatter_rows_kernel<T><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(     \
-      (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const T*)idx, (int)k, inter,     \
-      (uint16_t*)s_sparse, (uint16_t*)z_full, ld)
+  const bool vec = entries_vec_ok(k, idx_dtype, idx, g_sparse, u_sparse, s_sparse);
+#define MOC_GCPS(T)                                                                                  \
+  if (vec)                                                                                           \
+    gcp_scatter_rows_kernel<T, true><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(   \
+        (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const T*)idx, (int)k, inter,         \
+        (uint16_t*)s_sparse, (uint16_t*)z_full, ld);                                                 \
+  else                                                                                               \
+    gcp_scatter_rows_kernel<T, false><<<dim3(static_cast<unsigned>(rows)), kRowThreads, lds, st>>>(  \
+        (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const T*)idx, (int)k, inter,         \
+        (uint16_t*)s_sparse, (uint16_t*)z_full, ld)
   MOC_IDX_DISPATCH(idx_dtype, MOC_GCPS);
 #undef MOC_GCPS
   return check_launch("gcp_scatter_rows_kernel");

@@ -551,6 +551,49 @@ def test_sparse_aux_forward_backward(dtype, shape):
         assert torch.equal(fz.cpu(), K().scatter_sparse_to_dense(kz, ti, inter).cpu())
 
 
+@pytest.mark.parametrize("idx_dtype", [torch.int16, torch.int32, torch.int64])
+@pytest.mark.parametrize("k", [1024, 383])
+def test_sparse_aux_row_kernels_vector_and_element_entry_loads(idx_dtype, k):
+    """The row kernels (forward aux, GCP recompute + scatter, backward aux)
+    read a row's sparse entries four at a time (8-byte loads and stores)
+    when k is a multiple of 4 and the rows are aligned, else one by one:
+    both forms give the same bits.  Misaligned copies of the sparse
+    inputs (views one element into a buffer) force the element form."""
+    rows, inter = 256, 5461
+    g = gen(7)
+    G = torch.randn(rows, inter, generator=g).to(torch.bfloat16)
+    GZ = torch.randn(rows, inter, generator=g).to(torch.bfloat16).to(DEV)
+    U = torch.randn(rows, k, generator=g).to(torch.bfloat16)
+    idx = O.topk_indices(G, k)
+    vals = O.gather_rows(G, idx).to(DEV)
+    u_s = U.to(DEV)
+    ti = torch.from_numpy(idx).to(idx_dtype).to(DEV)
+
+    def shifted(t):  # same values, base one element past an aligned buffer
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=DEV)
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    Gd = K().aligned_rows(G.to(DEV))  # 16-byte aligned rows: the row kernel
+    f1 = K().sparse_forward_aux(vals, ti, Gd, inter)
+    f2 = K().sparse_forward_aux(shifted(vals), shifted(ti), Gd, inter)
+    for a, b in zip(f1, f2):
+        assert torch.equal(a, b)
+    s1, z1 = K().gcp_recompute_scatter(vals, u_s, ti, inter)
+    s2, z2 = K().gcp_recompute_scatter(shifted(vals), shifted(u_s), shifted(ti), inter)
+    assert torch.equal(s1, s2) and torch.equal(z1, z2)
+    gg1, gu1 = K().sparse_backward_aux(ti, vals, u_s, s1, GZ, inter)
+    gg2, gu2 = K().sparse_backward_aux(shifted(ti), shifted(vals), shifted(u_s), shifted(s1), GZ, inter)
+    assert torch.equal(gg1, gg2) and torch.equal(gu1, gu2)
+    # and against the oracle
+    rs, rz = O.gcp_recompute(vals.cpu(), U)
+    close(s1, rs, rtol=2e-2, atol=2e-2)
+    gg, gu = O.sparse_backward_aux(idx, vals.cpu(), U, rs, GZ.cpu(), inter)
+    close(gg1, gg, rtol=2e-2, atol=2e-2)
+    close(gu1, gu, rtol=2e-2, atol=2e-2)
+
+
 # ------------------------------------------------------------------- decode
 @pytest.mark.parametrize("nb", [1, 4, 16])
 def test_global_decode_path_1b(nb):
