@@ -32,9 +32,11 @@
 // operand whose K is not a multiple of 64 goes through registers with
 // element masking (one tile per launch).
 //
-// Tiling: 256x256 C tile per workgroup, K step 64, two LDS stages (128 KB).
-// The main kernel (gemm_pp_kernel) runs eight waves of 128x64, two per SIMD,
-// that alternate between MFMA phases and LDS/memory phases (see there); a
+// Tiling: 256x256 C tile per workgroup, K step 64.  The main kernel
+// (gemm_pp_kernel) runs eight waves of 128x64, two per SIMD, that alternate
+// between MFMA phases and LDS/memory phases, its K tiles staged as halves in
+// a five-slot LDS ring (160 KB; two whole stages plus an L2 prefetch for the
+// structured-sparse product) (see there); a
 // four-wave kernel (128x128 per wave, one barrier per K step) covers operands
 // whose buffer offsets could wrap 32 bits.  Workgroup ids are remapped so
 // that each XCD (ids are dealt round-robin over the 8 XCDs) works on a
@@ -73,6 +75,18 @@ constexpr int kSpATile = 256 * 32 * 2;          // SP: packed A tile; its positi
 static_assert(kSpATile + 2048 <= kTileBytes, "SP: packed A and positions share the A stage");
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kLoads == 2 * (kBK / 16), "each k16 step issues two loads per operand");
+// The 512-thread kernel's LDS ring (every product but the structured-sparse
+// one): five 32 KB slots, each holding one half of a K tile of A (its first
+// 16 KB) and of B (the next 16 KB).  A half is what one wave group loads:
+// loads [0, kLoads / 2) or [kLoads / 2, kLoads) of each operand, i.e. rows
+// 0-127 or 128-255 of a KC tile (0-63 or 64-127 of a 128-row A tile) and
+// k-rows 0-31 or 32-63 of an MN tile.  Five slots let group 1 request its
+// half of K tile t + 2 while tiles t and t + 1 are resident.
+constexpr int kSlots = 5;
+constexpr int kSlotBytes = 32 * 1024;
+constexpr int kSlotB = 16 * 1024;  // B's half inside a slot
+constexpr int kRingBytes = kSlots * kSlotBytes;
+static_assert(kRingBytes <= 160 * 1024 && kSinkOffset + 4 <= kRingBytes, "LDS budget");
 
 struct Operand {
   const uint16_t* p;
@@ -312,13 +326,15 @@ struct FragMap {
   }
 
   // so: byte offset of the stage's tile (a multiple of 32 KB, so adding it
-  // before the XOR is the same as after)
-  __device__ __forceinline__ bf16x8_t read(const char* lds, int blk, int ks, uint32_t so) const {
+  // before the XOR is the same as after).  ring: so is the ring slot of the
+  // half that holds the fragment; an MN half holds two k16 steps.
+  __device__ __forceinline__ bf16x8_t read(const char* lds, int blk, int ks, uint32_t so,
+                                           bool ring = false) const {
     if (KC) {
       const char* p = lds + ((base + so) ^ (32u * ks)) + blk * (32 * kBK * 2);
       return __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(p));
     } else {
-      const char* p = lds + ((base + so) ^ (64u * blk)) + ks * 8192;
+      const char* p = lds + ((base + so) ^ (64u * blk)) + (ring ? (ks & 1) : ks) * 8192;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)p);
       const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(p + 4 * 512));
       const i16x4_t v[2] = {lo, hi};
@@ -715,19 +731,20 @@ struct LoadMap {
   }
 
   // Load j of the K tile whose tile_base is b into the tile at LDS byte
-  // `tile` (the placement of TileMap::issue2).
+  // `tile` (the placement of TileMap::issue2), counted from load jbase: the
+  // loads of one half of a tile in an LDS ring slot.
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, uint32_t b,
-                                        uint32_t tile, int wave, int j) const {
+                                        uint32_t tile, int wave, int j, int jbase = 0) const {
     const uint32_t jstride = KC ? static_cast<uint32_t>(4 * kRowsPerLoad * o.ld * 2)
                                 : static_cast<uint32_t>(8 * o.ld * 2);
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + (j * 4 + wave) * 1024);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(tile + ((j - jbase) * 4 + wave) * 1024);
     dma16(rsrc, m0, b + j * jstride);
   }
 
   // KC, K % 8 != 0: zero the elements k >= K of the chunk that straddles K
-  // (its loads must have landed).
-  __device__ __forceinline__ void zero_straddle(char* lds, const Operand& o, int k0,
-                                                uint32_t tile, int wave, int lane, int j0, int j1) const {
+  // (its loads must have landed); loads [j0, j1) placed as by issue.
+  __device__ __forceinline__ void zero_straddle(char* lds, const Operand& o, int k0, uint32_t tile, int wave,
+                                                int lane, int j0, int j1, int jbase = 0) const {
     const int k = k0 + kchunk;
     if (!(k < o.K && o.K < k + 8)) return;
     const int valid = o.K - k;  // 1 .. 7 elements stay
@@ -738,7 +755,7 @@ struct LoadMap {
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       if (j < j0 || j >= j1) continue;
-      uint4* q = reinterpret_cast<uint4*>(lds + tile + (j * 4 + wave) * 1024 + lane * 16);
+      uint4* q = reinterpret_cast<uint4*>(lds + tile + ((j - jbase) * 4 + wave) * 1024 + lane * 16);
       uint4 v = *q;
       v.x &= keep[0];
       v.y &= keep[1];
@@ -915,7 +932,10 @@ void gemm_pp_kernel(GemmArgs g) {
   static_assert(!SHORT || (A_KC && !GU && !SP), "128-row tiles: K-contiguous A, plain products");
   // SHORT: 128 x 256 C tiles (the A tile half as tall; wave tiles 64 x 64)
   constexpr int MI = SHORT ? 2 : 4;  // 32-row blocks of a wave's tile
-  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes];
+  // RING: K tiles staged in the five-slot LDS ring (kSlots); the
+  // structured-sparse product keeps two whole stages and the L2 prefetch
+  constexpr bool RING = !SP;
+  __shared__ __attribute__((aligned(1024))) char lds[RING ? kRingBytes : kLdsBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -960,8 +980,19 @@ void gemm_pp_kernel(GemmArgs g) {
 
   FragMap<A_KC> fa_map;
   FragMap<B_KC> fb_map;
-  fa_map.init(0, wm, lane);
-  fb_map.init(kBOffset, wn, lane);
+  // RING: the rows of a KC operand that a wave reads lie in one half of the
+  // tile (ha, hb), addressed inside that half's region of a slot; an MN
+  // operand's k16 steps 0-1 and 2-3 lie in halves 0 and 1
+  constexpr int kHalfRowsA = SHORT ? 64 : 128;
+  const int ha = RING && A_KC ? wm / kHalfRowsA : 0;
+  const int hb = RING && B_KC ? wn / 128 : 0;
+  if constexpr (RING) {
+    fa_map.init(0, wm - ha * kHalfRowsA, lane);
+    fb_map.init(kSlotB, wn - hb * 128, lane);
+  } else {
+    fa_map.init(0, wm, lane);
+    fb_map.init(kBOffset, wn, lane);
+  }
 
   f32x16_t acc[MI][2];
 #pragma unroll
@@ -1001,6 +1032,25 @@ void gemm_pp_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
       }
+    }
+  };
+  // RING: LDS byte of the slot of half h of K tile t.  Halves are requested
+  // in the order H1(kt0), H0(kt0), H1(kt0 + 1), H0(kt0 + 1), ... (sequence
+  // number 2 (t - kt0) + 1 - h) and take the slots round-robin; the schedule
+  // below has each half dead before its slot comes round again.
+  auto slot_of = [&](int t, int h) -> uint32_t {
+    return static_cast<uint32_t>((2 * (t - kt0) + 1 - h) % kSlots) * kSlotBytes;
+  };
+  auto read_frags_ring = [&](int t) {
+    const uint32_t s0 = slot_of(t, 0), s1 = slot_of(t, 1);
+    const uint32_t sa = ha ? s1 : s0, sb = hb ? s1 : s0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint32_t sk = ks < 2 ? s0 : s1;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) fa[ks][i] = fa_map.read(lds, i, ks, A_KC ? sa : sk, true);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, B_KC ? sb : sk, true);
     }
   };
   // The 32 MFMAs of a K tile (order pinned); SP: 16 structured-sparse ones,
@@ -1147,14 +1197,93 @@ void gemm_pp_kernel(GemmArgs g) {
     if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, SHORT ? j0 / 2 : j0, SHORT ? j1 / 2 : j1);
     if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane, j0, j1);
   };
+  // RING: half h of K tile t into its slot (kRingHalfLoads loads per wave:
+  // A loads [h JA, h JA + JA) and B loads [4h, 4h + 4)), and the K-straddle
+  // fix of that half once it has landed.
+  constexpr int JA = SHORT ? kLoads / 4 : kLoads / 2;
+  constexpr int kRingHalfLoads = JA + kLoads / 2;
+  auto load_half = [&](int t, int h) {
+    const uint32_t sl = lds0 + slot_of(t, h);
+    const bool p1 = DUAL && t >= nk0;
+    const int k0 = (p1 ? t - nk0 : t) * kBK;
+    const Operand& oa = p1 ? g.a[1] : g.a[0];
+    const Operand& ob = p1 ? g.b[1] : g.b[0];
+    const LoadMap<A_KC>& la = p1 ? ma1 : ma0;
+    const LoadMap<B_KC>& lb = p1 ? mb1 : mb0;
+    const uint32_t ba = la.tile_base(oa, k0);
+    // GU: half 1 of the B tile is the W_up rows
+    const bool up = GU && h == 1;
+    const uint32_t bb = up ? mb1.tile_base(g.b[1], k0) : lb.tile_base(ob, k0);
+#pragma unroll
+    for (int jj = 0; jj < kLoads / 2; ++jj) {
+      if (jj < JA) la.issue(p1 ? ra1 : ra0, oa, ba, sl, sw, h * JA + jj, h * JA);
+      if (up) mb1.issue(rb1, g.b[1], bb, sl + kSlotB, sw, 4 * h + jj, 4 * h);
+      else lb.issue(p1 ? rb1 : rb0, ob, bb, sl + kSlotB, sw, 4 * h + jj, 4 * h);
+    }
+  };
+  auto fix_half = [&](int t, int h) {
+    const bool p1 = DUAL && t >= nk0;
+    const Operand& oa = p1 ? g.a[1] : g.a[0];
+    const int k0 = (p1 ? t - nk0 : t) * kBK;
+    if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
+    const uint32_t sl = slot_of(t, h);
+    if (A_KC) ma0.zero_straddle(lds, oa, k0, sl, sw, lane, h * JA, h * JA + JA, h * JA);
+    if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, sl + kSlotB, sw, lane, 4 * h, 4 * h + 4, 4 * h);
+  };
 
-  // The loads of K tile t+1 are split between the groups: group 0 issues
-  // its share at the start of phase 2t, group 1 the rest at the start of
-  // phase 2t+1 (it would otherwise idle at the barrier there), and each
-  // waits for its own before the barrier that ends phase 2t+1.  Issuing a
-  // whole tile from one group stalls that group's phase: the address unit
-  // accepts a 1 KB load every ~25 cycles, 64 per tile.
-  if (grp == 0) {
+  // The loads of a K tile are split between the groups, half 0 from group
+  // 0 and half 1 from group 1, each issued at the start of the group's
+  // memory phase (issuing a whole tile from one group stalls that group's
+  // phase: the address unit accepts a 1 KB load every ~25 cycles, 64 per
+  // tile).
+  // RING: in phase 2t group 0 requests H0(t + 1) and waits for it at the end
+  // of phase 2t + 1; in phase 2t + 1 group 1 requests H1(t + 2) and waits for
+  // H1(t + 1), requested a phase earlier, so neither group waits out a load's
+  // latency in the phase that issued it.  Slot reuse: H0(t + 1) takes the
+  // slot of H1(t - 1) and H1(t + 2) that of H0(t - 1), both last read in
+  // phase 2t - 1.
+  if constexpr (RING) {
+    if (grp == 0) {
+      load_half(kt0, 0);
+      load_half(kt0, 1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      fix_half(kt0, 0);
+      fix_half(kt0, 1);
+      phase_end();
+      for (int t = kt0; t < nk; ++t) {
+        if (t + 1 < nk) load_half(t + 1, 0);
+        read_frags_ring(t);
+        phase_end();  // phase 2t -> 2t+1
+        compute();
+        if (t + 1 < nk) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          fix_half(t + 1, 0);
+        }
+        phase_end();  // phase 2t+1 -> 2t+2
+      }
+    } else {
+      if (kt0 + 1 < nk) load_half(kt0 + 1, 1);
+      phase_end();
+      for (int t = kt0; t < nk; ++t) {
+        if (t > kt0) compute();
+        phase_end();  // phase 2t -> 2t+1
+        const bool ahead = t + 2 < nk;
+        if (ahead) load_half(t + 2, 1);
+        read_frags_ring(t);
+        if (t + 1 < nk) {
+          // H1(t + 1) has landed once at most the loads just issued are in
+          // flight (vector memory loads complete in issue order)
+          if (!ahead) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          else if constexpr (kRingHalfLoads == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+          fix_half(t + 1, 1);
+        }
+        phase_end();  // phase 2t+1 -> 2t+2
+      }
+      compute();
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  } else if (grp == 0) {
     load_tile(kt0, 0, kLoads);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     fix_tile(kt0, 0, kLoads);
