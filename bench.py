@@ -382,7 +382,7 @@ def time_train_layer(m, x, go, steps, warmup, probe: list | None = None,
 # FETCH_SIZE / WRITE_SIZE counter runs in profiles/gemm_GU_pair_traffic.md, each
 # scaled by what the counter reads for a copy kernel of known size
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).
-GEMM_GU_TRAFFIC_BYTES = 1133.3e6 + 358.6e6
+GEMM_GU_TRAFFIC_BYTES = 1120.2e6 + 358.6e6
 # the same for the B=1 decode layer (gate GEMV + fused select/up/down),
 # profiles/decode_B1_traffic.md
 DECODE_B1_TRAFFIC_BYTES = 22.48e6 + 9.33e6
