@@ -35,8 +35,7 @@
 // Tiling: 256x256 C tile per workgroup, K step 64.  The main kernel
 // (gemm_pp_kernel) runs eight waves of 128x64, two per SIMD, that alternate
 // between MFMA phases and LDS/memory phases, its K tiles staged as halves in
-// a five-slot LDS ring (160 KB; two whole stages plus an L2 prefetch for the
-// structured-sparse product) (see there); a
+// a five-slot LDS ring (160 KB; see there); a
 // four-wave kernel (128x128 per wave, one barrier per K step) covers operands
 // whose buffer offsets could wrap 32 bits.  Workgroup ids are remapped so
 // that each XCD (ids are dealt round-robin over the 8 XCDs) works on a
@@ -71,13 +70,12 @@ constexpr int kRowsPerLoad = 64 / kCpr;         // KC rows one wave instruction 
 constexpr int kBufferFlags = 0x00020000;        // raw buffer, 32-bit dwords
 constexpr int kGroupM = 4;                      // M tiles per L2 group
 constexpr uint32_t kOob = 0x80000000u;          // a buffer offset that reads as zero
-constexpr int kSpATile = 256 * 32 * 2;          // SP: packed A tile; its positions follow (2 KB)
-static_assert(kSpATile + 2048 <= kTileBytes, "SP: packed A and positions share the A stage");
+
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kLoads == 2 * (kBK / 16), "each k16 step issues two loads per operand");
-// The 512-thread kernel's LDS ring (every product but the structured-sparse
-// one): five 32 KB slots, each holding one half of a K tile of A (its first
-// 16 KB) and of B (the next 16 KB).  A half is what one wave group loads:
+// The 512-thread kernel's LDS ring: five 32 KB slots, each holding one half
+// of a K tile of A (its first 16 KB) and of B (the next 16 KB).  A half is
+// what one wave group loads:
 // loads [0, kLoads / 2) or [kLoads / 2, kLoads) of each operand, i.e. rows
 // 0-127 or 128-255 of a KC tile (0-63 or 64-127 of a 128-row A tile) and
 // k-rows 0-31 or 32-63 of an MN tile.  Five slots let group 1 request its
@@ -86,7 +84,15 @@ constexpr int kSlots = 5;
 constexpr int kSlotBytes = 32 * 1024;
 constexpr int kSlotB = 16 * 1024;  // B's half inside a slot
 constexpr int kRingBytes = kSlots * kSlotBytes;
-static_assert(kRingBytes <= 160 * 1024 && kSinkOffset + 4 <= kRingBytes, "LDS budget");
+static_assert(kRingBytes <= 160 * 1024, "LDS budget");
+// Structured-sparse product: a half's A region holds its 128 rows of
+// 2:4-packed values (32 per 64-channel K tile: 64 bytes a row) and then
+// their positions (8 bytes a row).
+constexpr int kSpAHalf = 128 * 32 * 2;
+static_assert(kSpAHalf + 128 * 8 <= kSlotB, "SP: packed rows and positions share a half's A region");
+// The fix-up's LDS flag word after the main loop: past every epilogue's
+// staging area (at most 128 KB)
+constexpr int kFlagOffset = kRingBytes - 64;
 
 struct Operand {
   const uint16_t* p;
@@ -668,30 +674,6 @@ void gemm_bf16_kernel(GemmArgs g) {
 // ---------------------------------------------------------------------------
 constexpr int kPpThreads = 512;
 constexpr int kShortMaxKTiles = 40;  // longest K (in 64-deep tiles) run on 128-row tiles
-constexpr int kG0Loads = 4;   // of the 8 loads per operand and wave, those group 0 issues
-
-// One 16-byte load into the LDS sink for line `idx` of slice `slice` (of n)
-// of the K tile at k0: a KC tile is 256 rows of 128 bytes, an MN tile 64
-// k-rows of four 128-byte lines.  Lines past the operand or the slice read
-// as zero.
-template <bool KC, int ROWS = 256>
-__device__ __forceinline__ void prefetch_slice(__amdgpu_buffer_rsrc_t rsrc, const Operand& o, int k0,
-                                               int row0, uint32_t sink, int idx, int slice, int n) {
-  uint32_t off;
-  if (idx >= (KC ? ROWS : 256) / n) {
-    off = kOob;
-  } else if (KC) {
-    const int r = row0 + slice * (ROWS / n) + idx;
-    off = (r < o.ext && k0 < o.K) ? static_cast<uint32_t>((static_cast<int64_t>(r) * o.ld + k0) * 2)
-                                  : kOob;
-  } else {
-    const int kr = k0 + slice * (64 / n) + (idx >> 2);
-    off = kr < o.K ? static_cast<uint32_t>((static_cast<int64_t>(kr) * o.ld + row0 + 64 * (idx & 3)) * 2)
-                   : kOob;
-  }
-  dma16(rsrc, __builtin_amdgcn_readfirstlane(sink), off);
-}
-
 // Direct-to-LDS load offsets of one operand for a wave (index 0-3 within its
 // group): the eight loads of a tile differ by a uniform stride, so only load
 // 0 is kept.
@@ -932,10 +914,8 @@ void gemm_pp_kernel(GemmArgs g) {
   static_assert(!SHORT || (A_KC && !GU && !SP), "128-row tiles: K-contiguous A, plain products");
   // SHORT: 128 x 256 C tiles (the A tile half as tall; wave tiles 64 x 64)
   constexpr int MI = SHORT ? 2 : 4;  // 32-row blocks of a wave's tile
-  // RING: K tiles staged in the five-slot LDS ring (kSlots); the
-  // structured-sparse product keeps two whole stages and the L2 prefetch
-  constexpr bool RING = !SP;
-  __shared__ __attribute__((aligned(1024))) char lds[RING ? kRingBytes : kLdsBytes];
+  // K tiles staged as halves in the five-slot LDS ring (kSlots)
+  __shared__ __attribute__((aligned(1024))) char lds[kRingBytes];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -957,7 +937,6 @@ void gemm_pp_kernel(GemmArgs g) {
   }
   int tm, tn;
   tile_coords(tbid, g.tiles_m, g.tiles_n, tm, tn);
-  const int tn_all = tn;  // column of the concatenated tile grid (L2 prefetch slices)
   if (!GU && !DUAL && !SPLIT && g.ncat_tn > 0 && tn >= g.ncat_tn) {
     tn -= g.ncat_tn;
     g.b[0] = g.b[1];
@@ -980,19 +959,14 @@ void gemm_pp_kernel(GemmArgs g) {
 
   FragMap<A_KC> fa_map;
   FragMap<B_KC> fb_map;
-  // RING: the rows of a KC operand that a wave reads lie in one half of the
-  // tile (ha, hb), addressed inside that half's region of a slot; an MN
+  // The rows of a KC operand that a wave reads lie in one half of the tile
+  // (ha, hb), addressed inside that half's region of a slot; an MN
   // operand's k16 steps 0-1 and 2-3 lie in halves 0 and 1
   constexpr int kHalfRowsA = SHORT ? 64 : 128;
-  const int ha = RING && A_KC ? wm / kHalfRowsA : 0;
-  const int hb = RING && B_KC ? wn / 128 : 0;
-  if constexpr (RING) {
-    fa_map.init(0, wm - ha * kHalfRowsA, lane);
-    fb_map.init(kSlotB, wn - hb * 128, lane);
-  } else {
-    fa_map.init(0, wm, lane);
-    fb_map.init(kBOffset, wn, lane);
-  }
+  const int ha = A_KC ? wm / kHalfRowsA : 0;
+  const int hb = B_KC ? wn / 128 : 0;
+  fa_map.init(0, wm - ha * kHalfRowsA, lane);
+  fb_map.init(kSlotB, wn - hb * 128, lane);
 
   f32x16_t acc[MI][2];
 #pragma unroll
@@ -1004,46 +978,38 @@ void gemm_pp_kernel(GemmArgs g) {
 
   bf16x8_t fa[4][MI], fb[4][2];  // [k16 step][block]  (SP: fa[32-channel step][block])
   uint32_t fm[4];               // SP: positions of the stored A values, per block
-  // SP: the lane's A fragment of block 0, step 0 (row wm + (lane & 31),
-  // logical chunk lane >> 5); step s is chunk 2s + (lane >> 5), one XOR away
-  const uint32_t spa_base =
-      static_cast<uint32_t>((wm + (lane & 31)) * 64 + (((lane >> 5) ^ sp_swz(lane & 15)) << 4));
-  const uint32_t spm_base = static_cast<uint32_t>(kSpATile + (wm + (lane & 31)) * 8 + (lane >> 5) * 4);
-  auto read_frags = [&](int st) {
-    const uint32_t so = st * kTileBytes;
-    if constexpr (SP) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          fa[s][i] = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const uint4*>(lds + ((spa_base + so) ^ (32u * s)) + i * 2048));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fm[i] = *reinterpret_cast<const uint32_t*>(lds + so + spm_base + i * 256);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i) fa[ks][i] = fa_map.read(lds, i, ks, so);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, so);
-      }
-    }
-  };
-  // RING: LDS byte of the slot of half h of K tile t.  Halves are requested
+  // SP: a half's A region holds its 128 packed rows (8 KB, kSpAHalf) and
+  // then their positions (1 KB).  The lane's A fragment of block 0, step 0
+  // (row wm + (lane & 31) of the tile, logical chunk lane >> 5); step s is
+  // chunk 2s + (lane >> 5), one XOR away; and its positions word
+  const int wr = wm - ha * 128 + (lane & 31);  // row inside the half
+  const uint32_t spa_base = static_cast<uint32_t>(wr * 64 + (((lane >> 5) ^ sp_swz(lane & 15)) << 4));
+  const uint32_t spm_base = static_cast<uint32_t>(kSpAHalf + wr * 8 + (lane >> 5) * 4);
+  // LDS byte of the slot of half h of K tile t.  Halves are requested
   // in the order H1(kt0), H0(kt0), H1(kt0 + 1), H0(kt0 + 1), ... (sequence
   // number 2 (t - kt0) + 1 - h) and take the slots round-robin; the schedule
   // below has each half dead before its slot comes round again.
   auto slot_of = [&](int t, int h) -> uint32_t {
     return static_cast<uint32_t>((2 * (t - kt0) + 1 - h) % kSlots) * kSlotBytes;
   };
-  auto read_frags_ring = [&](int t) {
+  auto read_frags = [&](int t) {
     const uint32_t s0 = slot_of(t, 0), s1 = slot_of(t, 1);
     const uint32_t sa = ha ? s1 : s0, sb = hb ? s1 : s0;
+    if constexpr (SP) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          fa[s][i] = __builtin_bit_cast(
+              bf16x8_t, *reinterpret_cast<const uint4*>(lds + ((spa_base + sa) ^ (32u * s)) + i * 2048));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fm[i] = *reinterpret_cast<const uint32_t*>(lds + sa + spm_base + i * 256);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) fb[ks][j] = fb_map.read(lds, j, ks, B_KC ? sb : (ks < 2 ? s0 : s1), true);
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const uint32_t sk = ks < 2 ? s0 : s1;
@@ -1118,92 +1084,46 @@ void gemm_pp_kernel(GemmArgs g) {
     rb1 = make_rsrc(g.b[1]);
   }
   // SP: the 16 wave loads of a packed A tile (load L fills tile rows
-  // 16L .. 16L + 15: lane l row 16L + l/4, slot l % 4) and the 2 of its
-  // positions (load L covers rows 128L .. 128L + 127, two per lane).
+  // 16L .. 16L + 15: lane l row 16L + l/4, slot l % 4; eight per half) and
+  // the 2 of its positions (load L covers rows 128L .. 128L + 127, two per
+  // lane; one per half).
   const __amdgpu_buffer_rsrc_t rm = SP ? __builtin_amdgcn_make_buffer_rsrc(
                                              const_cast<uint32_t*>(g.sp_meta), (short)0,
                                              g.nk[0] * g.sp_rows * 8, kBufferFlags)
                                        : ra0;
   const uint32_t spa_voff = static_cast<uint32_t>(
       (static_cast<int64_t>(row0 + (lane >> 2)) * g.a[0].ld + 8 * ((lane & 3) ^ sp_swz(lane >> 2))) * 2);
-  auto sp_load = [&](int t, int half) {
-    const uint32_t at = lds0 + (t % kStages) * kTileBytes;
-    const uint32_t kofs = static_cast<uint32_t>(t) * 64u;
-    const uint32_t rstride = static_cast<uint32_t>(16 * g.a[0].ld * 2);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int L = 8 * half + 4 * u + sw;
-      uint32_t off = spa_voff + kofs + static_cast<uint32_t>(L) * rstride;
-      asm volatile("" : "+v"(off));
-      dma16(ra0, __builtin_amdgcn_readfirstlane(at + L * 1024), off);
-    }
-    if (half == 1 && sw >= 2) {
-      const int L = sw - 2;
-      const uint32_t off = static_cast<uint32_t>(
-          ((static_cast<int64_t>(t) * g.sp_rows + row0 + 128 * L + 2 * lane) * 8));
-      dma16(rm, __builtin_amdgcn_readfirstlane(at + kSpATile + L * 1024), off);
-    }
-  };
-  // Loads [j0, j1) of A and of B of K tile t into its stage.
-  auto load_tile = [&](int t, int j0, int j1) {
-    const int st = t % kStages;
-    const uint32_t at = lds0 + st * kTileBytes, bt = lds0 + kBOffset + st * kTileBytes;
-    if constexpr (SP) {
-      // A: group 0's share is the first half, group 1's the second
-      for (int half = j0 / kG0Loads; half < j1 / kG0Loads; ++half) sp_load(t, half);
-      const uint32_t bb = mb0.tile_base(g.b[0], t * kBK);
-#pragma unroll
-      for (int j = 0; j < kLoads; ++j)
-        if (j >= j0 && j < j1) mb0.issue(rb0, g.b[0], bb, bt, sw, j);
-      return;
-    }
-    const bool p1 = DUAL && t >= nk0;
-    const int k0 = (p1 ? t - nk0 : t) * kBK;
-    const Operand& oa = p1 ? g.a[1] : g.a[0];
-    const Operand& ob = p1 ? g.b[1] : g.b[0];
-    const LoadMap<A_KC>& la = p1 ? ma1 : ma0;
-    const LoadMap<B_KC>& lb = p1 ? mb1 : mb0;
-    constexpr int kHalf = kLoads / 2;  // GU: loads [kHalf, kLoads) read W_up
-    const uint32_t ba = la.tile_base(oa, k0);
-    const uint32_t bb = GU && j0 >= kHalf ? 0u : lb.tile_base(ob, k0);
-    const uint32_t bu = GU && j1 > kHalf ? mb1.tile_base(g.b[1], k0) : 0u;
-    // SHORT: the 128-row A tile is loads [0, kHalf); a group issues the
-    // half of them that matches its half of B's
-    const int ja0 = SHORT ? j0 / 2 : j0, ja1 = SHORT ? j1 / 2 : j1;
-#pragma unroll
-    for (int j = 0; j < kLoads; ++j) {
-      if (j >= ja0 && j < ja1) la.issue(p1 ? ra1 : ra0, oa, ba, at, sw, j);
-      if (j >= j0 && j < j1) {
-        if (GU && j >= kHalf) mb1.issue(rb1, g.b[1], bu, bt, sw, j);
-        else lb.issue(p1 ? rb1 : rb0, ob, bb, bt, sw, j);
-      }
-    }
-  };
-  // After loads [j0, j1) of tile t have landed: zero KC elements beyond a K
-  // that is not a multiple of 8 (only the last tile of a product can need it).
-  auto fix_tile = [&](int t, int j0, int j1) {
-    const int st = t % kStages;
-    const uint32_t at = st * kTileBytes, bt = kBOffset + st * kTileBytes;
-    const bool p1 = DUAL && t >= nk0;
-    const Operand& oa = p1 ? g.a[1] : g.a[0];
-    const int k0 = (p1 ? t - nk0 : t) * kBK;
-    if (SP) {  // packed A tiles are whole; only a KC B can straddle K
-      if (B_KC && k0 + kBK > g.b[0].K && (g.b[0].K & 7) != 0)
-        mb0.zero_straddle(lds, g.b[0], k0, bt, sw, lane, j0, j1);
-      return;
-    }
-    if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
-    // kchunk depends on the lane only, so the product-0 maps serve both
-    if (A_KC) ma0.zero_straddle(lds, oa, k0, at, sw, lane, SHORT ? j0 / 2 : j0, SHORT ? j1 / 2 : j1);
-    if (B_KC) mb0.zero_straddle(lds, p1 ? g.b[1] : g.b[0], k0, bt, sw, lane, j0, j1);
-  };
-  // RING: half h of K tile t into its slot (kRingHalfLoads loads per wave:
-  // A loads [h JA, h JA + JA) and B loads [4h, 4h + 4)), and the K-straddle
-  // fix of that half once it has landed.
+  // Half h of K tile t into its slot (kRingHalfLoads loads per wave: A
+  // loads [h JA, h JA + JA) and B loads [4h, 4h + 4); SP: see there), and
+  // the K-straddle fix of that half once it has landed (only the last tile
+  // of a product can need it; kchunk depends on the lane only, so the
+  // product-0 maps serve both products).
   constexpr int JA = SHORT ? kLoads / 4 : kLoads / 2;
   constexpr int kRingHalfLoads = JA + kLoads / 2;
   auto load_half = [&](int t, int h) {
     const uint32_t sl = lds0 + slot_of(t, h);
+    if constexpr (SP) {
+      // the packed A rows 128h .. +127 (two loads per wave), their positions
+      // (one load, wave 2 of the group) and B's k-rows of the half
+      const uint32_t kofs = static_cast<uint32_t>(t) * 64u;
+      const uint32_t rstride = static_cast<uint32_t>(16 * g.a[0].ld * 2);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int L = 8 * h + 4 * u + sw;
+        uint32_t off = spa_voff + kofs + static_cast<uint32_t>(L) * rstride;
+        asm volatile("" : "+v"(off));
+        dma16(ra0, __builtin_amdgcn_readfirstlane(sl + (4 * u + sw) * 1024), off);
+      }
+      if (sw == 2) {
+        const uint32_t off = static_cast<uint32_t>(
+            ((static_cast<int64_t>(t) * g.sp_rows + row0 + 128 * h + 2 * lane) * 8));
+        dma16(rm, __builtin_amdgcn_readfirstlane(sl + kSpAHalf), off);
+      }
+      const uint32_t bb = mb0.tile_base(g.b[0], t * kBK);
+#pragma unroll
+      for (int jj = 0; jj < kLoads / 2; ++jj) mb0.issue(rb0, g.b[0], bb, sl + kSlotB, sw, 4 * h + jj, 4 * h);
+      return;
+    }
     const bool p1 = DUAL && t >= nk0;
     const int k0 = (p1 ? t - nk0 : t) * kBK;
     const Operand& oa = p1 ? g.a[1] : g.a[0];
@@ -1225,6 +1145,11 @@ void gemm_pp_kernel(GemmArgs g) {
     const bool p1 = DUAL && t >= nk0;
     const Operand& oa = p1 ? g.a[1] : g.a[0];
     const int k0 = (p1 ? t - nk0 : t) * kBK;
+    if constexpr (SP) {  // packed A tiles are whole; only a KC B can straddle K
+      if (B_KC && k0 + kBK > g.b[0].K && (g.b[0].K & 7) != 0)
+        mb0.zero_straddle(lds, g.b[0], k0, slot_of(t, h) + kSlotB, sw, lane, 4 * h, 4 * h + 4, 4 * h);
+      return;
+    }
     if (k0 + kBK <= oa.K || (oa.K & 7) == 0) return;
     const uint32_t sl = slot_of(t, h);
     if (A_KC) ma0.zero_straddle(lds, oa, k0, sl, sw, lane, h * JA, h * JA + JA, h * JA);
@@ -1235,112 +1160,47 @@ void gemm_pp_kernel(GemmArgs g) {
   // 0 and half 1 from group 1, each issued at the start of the group's
   // memory phase (issuing a whole tile from one group stalls that group's
   // phase: the address unit accepts a 1 KB load every ~25 cycles, 64 per
-  // tile).
-  // RING: in phase 2t group 0 requests H0(t + 1) and waits for it at the end
-  // of phase 2t + 1; in phase 2t + 1 group 1 requests H1(t + 2) and waits for
-  // H1(t + 1), requested a phase earlier, so neither group waits out a load's
-  // latency in the phase that issued it.  Slot reuse: H0(t + 1) takes the
-  // slot of H1(t - 1) and H1(t + 2) that of H0(t - 1), both last read in
-  // phase 2t - 1.
-  if constexpr (RING) {
-    if (grp == 0) {
-      load_half(kt0, 0);
-      load_half(kt0, 1);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      fix_half(kt0, 0);
-      fix_half(kt0, 1);
-      phase_end();
-      for (int t = kt0; t < nk; ++t) {
-        if (t + 1 < nk) load_half(t + 1, 0);
-        read_frags_ring(t);
-        phase_end();  // phase 2t -> 2t+1
-        compute();
-        if (t + 1 < nk) {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          fix_half(t + 1, 0);
-        }
-        phase_end();  // phase 2t+1 -> 2t+2
-      }
-    } else {
-      if (kt0 + 1 < nk) load_half(kt0 + 1, 1);
-      phase_end();
-      for (int t = kt0; t < nk; ++t) {
-        if (t > kt0) compute();
-        phase_end();  // phase 2t -> 2t+1
-        const bool ahead = t + 2 < nk;
-        if (ahead) load_half(t + 2, 1);
-        read_frags_ring(t);
-        if (t + 1 < nk) {
-          // H1(t + 1) has landed once at most the loads just issued are in
-          // flight (vector memory loads complete in issue order)
-          if (!ahead) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          else if constexpr (kRingHalfLoads == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-          else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-          fix_half(t + 1, 1);
-        }
-        phase_end();  // phase 2t+1 -> 2t+2
-      }
-      compute();
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-  } else if (grp == 0) {
-    load_tile(kt0, 0, kLoads);
+  // tile).  In phase 2t group 0 requests H0(t + 1) and waits for it at the
+  // end of phase 2t + 1; in phase 2t + 1 group 1 requests H1(t + 2) and
+  // waits for H1(t + 1), requested a phase earlier, so neither group waits
+  // out a load's latency in the phase that issued it.  Slot reuse: H0(t + 1)
+  // takes the slot of H1(t - 1) and H1(t + 2) that of H0(t - 1), both last
+  // read in phase 2t - 1.
+  if (grp == 0) {
+    load_half(kt0, 0);
+    load_half(kt0, 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    fix_tile(kt0, 0, kLoads);
+    fix_half(kt0, 0);
+    fix_half(kt0, 1);
     phase_end();
     for (int t = kt0; t < nk; ++t) {
-      if (t + 1 < nk) load_tile(t + 1, 0, kG0Loads);
-      read_frags(t % kStages);
+      if (t + 1 < nk) load_half(t + 1, 0);
+      read_frags(t);
       phase_end();  // phase 2t -> 2t+1
       compute();
       if (t + 1 < nk) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        fix_tile(t + 1, 0, kG0Loads);
+        fix_half(t + 1, 0);
       }
       phase_end();  // phase 2t+1 -> 2t+2
     }
   } else {
-    // L2 prefetch, shared out over the workgroups of an XCD: the 32
-    // concurrent tiles of an XCD form a 4 (M) x 8 (N) block (see tile_coords),
-    // so A tile tm is wanted by eight workgroups and B tile tn by four.  Each
-    // pulls its own eighth of A (by tn % 8, wave 0 of the group) and quarter
-    // of B (by tm % 4, wave 1): every line of the block is requested about
-    // once, ahead of the direct-to-LDS loads that then hit in L2.  Waves 0
-    // and 1 issue exactly one load per prefetch, the others none.
-    auto tile_prefetch = [&](int t) {
-      const uint32_t sink = lds0 + kSinkOffset;
-      const bool p1 = DUAL && t >= nk0;
-      const int k0 = (p1 ? t - nk0 : t) * kBK;
-      if (sw == 0) {
-        const Operand& o = p1 ? g.a[1] : g.a[0];
-        // SP: the packed tile's 64-byte row segments (k0 in stored values)
-        prefetch_slice<A_KC, SHORT ? 128 : 256>(p1 ? ra1 : ra0, o, SP ? t * 32 : k0, row0, sink, lane,
-                                                tn_all & 7, 8);
-      } else if (sw == 1) {
-        const Operand& o = p1 ? g.b[1] : g.b[0];
-        if (GU && (tm & 3) >= 2)  // quarters 2-3 of the B tile are W_up rows
-          prefetch_slice<B_KC>(rb1, g.b[1], k0, col0 - 128, sink, lane, tm & 3, 4);
-        else
-          prefetch_slice<B_KC>(p1 ? rb1 : rb0, o, k0, col0, sink, lane, tm & 3, 4);
-      }
-    };
-#pragma unroll
-    for (int p = 1; p <= kPrefetch; ++p)
-      if (kt0 + p < nk) tile_prefetch(kt0 + p);
+    if (kt0 + 1 < nk) load_half(kt0 + 1, 1);
     phase_end();
     for (int t = kt0; t < nk; ++t) {
       if (t > kt0) compute();
       phase_end();  // phase 2t -> 2t+1
-      const bool pf = t + 1 + kPrefetch < nk;
-      if (t + 1 < nk) load_tile(t + 1, kG0Loads, kLoads);
-      if (pf) tile_prefetch(t + 1 + kPrefetch);
-      read_frags(t % kStages);
+      const bool ahead = t + 2 < nk;
+      if (ahead) load_half(t + 2, 1);
+      read_frags(t);
       if (t + 1 < nk) {
-        // the prefetch (one load, waves 0-1) was issued after this tile's
-        // loads and may stay in flight: vector memory loads retire in order
-        if (pf && sw < 2) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        fix_tile(t + 1, kG0Loads, kLoads);
+        // H1(t + 1) has landed once at most the loads just issued are in
+        // flight (vector memory loads complete in issue order)
+        if (!ahead) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if (SP && sw == 2) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");  // + the positions
+        else if constexpr (kRingHalfLoads == 8 && !SP) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        fix_half(t + 1, 1);
       }
       phase_end();  // phase 2t+1 -> 2t+2
     }
@@ -1355,7 +1215,7 @@ void gemm_pp_kernel(GemmArgs g) {
     if constexpr (SP) store_tile_t<OUT_F32, 2>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
     else store_tile_w<OUT_F32, 2, MI>(gs, lds, acc, row0, col0, wm, wn, wave, lane);
   } else {
-    if (part >= 0 && !fix_arrive<MI>(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kSinkOffset)))
+    if (part >= 0 && !fix_arrive<MI>(g, acc, slot, part, tid, reinterpret_cast<int*>(lds + kFlagOffset)))
       return;
     if constexpr (SP) store_tile_t<OUT_F32, 2>(g, lds, acc, row0, col0, wm, wn, wave, lane);
     else store_tile_w<OUT_F32, 2, MI>(g, lds, acc, row0, col0, wm, wn, wave, lane);
