@@ -383,9 +383,9 @@ def time_train_layer(m, x, go, steps, warmup, probe: list | None = None,
 # scaled by what the counter reads for a copy kernel of known size
 # (FETCH_SIZE x 2.000, WRITE_SIZE x 1.000).
 GEMM_GU_TRAFFIC_BYTES = 1120.2e6 + 358.6e6
-# the same for the B=1 decode layer (gate GEMV + fused select/up/down),
-# profiles/decode_B1_traffic.md
-DECODE_B1_TRAFFIC_BYTES = 22.48e6 + 9.33e6
+# the same for the B=1 decode layer (the gate + dense-U GEMV pair, then the
+# column-owning select/down kernel), profiles/decode_B1_traffic.md
+DECODE_B1_TRAFFIC_BYTES = 44.79e6 + 0.09e6 + 4.58e6
 
 
 def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
@@ -1142,7 +1142,8 @@ def main():
     d1 = dec[1]
     roof_dec = {"bound": "hbm", "achieved": d1["achieved_GBs"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": d1["frac_hbm"], "traffic": DECODE_B1_TRAFFIC_BYTES,
-                "kernel": "decode layer (gate GEMV + Top-K + selected Up + selected Down), B=1",
+                "kernel": "decode layer (gate + dense-U GEMV pair, then Top-K + z + selected Down "
+                          "in one launch), B=1",
                 "us": d1["us_median"], "bytes": d1["bytes"]}
     cpu_on = not args.no_cpu_baseline
     if not args.skip_extra:

@@ -382,22 +382,37 @@ int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, 
                                         void* y, void* idx_out, void* workspace,
                                         int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes moc_global_decode_bf16 needs: the after-gate workspace
- * followed by the gate scores. */
+/* Workspace bytes moc_global_decode_bf16 and
+ * moc_global_decode_rmsnorm_residual_bf16 need (the after-gate workspace's
+ * 64 KB of counters, then G and U, or the after-gate workspace and G). */
 int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, int64_t k, int64_t hidden);
 
-/* The global-MoC decode layer from x (nb <= 16 tokens): the gate projection
- * G = x W_gate^T (bf16, into the workspace) and then
- * moc_global_after_gate_bf16 on it, i.e. module.gate_proj(x) followed by
- * moc_native::optimized_global_after_gate_bf16 (moc/inference/
- * inference_ffn.py:181-196, optimized_global_moc_ext.cu:457-540).  From 4
- * tokens on the dense U = x W_up^T the after-gate kernel uses is computed in
- * the same GEMV launch as G.  Same selection, rounding and results as the
- * two calls; same workspace rules (64 KB of counters at its start, zero
- * before the first call). */
+/* The global-MoC decode layer from x (nb <= 16 tokens): module.gate_proj(x)
+ * followed by moc_native::optimized_global_after_gate_bf16 (moc/inference/
+ * inference_ffn.py:181-196, optimized_global_moc_ext.cu:457-540).  Where
+ * hidden % 256 == 0, inter <= 8192 and k <= 4096: G = x W_gate^T and the
+ * dense U = x W_up^T in one GEMV launch, then one launch in which each
+ * workgroup ranks a token's G row and sums the token's selected channels
+ * for a block of output columns; otherwise the gate GEMV (with the dense U
+ * from 4 tokens) and moc_global_after_gate_bf16.  The selection (idx_out)
+ * is the Top-K's bit for bit, z rounds as in moc_global_after_gate_bf16,
+ * and y is the same sum in another f32 order.  Same workspace rules (64 KB
+ * of counters at its start, zero before the first call, left zero). */
 int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
                            const void* w_up, int64_t inter, const void* w_down_t, int64_t k, void* y,
                            void* idx_out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The decoder layer's FFN half y = bf16(x + bf16(FFN(RMSNorm(x)))) for nb <= 4
+ * tokens (benchmark_decode.py:101-109,303): the norm (rounding as in
+ * moc_gemv_rmsnorm_bf16) inside the gate/up GEMV pair, the residual added in
+ * the last step of the after-gate kernel.  hidden % 256 == 0 and <= 4096,
+ * inter <= 8192, k <= 4096; workspace of moc_global_decode_workspace_size;
+ * y must not alias x. */
+int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb, int64_t hidden,
+                                            const void* norm_w, float eps, const void* w_gate,
+                                            const void* w_up, int64_t inter, const void* w_down_t,
+                                            int64_t k, void* y, void* idx_out, void* workspace,
+                                            int64_t workspace_bytes, void* stream);
 
 /* Bytes of the library's own device scratch array (one per GPU, held until
  * the process ends) behind moc_global_after_gate_noalloc_bf16. */

@@ -206,16 +206,22 @@ __device__ __forceinline__ uint32_t pack_group_2of8(int p1, uint16_t v1, int p2,
 // Positions byte of an 8-group with nothing to pack (zeros at 0, 1 per half).
 constexpr uint32_t kPackEmpty2of8 = 0x44u;
 
-// Dot product of 8 bf16 pairs (two 16-byte chunks) accumulated in f32.
+// Dot product of 8 bf16 pairs (two 16-byte chunks) accumulated in f32: one
+// v_dot2c_f32_bf16 per packed pair (acc + a0 b0 + a1 b1; the bf16 products
+// are exact in f32), where unpacking each half and an FMA per product took
+// six VALU instructions per pair.
+typedef __bf16 dot_bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dot_bf16x2_t, a),
+                                         __builtin_bit_cast(dot_bf16x2_t, b), acc, false);
+}
+
 __device__ __forceinline__ float dot8(uint4 a, uint4 b, float acc) {
-  const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-  const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc = fmaf(__uint_as_float(aw[i] << 16), __uint_as_float(bw[i] << 16), acc);
-    acc = fmaf(__uint_as_float(aw[i] & 0xFFFF0000u), __uint_as_float(bw[i] & 0xFFFF0000u), acc);
-  }
-  return acc;
+  acc = dot2_bf16(a.x, b.x, acc);
+  acc = dot2_bf16(a.y, b.y, acc);
+  acc = dot2_bf16(a.z, b.z, acc);
+  return dot2_bf16(a.w, b.w, acc);
 }
 
 // RMSNorm of 8 bf16 values with the row's factor r = 1 / sqrt(mean(x^2) +

@@ -446,6 +446,68 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const uint16_t* __restri
   }
 }
 
+// The gate and up projections of the same channels in one wave: wave r
+// requests row r of both W and W2 at once (two 4 KB rows at hidden 2048)
+// and writes y[., r] and y2[., r].  Half the waves of the two-range pair
+// form above, so the whole launch is resident in one round.  Same lane
+// split, dot products and wave sums as gemv_rows_kernel: same bits.
+template <int NB, int CHN>
+__global__ __launch_bounds__(256) void gemv_dual_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                             const uint16_t* __restrict__ W,
+                                                             const uint16_t* __restrict__ W2, int64_t ldw,
+                                                             int rows, int hidden, uint16_t* __restrict__ y,
+                                                             uint16_t* __restrict__ y2, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = hidden / 8;
+  uint4 wv[CHN], wv2[CHN];
+#pragma unroll
+  for (int i = 0; i < CHN; ++i) {
+    const int c = lane + 64 * i;
+    const int64_t o = static_cast<int64_t>(row) * ldw + c * 8;
+    wv[i] = c < nch ? *reinterpret_cast<const uint4*>(W + o) : make_uint4(0, 0, 0, 0);
+    wv2[i] = c < nch ? *reinterpret_cast<const uint4*>(W2 + o) : make_uint4(0, 0, 0, 0);
+  }
+  float acc[NB], acc2[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    acc[t] = 0.f;
+    acc2[t] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CHN; ++i) {
+      const int c = lane + 64 * i;
+      const uint4 xv = c < nch ? *reinterpret_cast<const uint4*>(x + t * ldx + c * 8) : make_uint4(0, 0, 0, 0);
+      acc[t] = dot8(wv[i], xv, acc[t]);
+      acc2[t] = dot8(wv2[i], xv, acc2[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    const float tot = wave_sum(acc[t]), tot2 = wave_sum(acc2[t]);
+    if (lane == 0) {
+      y[t * ldy + row] = f32_to_bf16(tot);
+      y2[t * ldy + row] = f32_to_bf16(tot2);
+    }
+  }
+}
+
+template <int NB>
+void launch_gemv_dual_rows(const void* x, int64_t ldx, const void* W, const void* W2, int64_t ldw, int rows,
+                           int hidden, void* y, void* y2, int64_t ldy, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+  const int chn = (hidden / 8 + 63) / 64;
+#define MOC_GD(C)                                                                                      \
+  gemv_dual_rows_kernel<NB, C><<<grid, block, 0, st>>>((const uint16_t*)x, ldx, (const uint16_t*)W,     \
+                                                       (const uint16_t*)W2, ldw, rows, hidden, (uint16_t*)y, \
+                                                       (uint16_t*)y2, ldy)
+  if (chn <= 1) MOC_GD(1);
+  else if (chn <= 2) MOC_GD(2);
+  else if (chn <= 4) MOC_GD(4);
+  else MOC_GD(8);
+#undef MOC_GD
+}
+
 template <int NB, bool NORM = false>
 void launch_gemv_rows(const void* x, int64_t ldx, const void* W, int64_t ldw, int rows, int hidden,
                       void* y, int64_t ldy, hipStream_t st, const void* norm_w = nullptr,
@@ -508,7 +570,7 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
   constexpr int S = kUdThreads / QN;    // row segments summed in parallel
   static_assert(S * QN == kUdThreads, "CW / 8 must divide the workgroup");
   constexpr int NW = kUdThreads / 64;
-  __shared__ uint32_t sel_lds[select_lds_dwords<kSelWaves, kSelCopies>()];
+  __shared__ __attribute__((aligned(16))) uint32_t sel_lds[select_lds_dwords<kSelWaves, kSelCopies>()];
   __shared__ __attribute__((aligned(16))) uint32_t row_lds[kUdThreads * L / 2];  // raw gate row
   __shared__ int sch[kFusedMaxSel];
   __shared__ float sv[kFusedMaxSel];  // bf16(SiLU(g)), then z
@@ -536,17 +598,23 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     select_threshold<kSelWaves, kSelCopies, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k),
                                                                       sel_lds, thr, krem);
     select_ranks<kSelWaves, kSelCopies, L, true>(w, thr, krem, sel_lds, take, first);
-    const uint16_t* raw = reinterpret_cast<const uint16_t*>(row_lds);
-    select_emit<L>(take, c0, first, [&](int c, uint32_t pos) {
-      if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) {
-        sch[pos - lo] = c;
-        sv[pos - lo] = round_bf16(silu_f32(bf16_to_f32(raw[c])));
-        // the selection itself, written once per token (column block 0)
-        if (idx_out != nullptr && cb == 0) idx_out[static_cast<int64_t>(b) * k + pos] = c;
-      }
-    });
+    // only threads holding ranks of the slice list their channels (ids
+    // only: SiLU is taken where z is formed, in parallel)
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int d = 0; d < (L + 31) / 32; ++d) cnt += __popc(take[d]);
+    if (static_cast<int>(first) < hi && static_cast<int>(first + cnt) > lo) {
+      select_emit<L>(take, c0, first, [&](int c, uint32_t pos) {
+        if (static_cast<int>(pos) >= lo && static_cast<int>(pos) < hi) sch[pos - lo] = c;
+      });
+    }
   }
   __syncthreads();
+  const uint16_t* raw = reinterpret_cast<const uint16_t*>(row_lds);
+  // the selection itself, written once per token (column block 0)
+  if (idx_out != nullptr && cb == 0) {
+    for (int e = tid; e < nsel; e += kUdThreads) idx_out[static_cast<int64_t>(b) * k + lo + e] = sch[e];
+  }
 
   // 1. first batch of W_down^T segments in flight, then selected Up * SiLU
   const int q = tid % QN, sl = tid / QN;
@@ -560,9 +628,11 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
   }
   const int nch = hidden / 8;
   const uint16_t* xb = x + static_cast<int64_t>(b) * hidden;
+  // z = bf16(bf16(SiLU(g)) * bf16(u))
+  auto silu_g = [&](int e) { return round_bf16(silu_f32(bf16_to_f32(raw[sch[e]]))); };
   if (up_ld > 0) {  // w_up holds the tokens' dense U rows [nb, up_ld]
     for (int e = tid; e < nsel; e += kUdThreads)
-      sv[e] = round_bf16(sv[e] * bf16_to_f32(w_up[static_cast<int64_t>(b) * up_ld + sch[e]]));
+      sv[e] = round_bf16(silu_g(e) * bf16_to_f32(w_up[static_cast<int64_t>(b) * up_ld + sch[e]]));
   }
   for (int e0 = wave * kUpPerWave; up_ld == 0 && e0 < nsel; e0 += kUpPerWave * NW) {
     float acc[kUpPerWave] = {};
@@ -589,7 +659,7 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     for (int u = 0; u < kUpPerWave; ++u) {
       const float tot = wave_sum(acc[u]);
       const int e = e0 + u;
-      if (lane == 0 && e < nsel) sv[e] = round_bf16(sv[e] * round_bf16(tot));
+      if (lane == 0 && e < nsel) sv[e] = round_bf16(silu_g(e) * round_bf16(tot));
     }
   }
   __syncthreads();
@@ -673,6 +743,168 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     y[o] = res ? f32_to_bf16(bf16_to_f32(res[o]) + round_bf16(t)) : f32_to_bf16(t);
   }
   if (tid == 0) cnt[b * CB + cb] = 0;  // ready for the next call
+}
+
+// ---------------------------------------------------------------------------
+// Decode after the gate from the tokens' dense U rows (written together with
+// G by the gate/up GEMV pair).  Workgroup (b, cb): token b and the CW output
+// columns [cb CW, cb CW + CW), over every selected channel of the token.
+//  (0) token b's G and U rows are staged in LDS with one round of loads; the
+//      order keys of G and the selection as in select_up_down_kernel
+//      (select.h), every selected channel listed in rank (= channel) order;
+//  (1) thread (r, q) requests the W_down^T row segments (8 columns q of the
+//      block) of the ranks r, r + R, ... (up to kSdBatch in flight), and
+//      while they are in flight z_e = bf16(bf16(SiLU(g_c)) * bf16(u_c)) is
+//      formed for every rank e, one rank per thread;
+//  (2) y[b, cols] = sum_e z_e W_down^T[c_e, cols]: the R slot sums of each
+//      column are added in slot order.
+// Every workgroup of a token ranks the row itself; the output of a column
+// block is summed inside one workgroup, so no partial sums, arrival counters
+// or final-sum step follow (the selected-row kernel above needs all three:
+// its workgroups split the ranks of a column block).  Workgroups are ordered
+// so that the column blocks of one XCD are contiguous (CB a multiple of 8):
+// the tokens' workgroups of a block, which read the same W_down^T rows where
+// their selections meet, and blocks sharing 128-byte lines use one L2.
+// Rows of G and U: pitch ld (a multiple of 8), 16-byte aligned; inter <=
+// kSdMaxInter, k <= kSdMaxK.
+// ---------------------------------------------------------------------------
+constexpr int kSdThreads = 512;
+constexpr int kSdMaxInter = 8192;
+constexpr int kSdMaxK = 4096;
+constexpr int kSdBatch = 16;
+
+template <int L, int CW>
+__global__ __launch_bounds__(kSdThreads) void select_down_kernel(
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ld, int inter, int k,
+    int hidden, int CB, const uint16_t* __restrict__ wdt, uint16_t* __restrict__ y,
+    const uint16_t* __restrict__ res, int* __restrict__ idx_out) {
+  constexpr int NW = kSdThreads / 64;
+  constexpr int CPT = L / 8;          // 16-byte chunks of a row per thread
+  constexpr int Q = CW / 8;           // 16-byte chunks per row segment
+  constexpr int R = kSdThreads / Q;   // rank slots summed in parallel
+  static_assert(R * Q == kSdThreads && R * (CW + 1) >= kSdThreads, "CW / 8 must divide the workgroup");
+  __shared__ __attribute__((aligned(16))) uint32_t sel_lds[select_lds_dwords<NW, kSelCopies>()];
+  __shared__ __attribute__((aligned(16))) uint4 g_st[kSdThreads * CPT];
+  __shared__ __attribute__((aligned(16))) uint4 u_st[kSdThreads * CPT];
+  __shared__ uint16_t sch[kSdMaxK];
+  __shared__ float zs[kSdMaxK];
+  __shared__ float red[R][CW + 1];
+
+  const int tid = threadIdx.x;
+  int b, cb;
+  if (CB % 8 == 0) {
+    const int xcd = static_cast<int>(blockIdx.x) & 7, s = static_cast<int>(blockIdx.x) >> 3;
+    const int per = CB / 8;
+    cb = xcd * per + s % per;
+    b = s / per;
+  } else {
+    b = static_cast<int>(blockIdx.x) / CB;
+    cb = static_cast<int>(blockIdx.x) - b * CB;
+  }
+
+  // 0. the token's G and U rows in LDS, G's keys in registers, selection
+  const uint4* g4 = reinterpret_cast<const uint4*>(gate + static_cast<int64_t>(b) * ld);
+  const uint4* u4 = reinterpret_cast<const uint4*>(up + static_cast<int64_t>(b) * ld);
+  const int nch = (inter + 7) / 8;
+  {
+    uint4 gv[CPT], uv[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int ch = tid + kSdThreads * i;
+      gv[i] = ch < nch ? g4[ch] : make_uint4(0, 0, 0, 0);
+      uv[i] = ch < nch ? u4[ch] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      g_st[tid + kSdThreads * i] = gv[i];
+      u_st[tid + kSdThreads * i] = uv[i];
+    }
+  }
+  __syncthreads();
+  {
+    const int c0 = tid * L;
+    uint32_t w[sel_words<true, L>()];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const uint4 a = g_st[tid * CPT + i];
+      w[4 * i + 0] = a.x; w[4 * i + 1] = a.y; w[4 * i + 2] = a.z; w[4 * i + 3] = a.w;
+    }
+    raw_to_keys<true, L>(inter, c0, 0, [](uint32_t r) { return r; }, w);
+    uint32_t thr, krem, take[(L + 31) / 32], first;
+    select_threshold<NW, kSelCopies, sel_words<true, L>(), 16>(w, static_cast<uint32_t>(k), sel_lds, thr,
+                                                               krem);
+    select_ranks<NW, kSelCopies, L, true>(w, thr, krem, sel_lds, take, first);
+    select_emit<L>(take, c0, first, [&](int c, uint32_t pos) { sch[pos] = static_cast<uint16_t>(c); });
+  }
+  __syncthreads();
+
+  // 1. the first batch of W_down^T segments in flight, then z for every rank
+  //    (and the selection itself, once per token)
+  const int q = tid % Q, r = tid / Q;
+  const int col = cb * CW + q * 8;
+  uint4 dv[kSdBatch];
+#pragma unroll
+  for (int j = 0; j < kSdBatch; ++j) {
+    const int e = r + R * j;
+    dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+                  : make_uint4(0, 0, 0, 0);
+  }
+  {
+    const uint16_t* graw = reinterpret_cast<const uint16_t*>(g_st);
+    const uint16_t* uraw = reinterpret_cast<const uint16_t*>(u_st);
+    const bool write_idx = idx_out != nullptr && cb == 0;
+    for (int e = tid; e < k; e += kSdThreads) {
+      const int c = sch[e];
+      zs[e] = round_bf16(round_bf16(silu_f32(bf16_to_f32(graw[c]))) * bf16_to_f32(uraw[c]));
+      if (write_idx) idx_out[static_cast<int64_t>(b) * k + e] = c;
+    }
+  }
+  __syncthreads();
+
+  // 2. column sums over the ranks
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int e0 = r;; e0 += R * kSdBatch) {
+#pragma unroll
+    for (int j = 0; j < kSdBatch; ++j) {
+      const int e = e0 + R * j;
+      const float zz = e < k ? zs[e] : 0.f;
+      const uint32_t a[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] = fmaf(zz, __uint_as_float(a[i] << 16), acc[2 * i]);
+        acc[2 * i + 1] = fmaf(zz, __uint_as_float(a[i] & 0xFFFF0000u), acc[2 * i + 1]);
+      }
+    }
+    if (e0 + R * kSdBatch >= k) break;
+#pragma unroll
+    for (int j = 0; j < kSdBatch; ++j) {
+      const int e = e0 + R * kSdBatch + R * j;
+      dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[r][q * 8 + i] = acc[i];
+  __syncthreads();
+  // thread (g, c) of G = 512 / CW groups adds the slots g, g + G, ... of
+  // column c; then the G group sums in group order
+  constexpr int G = kSdThreads / CW;
+  {
+    const int c = tid % CW, g = tid / CW;
+    float t = 0.f;
+    for (int rr = g; rr < R; rr += G) t += red[rr][c];
+    __syncthreads();
+    reinterpret_cast<float*>(red)[tid] = t;  // red holds R (CW + 1) >= 512 floats
+  }
+  __syncthreads();
+  if (tid < CW) {
+    const float* flat = reinterpret_cast<const float*>(red);
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) t += flat[g * CW + tid];
+    const int64_t o = static_cast<int64_t>(b) * hidden + cb * CW + tid;
+    y[o] = res ? f32_to_bf16(bf16_to_f32(res[o]) + round_bf16(t)) : f32_to_bf16(t);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -872,6 +1104,23 @@ void launch_fused(const void* x, int hidden, const void* gate, int inter, int k,
   else if (per <= 24) MOC_FU(24);
   else MOC_FU(32);
 #undef MOC_FU
+}
+
+// Column-owning after-gate launch (select_down_kernel), CW columns per
+// workgroup.
+template <int CW>
+void launch_select_down_cw(const void* g, const void* u, int64_t ld, int nb, int inter, int k, int hidden,
+                           const void* wdt, void* y, const void* res, int* idx_out, hipStream_t st) {
+  const int CB = hidden / CW;
+  const dim3 grid(static_cast<unsigned>(nb * CB)), block(kSdThreads);
+  const int per = (inter + kSdThreads - 1) / kSdThreads;
+#define MOC_SD(N)                                                                                  \
+  select_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)g, (const uint16_t*)u, ld, inter, k, \
+                                                     hidden, CB, (const uint16_t*)wdt, (uint16_t*)y,      \
+                                                     (const uint16_t*)res, idx_out)
+  if (per <= 8) MOC_SD(8);
+  else MOC_SD(16);
+#undef MOC_SD
 }
 
 }  // namespace
@@ -1120,13 +1369,71 @@ extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores
                            workspace, workspace_bytes, stream);
 }
 
-// The whole decode layer from x: the gate projection (with, from 4 tokens
-// on, the dense U of the same tokens in the same GEMV launch: two
-// projections of one x stream as one pass over both weights), then the
-// after-gate kernel.  Workspace: the after-gate workspace, then G.
+// The whole decode layer from x.  Where select_down_kernel fits the shape:
+// G and the dense U of every token in one GEMV launch (two projections of
+// one x stream), then the column-owning after-gate kernel; G and U rows at
+// a pitch of a multiple of 8, after the after-gate workspace's counters
+// (which this path leaves as they are).  Otherwise: the gate projection
+// (with, from 4 tokens on, the dense U in the same launch), then
+// select_up_down_kernel; workspace: the after-gate workspace, then G.
+namespace {
+inline int64_t sd_pitch(int64_t inter) { return (inter + 7) / 8 * 8; }
+
+inline bool sd_fits(int64_t nb, int64_t inter, int64_t k, int64_t hidden) {
+  return nb >= 1 && nb <= 16 && inter <= kSdMaxInter && k <= kSdMaxK && hidden % 256 == 0;
+}
+}  // namespace
+
+namespace {
+// The column-owning layer: G and U of every token (of RMSNorm(x) when
+// norm_w != nullptr) in one GEMV launch, then select_down_kernel (with the
+// residual added when res != nullptr).  Workspace after the counters: U, G
+// (pitch sd_pitch(inter)), then xn [nb, hidden].
+int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm_w, float eps,
+                     const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t, int64_t k,
+                     const void* res, void* y, void* idx_out, char* ws, hipStream_t st) {
+  const int64_t pitch = sd_pitch(inter);
+  void* u = ws + kFusedCounterBytes;
+  void* gs = ws + kFusedCounterBytes + align256(nb * pitch * 2);
+  void* xn = ws + kFusedCounterBytes + 2 * align256(nb * pitch * 2);
+  const int in = static_cast<int>(inter), hd = static_cast<int>(hidden);
+  int rc;
+  if (norm_w != nullptr) {
+    // gate rows, then the up rows as the pair's second range; every wave
+    // normalises its own copy of x (nb <= 4, checked by the caller)
+    switch (nb) {
+      case 1: launch_gemv_rows<1, true>(x, hidden, w_gate, hidden, in, hd, gs, pitch, st, norm_w, eps, xn, hidden, w_up, hidden, in, u, pitch); break;
+      case 2: launch_gemv_rows<2, true>(x, hidden, w_gate, hidden, in, hd, gs, pitch, st, norm_w, eps, xn, hidden, w_up, hidden, in, u, pitch); break;
+      case 3: launch_gemv_rows<3, true>(x, hidden, w_gate, hidden, in, hd, gs, pitch, st, norm_w, eps, xn, hidden, w_up, hidden, in, u, pitch); break;
+      default: launch_gemv_rows<4, true>(x, hidden, w_gate, hidden, in, hd, gs, pitch, st, norm_w, eps, xn, hidden, w_up, hidden, in, u, pitch); break;
+    }
+    rc = check_launch("gemv_rows_kernel");
+  } else if (nb >= 3 && nb <= 4 && hidden <= 4096) {
+    // 3-4 tokens: one wave per (gate row, up row) pair measured faster
+    // (4 tokens 24.3 -> 23.1 us per layer); 1-2 tokens: the two-range form
+    if (nb == 3) launch_gemv_dual_rows<3>(x, hidden, w_gate, w_up, hidden, in, hd, gs, u, pitch, st);
+    else launch_gemv_dual_rows<4>(x, hidden, w_gate, w_up, hidden, in, hd, gs, u, pitch, st);
+    rc = check_launch("gemv_dual_rows_kernel");
+  } else {
+    rc = gemv_launch(x, hidden, nb, w_gate, hidden, inter, hidden, gs, pitch, w_up, hidden, inter, u, pitch, st);
+  }
+  if (rc != MOC_OK) return rc;
+  // 64 columns per workgroup up to 8 tokens (<= 256 workgroups at hidden
+  // 2048), 128 beyond (12-16 tokens: 32.0-32.5 -> 26.5-26.9 us per layer)
+  if (nb <= 8)
+    launch_select_down_cw<64>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, y, res, static_cast<int*>(idx_out), st);
+  else
+    launch_select_down_cw<128>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, y, res, static_cast<int*>(idx_out), st);
+  return check_launch("select_down_kernel");
+}
+}  // namespace
+
 extern "C" int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, int64_t k, int64_t hidden) {
   const int64_t a = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
-  return a > 0 ? a + align256(nb * inter * 2) : 0;
+  if (a <= 0) return 0;
+  const int64_t legacy = a + align256(nb * inter * 2);
+  const int64_t sd = kFusedCounterBytes + 2 * align256(nb * sd_pitch(inter) * 2) + align256(nb * hidden * 2);
+  return legacy > sd ? legacy : sd;
 }
 
 extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
@@ -1146,9 +1453,12 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
               "moc_global_decode_bf16: workspace of %lld bytes required", (long long)need);
   const int64_t abytes = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
   char* ws = static_cast<char*>(workspace);
-  void* g = ws + abytes;
   hipStream_t st = as_stream(stream);
   int rc;
+  if (sd_fits(nb, inter, k, hidden))
+    return global_decode_sd(x, nb, hidden, nullptr, 0.f, w_gate, w_up, inter, w_down_t, k, nullptr, y, idx_out, ws,
+                            st);
+  void* g = ws + abytes;
   const bool pair = dense_up_bytes(nb, inter) > 0;
   if (pair) {
     const FusedShape f = fused_shape(nb, k, hidden);
@@ -1160,6 +1470,35 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
   if (rc != MOC_OK) return rc;
   return global_after_gate(x, g, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out, workspace, abytes,
                            stream, pair);
+}
+
+// The decoder layer's FFN half x + FFN(RMSNorm(x)) for <= 4 tokens in two
+// launches: the norm inside the gate/up GEMV pair, the residual add in the
+// last step of the column-owning after-gate kernel.
+extern "C" int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb, int64_t hidden,
+                                                       const void* norm_w, float eps, const void* w_gate,
+                                                       const void* w_up, int64_t inter, const void* w_down_t,
+                                                       int64_t k, void* y, void* idx_out, void* workspace,
+                                                       int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 4, "moc_global_decode_rmsnorm_residual_bf16: 0 <= nb <= 4 tokens");
+  MOC_REQUIRE(inter >= 1 && hidden >= 8 && hidden <= 4096,
+              "moc_global_decode_rmsnorm_residual_bf16: bad shape");
+  MOC_REQUIRE(k >= 1 && k <= inter, "invalid k");
+  MOC_REQUIRE(sd_fits(nb < 1 ? 1 : nb, inter, k, hidden),
+              "moc_global_decode_rmsnorm_residual_bf16: needs hidden %% 256 == 0, inter <= %d, k <= %d",
+              kSdMaxInter, kSdMaxK);
+  MOC_REQUIRE(eps >= 0.f, "moc_global_decode_rmsnorm_residual_bf16: eps must be >= 0");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && norm_w && w_gate && w_up && w_down_t && y,
+              "moc_global_decode_rmsnorm_residual_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(norm_w) && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down_t),
+              "moc_global_decode_rmsnorm_residual_bf16: x, norm_w and weights must be 16-byte aligned");
+  MOC_REQUIRE(y != x, "moc_global_decode_rmsnorm_residual_bf16: y must not alias x");
+  const int64_t need = moc_global_decode_workspace_size(nb, inter, k, hidden);
+  MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "moc_global_decode_rmsnorm_residual_bf16: workspace of %lld bytes required", (long long)need);
+  return global_decode_sd(x, nb, hidden, norm_w, eps, w_gate, w_up, inter, w_down_t, k, x, y, idx_out,
+                          static_cast<char*>(workspace), as_stream(stream));
 }
 
 extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,

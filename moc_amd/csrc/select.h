@@ -12,8 +12,9 @@
 // select_threshold finds the k-th largest key T and how many T-valued
 // channels still have to be taken (krem) by an MSB-first radix select with
 // 8-bit digits (2 passes over the registers for 16-bit keys, 4 for 32-bit;
-// one wave with 16-bit keys first tries two passes over the 4096 keys below
-// the row's largest, select_threshold_window).
+// with 16-bit keys one wave (select_threshold_window) or a group of waves
+// (select_threshold_window_group) first tries two passes over the 4096 keys
+// below the row's largest).
 // The group counts into one 256-bin LDS histogram kept in C copies (lane % C
 // picks the copy): LDS atomics serialise on lanes of one instruction that
 // hit the same address, and real scores pile into a few exponent bins, so
@@ -43,16 +44,29 @@ typedef short sel_s16x2 __attribute__((ext_vector_type(2)));
 constexpr int kSelBins = 256;
 
 // Histogram layout for C copies (lane % C picks the copy): 256 bins, one
-// spare bin per lane sharing the copy, one pad dword.
+// spare bin per lane sharing the copy, pad dwords up to a multiple of four
+// (every copy starts 16-byte aligned, so a scan reads four bins at once; the
+// copies' bin b still fall in distinct LDS banks for C = 4 and 8).
 template <int C>
 constexpr int sel_copy_pitch() {
-  return kSelBins + 64 / C + 1;
+  return (kSelBins + 64 / C + 1 + 3) / 4 * 4;
 }
 
-// LDS dwords the selection of a group of NW waves needs.
+// The second pass of a group's windowed threshold counts the 16 keys of one
+// window bin into its own small histogram (C copies, a spare bin per lane
+// sharing the copy, one pad dword), so it needs no barrier to clear the
+// first pass's counts while other waves still read them.
+template <int C>
+constexpr int sel_copy_pitch16() {
+  return 16 + 64 / C + 1;
+}
+
+// LDS dwords the selection of a group of NW waves needs: the histogram, a
+// per-wave table, and (NW > 1) the 16-bin histogram of the window's second
+// pass.
 template <int NW, int C>
 constexpr int select_lds_dwords() {
-  return C * sel_copy_pitch<C>() + (NW > 1 ? NW : 0);
+  return C * sel_copy_pitch<C>() + (NW > 1 ? NW + C * sel_copy_pitch16<C>() : 0);
 }
 
 // Order keys of two packed bf16 values: 0x8000 + |v| for v >= 0 (and -0),
@@ -296,6 +310,35 @@ __device__ __forceinline__ bool sel_scan_bins(const uint32_t* hist, int lane, ui
   return true;
 }
 
+// The same scan with lane l owning the four contiguous bins 252 - 4l ...
+// 255 - 4l: one 16-byte LDS read per copy and one wave scan (hist must be
+// 16-byte aligned).
+template <int C>
+__device__ __forceinline__ bool sel_scan_bins4(const uint32_t* hist, int lane, uint32_t krem, uint32_t& pb,
+                                               uint32_t& gt) {
+  constexpr int kPitch = sel_copy_pitch<C>();
+  uint32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;  // bins 252 - 4l ... 255 - 4l
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const uint4 v = *reinterpret_cast<const uint4*>(hist + c * kPitch + kSelBins - 4 - 4 * lane);
+    s0 += v.x; s1 += v.y; s2 += v.z; s3 += v.w;
+  }
+  const uint32_t tot = s0 + s1 + s2 + s3;
+  const uint32_t incl = wave_inclusive_scan(tot);
+  uint32_t g = incl - tot;  // keys in the bins above this lane's four
+  const unsigned long long hits = __ballot(g < krem && incl >= krem);
+  if (hits == 0ull) return false;
+  const int src = __ffsll(hits) - 1;
+  uint32_t j = 3;  // from the top bin down: the first whose count reaches krem
+  if (g + s3 >= krem) j = 0;
+  else if (g + s3 + s2 >= krem) { j = 1; g += s3; }
+  else if (g + s3 + s2 + s1 >= krem) { j = 2; g += s3 + s2; }
+  else g += s3 + s2 + s1;
+  pb = kSelBins - 1 - 4 * src - wave_read_lane(j, src);
+  gt = wave_read_lane(g, src);
+  return true;
+}
+
 // Largest value over the 64 lanes, returned to every lane.
 __device__ __forceinline__ uint32_t sel_wave_max(uint32_t v) {
   v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
@@ -362,14 +405,107 @@ __device__ __forceinline__ bool select_threshold_window(const uint32_t (&w)[W], 
   return true;
 }
 
-template <int NW, int C, int W, int KEY_BITS>
-__device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_t k,
-                                                 uint32_t* hist, uint32_t& thr, uint32_t& krem) {
-  static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 histogram copies");
-  if constexpr (NW == 1 && KEY_BITS == 16) {
-    if (select_threshold_window<C, W>(w, k, hist, thr, krem)) return;
-    __builtin_amdgcn_wave_barrier();
+// The same window for a group of NW > 1 waves selecting one row together
+// (thread t of the group holds channels [t L, t L + L)), in three steps so
+// that a kernel can do its own work between them:
+//  - sel_window_pass1: the row's largest key (per-wave maxima through the
+//    table behind the histogram, which is cleared meanwhile, with the 16-bin
+//    one), the first pass and its scan, two workgroup barriers; every wave
+//    scans the counts itself.  Gives the bin [kb, kb + 16) that holds the
+//    k-th largest key and krem, the number of keys to take from it; returns
+//    false, uniformly over the group, when fewer than k keys lie in the
+//    window;
+//  - sel_window_pass2_count: the keys of that bin into the 16-bin histogram
+//    (no barrier: the caller puts one before the scan);
+//  - sel_window_pass2_scan: the threshold T and krem within T's keys.
+template <int NW, int C, int W>
+__device__ __forceinline__ bool sel_window_pass1(const uint32_t (&w)[W], uint32_t k, uint32_t* hist,
+                                                 int& kb, uint32_t& krem) {
+  constexpr int kPitch = sel_copy_pitch<C>();
+  constexpr int kPitch16 = sel_copy_pitch16<C>();
+  constexpr int kHist = C * kPitch;
+  uint32_t* tab = hist + kHist;
+  uint32_t* hist16 = tab + NW;
+  const int t = static_cast<int>(threadIdx.x), lane = t & 63, wave = t >> 6;
+  uint32_t* mine = hist + (lane % C) * kPitch;
+  const uint32_t spare = kSelBins + lane / C;
+  for (int i = t; i < kHist; i += 64 * NW) hist[i] = 0;
+  for (int i = t; i < C * kPitch16; i += 64 * NW) hist16[i] = 0;
+  sel_u16x2 m2 = {0, 0};
+#pragma unroll
+  for (int j = 0; j < W; ++j) m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(sel_u16x2, w[j]));
+  const uint32_t wmax = sel_wave_max(max(static_cast<uint32_t>(m2.x), static_cast<uint32_t>(m2.y)));
+  if (lane == 0) tab[wave] = wmax;
+  __syncthreads();
+  uint32_t hi = tab[0];
+#pragma unroll
+  for (int q = 1; q < NW; ++q) hi = max(hi, tab[q]);
+  // the lowest real key is 0x80; padding keys (0) fall below the window
+  const int lo = max(static_cast<int>(hi) - 4095, 1);
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    const uint32_t b0 = min(static_cast<uint32_t>(static_cast<int>(w[j] & 0xFFFFu) - lo) >> 4, spare);
+    const uint32_t b1 = min(static_cast<uint32_t>(static_cast<int>(w[j] >> 16) - lo) >> 4, spare);
+    __hip_atomic_fetch_add(&mine[b0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_fetch_add(&mine[b1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+  __syncthreads();
+  uint32_t pb, gt;
+  if (!sel_scan_bins4<C>(hist, lane, k, pb, gt)) return false;
+  krem = k - gt;
+  kb = lo + 16 * static_cast<int>(pb);
+  return true;
+}
+
+template <int NW, int C, int W>
+__device__ __forceinline__ void sel_window_pass2_count(const uint32_t (&w)[W], int kb, uint32_t* hist) {
+  constexpr int kPitch16 = sel_copy_pitch16<C>();
+  uint32_t* mine16 = hist + C * sel_copy_pitch<C>() + NW + (threadIdx.x % C) * kPitch16;
+#pragma unroll
+  for (int j = 0; j < W; ++j) {
+    const uint32_t d0 = static_cast<uint32_t>(static_cast<int>(w[j] & 0xFFFFu) - kb);
+    const uint32_t d1 = static_cast<uint32_t>(static_cast<int>(w[j] >> 16) - kb);
+    if (d0 < 16u) __hip_atomic_fetch_add(&mine16[d0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (d1 < 16u) __hip_atomic_fetch_add(&mine16[d1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+}
+
+template <int NW, int C>
+__device__ __forceinline__ void sel_window_pass2_scan(const uint32_t* hist, int kb, uint32_t& thr,
+                                                      uint32_t& krem) {
+  constexpr int kPitch16 = sel_copy_pitch16<C>();
+  const uint32_t* hist16 = hist + C * sel_copy_pitch<C>() + NW;
+  const int lane = threadIdx.x & 63;
+  // lane l < 16 holds key kb + 15 - l; the krem-th largest of the bin's keys
+  uint32_t s = 0;
+  if (lane < 16) {
+#pragma unroll
+    for (int c = 0; c < C; ++c) s += hist16[c * kPitch16 + 15 - lane];
+  }
+  const uint32_t incl = wave_inclusive_scan(s);
+  const unsigned long long hits = __ballot(lane < 16 && incl >= krem);
+  const int src = __ffsll(hits) - 1;  // the bin holds krem of its keys
+  thr = static_cast<uint32_t>(kb + 15 - src);
+  krem -= wave_read_lane(incl - s, src);
+}
+
+template <int NW, int C, int W>
+__device__ __forceinline__ bool select_threshold_window_group(const uint32_t (&w)[W], uint32_t k,
+                                                              uint32_t* hist, uint32_t& thr,
+                                                              uint32_t& krem) {
+  int kb;
+  if (!sel_window_pass1<NW, C, W>(w, k, hist, kb, krem)) return false;
+  sel_window_pass2_count<NW, C, W>(w, kb, hist);
+  __syncthreads();
+  sel_window_pass2_scan<NW, C>(hist, kb, thr, krem);
+  return true;
+}
+
+// The MSB-first radix passes alone (no window).
+template <int NW, int C, int W, int KEY_BITS>
+__device__ __forceinline__ void select_threshold_bytes(const uint32_t (&w)[W], uint32_t k,
+                                                       uint32_t* hist, uint32_t& thr, uint32_t& krem) {
+  static_assert(C == 4 || C == 8 || C == 16, "4, 8 or 16 histogram copies");
   constexpr int kPitch = sel_copy_pitch<C>();
   constexpr int kHist = C * kPitch;
   const int t = (NW > 1) ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x & 63);
@@ -420,6 +556,20 @@ __device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_
     prefix |= pb << shift;
   }
   thr = prefix;
+}
+
+template <int NW, int C, int W, int KEY_BITS>
+__device__ __forceinline__ void select_threshold(const uint32_t (&w)[W], uint32_t k,
+                                                 uint32_t* hist, uint32_t& thr, uint32_t& krem) {
+  if constexpr (NW == 1 && KEY_BITS == 16) {
+    if (select_threshold_window<C, W>(w, k, hist, thr, krem)) return;
+    __builtin_amdgcn_wave_barrier();
+  }
+  if constexpr (NW > 1 && KEY_BITS == 16) {
+    if (select_threshold_window_group<NW, C, W>(w, k, hist, thr, krem)) return;
+    __syncthreads();  // every wave is done reading the window's counts
+  }
+  select_threshold_bytes<NW, C, W, KEY_BITS>(w, k, hist, thr, krem);
 }
 
 // take[d] bit i: channel c0 + 32 d + i is selected; first: rank of the

@@ -255,6 +255,12 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         ensure_native_ops_ready()
         self._ensure_down_weight_t()
         x_2d = x_2d.contiguous()
+        c = self.config
+        if K.global_decode_rmsnorm_residual_fits(x_2d.shape[0], c.intermediate_size, c.k, c.hidden_size):
+            y = K.global_decode_rmsnorm_residual(
+                x_2d, norm_weight, eps, self.gate_proj.weight, self.up_proj.weight, self._down_weight_t, c.k,
+                workspace=self._global_decode_workspace(x_2d.shape[0], x_2d.device))
+            return self._restore_output_shape(y, shp)
         gate_full, xn = K.gemv_rmsnorm(x_2d, norm_weight, eps, self.gate_proj.weight)
         y = K.global_after_gate(xn, gate_full, self.up_proj.weight, self._down_weight_t,
                                 self.config.k, residual=x_2d,

@@ -697,6 +697,41 @@ def global_decode(x, gate_weight, up_weight, down_weight_t, k: int, *, workspace
     return y
 
 
+def global_decode_rmsnorm_residual(x, norm_weight, eps: float, gate_weight, up_weight, down_weight_t,
+                                   k: int, *, workspace=None, out=None,
+                                   idx_out: torch.Tensor | None = None) -> torch.Tensor:
+    """x + FFN(RMSNorm(x)) of a decoder layer, <= 4 tokens, global MoC: the
+    norm inside the gate/up GEMV, the residual added by the after-gate
+    kernel (moc_global_decode_rmsnorm_residual_bf16)."""
+    N.require_device(x, norm_weight, gate_weight, up_weight, down_weight_t, idx_out)
+    x, nw, wg, wu, wdt = _bf16_contig(x, norm_weight, gate_weight, up_weight, down_weight_t)
+    nb, hidden = x.shape
+    inter = wg.shape[0]
+    if nb > 4:
+        raise ValueError(f"global_decode_rmsnorm_residual takes at most 4 tokens (got {nb})")
+    if wg.shape != (inter, hidden) or wu.shape != (inter, hidden) or wdt.shape != (inter, hidden) \
+            or nw.shape != (hidden,):
+        raise ValueError("norm_weight [hidden]; gate_weight, up_weight, down_weight_t [intermediate, hidden]")
+    if idx_out is not None and (idx_out.dtype != torch.int32 or idx_out.shape != (nb, int(k))
+                                or not idx_out.is_contiguous()):
+        raise ValueError(f"idx_out must be a contiguous int32 [{nb}, {int(k)}] tensor")
+    y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
+    ws_bytes = N.query("moc_global_decode_workspace_size", nb, inter, int(k), hidden)
+    if workspace is None:
+        workspace = _decode_workspace(x.device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"global_decode_rmsnorm_residual: workspace of {ws_bytes} bytes required")
+    N.call("moc_global_decode_rmsnorm_residual_bf16", x.data_ptr(), nb, hidden, nw.data_ptr(), float(eps),
+           wg.data_ptr(), wu.data_ptr(), inter, wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out),
+           workspace.data_ptr(), ws_bytes, N.stream_of(x))
+    return y
+
+
+def global_decode_rmsnorm_residual_fits(nb: int, inter: int, k: int, hidden: int) -> bool:
+    """Shapes moc_global_decode_rmsnorm_residual_bf16 takes."""
+    return 1 <= nb <= 4 and hidden % 256 == 0 and hidden <= 4096 and inter <= 8192 and int(k) <= 4096
+
+
 # ----------------------------------------------------------------------- 2:8
 def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None,
                          norm_weight: torch.Tensor | None = None, eps: float = 1e-6):

@@ -625,11 +625,15 @@ def test_global_decode_path_1b(nb):
                                          (5, 5461, 2048), (16, 5461, 2048), (4, 1000, 256),
                                          (8, 777, 4096), (7, 50, 1024), (12, 3001, 384)])
 def test_global_decode_layer_entry(nb, inter, d):
-    """moc_global_decode_bf16 (gate GEMV, from 4 tokens on with the dense U
-    in the same launch, then the after-gate kernel) equals gemv +
-    global_after_gate bit for bit: y and the selected channels.  (8, 777,
-    4096) takes the GEMV fallback that launches twice; every G row is also
-    checked against the f32 product."""
+    """moc_global_decode_bf16 against gemv + global_after_gate on the same
+    G: the same selected channels bit for bit, y within one bf16 ulp (where
+    hidden % 256 == 0 the layer entry's after-gate kernel sums each output
+    column in another f32 order) and within 2e-2 of the oracle on that
+    selection; two calls in a row give the same bits, and a call of the
+    selected-row path in between (same workspace, its counters) changes
+    nothing.  (8, 777, 4096) takes the GEMV fallback that launches twice;
+    (4, 1000, 256) and (12, 3001, 384) the selected-row after-gate kernel;
+    every G row is also checked against the f32 product."""
     k = max(1, inter // 5)
     g = gen(360 + nb + inter)
     x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
@@ -637,15 +641,54 @@ def test_global_decode_layer_entry(nb, inter, d):
     wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
     wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
     G = K().gemv(x, wg)
-    bf16_close(G.cpu(), x.float().cpu() @ wg.float().cpu().t(), ulps=1, atol=1e-3)
+    Gc = G.cpu()
+    bf16_close(Gc, x.float().cpu() @ wg.float().cpu().t(), ulps=1, atol=1e-3)
     i_two = torch.empty(nb, k, dtype=torch.int32, device=DEV)
     y_two = K().global_after_gate(x, G, wu, wdt, k, idx_out=i_two)
     i_one = torch.empty(nb, k, dtype=torch.int32, device=DEV)
     ws = K().global_decode_workspace(nb, inter, k, d, DEV)
+    y_first = None
     for _ in range(2):  # the counters are left zero for the next call
         y_one = K().global_decode(x, wg, wu, wdt, k, workspace=ws, idx_out=i_one)
         assert torch.equal(i_one, i_two)
-        assert torch.equal(y_one, y_two)
+        if y_first is None:
+            y_first = y_one.clone()
+            # the selected-row kernel on the same workspace in between
+            K().global_after_gate(x, G, wu, wdt, k, workspace=ws[:K().global_after_gate_workspace_bytes(
+                nb, inter, k, d)])
+        assert torch.equal(y_one, y_first)
+    bf16_close(y_one, y_two, ulps=1, atol=1e-4)
+    y_ref, idx_ref, _ = O.masked_reference(x.cpu(), wg.cpu(), wu.cpu(), wdt.cpu().t().contiguous(), k,
+                                           g_override=Gc)
+    assert np.array_equal(i_one.cpu().numpy(), idx_ref)
+    close(y_one, y_ref)
+
+
+@pytest.mark.parametrize("nb", [1, 2, 3, 4])
+def test_global_decode_rmsnorm_residual(nb):
+    """moc_global_decode_rmsnorm_residual_bf16: the decoder layer's FFN half
+    x + FFN(RMSNorm(x)) in two launches.  Its norm and gate rows are the
+    gemv_rmsnorm kernel's (same bits), so the selection equals the oracle's
+    Top-K of gemv_rmsnorm's G bit for bit, and y is within 2e-2 of bf16(x +
+    bf16(oracle FFN of gemv_rmsnorm's xn)); a second call gives the same
+    bits."""
+    d, inter, k, eps = 2048, 5461, 1024, 1e-6
+    g = gen(380 + nb)
+    x = (torch.randn(nb, d, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    G, xn = K().gemv_rmsnorm(x, nw, eps, wg)
+    io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
+    ws = K().global_decode_workspace(nb, inter, k, d, DEV)
+    y = K().global_decode_rmsnorm_residual(x, nw, eps, wg, wu, wdt, k, workspace=ws, idx_out=io)
+    y2 = K().global_decode_rmsnorm_residual(x, nw, eps, wg, wu, wdt, k, workspace=ws)
+    assert torch.equal(y, y2)
+    ffn_ref, idx_ref, _ = O.masked_reference(xn.cpu(), wg.cpu(), wu.cpu(), wdt.cpu().t().contiguous(), k,
+                                             g_override=G.cpu())
+    assert np.array_equal(io.cpu().numpy(), idx_ref)
+    close(y, (x.cpu().float() + ffn_ref.float()).to(torch.bfloat16))
 
 
 @pytest.mark.parametrize("nb", [1, 2, 3, 4])
