@@ -255,7 +255,8 @@ def pmc_target(which: str) -> None:
         for _ in range(8):
             wg = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
             wu = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-            wdt = (torch.randn(I1B, D1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
+            wdt = K.down_weight_t_for_decode(
+                (torch.randn(D1B, I1B, device="cuda", generator=gen) * 0.02).to(torch.bfloat16))
             layers.append((wg, wu, wdt))
         x = torch.randn(1, D1B, device="cuda", generator=gen).to(torch.bfloat16)
         y = torch.empty(1, D1B, device="cuda", dtype=torch.bfloat16)
@@ -469,7 +470,7 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
         wg = (torch.randn(inter, d, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
         wu = (torch.randn(inter, d, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
         wd = (torch.randn(d, inter, device="cuda", generator=gen) * 0.02).to(torch.bfloat16)
-        wdt = wd.t().contiguous()
+        wdt = K.down_weight_t_for_decode(wd)  # the module's layout (padded row pitch)
         del wd
         layers.append((wg, wu, wdt))
     x = torch.randn(nb, d, device="cuda", generator=gen).to(torch.bfloat16)

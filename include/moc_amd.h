@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define MOC_ABI_VERSION 2
+#define MOC_ABI_VERSION 3
 
 /* status codes */
 #define MOC_OK 0
@@ -45,6 +45,14 @@ extern "C" {
 /* moc_gemm_ws: bytes of arrival counters at the start of its workspace (zero
  * when a call starts; every call leaves them zero). */
 #define MOC_GEMM_WS_COUNTER_BYTES 4096
+
+/* W_down^T [inter, hidden] of the decode entry points comes with its row
+ * pitch ldw_down (elements; >= hidden, a multiple of 8).  A pitch that is a
+ * multiple of 4 KB makes every row's same column block fall on the same
+ * memory channels; the decode kernels read one column block per workgroup
+ * down all selected rows, so MOC_DOWN_T_PITCH_PAD extra elements per row
+ * (128 bytes) spread them (1b decode layer at one token: 19.5 -> 18.3 us). */
+#define MOC_DOWN_T_PITCH_PAD 64
 
 /* ------------------------------------------------------------------ misc */
 const char* moc_last_error(void);
@@ -350,7 +358,7 @@ int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64_t hidden);
  * optimized_global_moc_ext.cu:247-372,429-455; moc::selected_grouped_down,
  * moc/inference/triton_fused_ffn_kernels.py:228-267). */
 int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
-                           const void* w_down_t, int64_t inter, int64_t hidden, void* y,
+                           const void* w_down_t, int64_t ldw_down, int64_t inter, int64_t hidden, void* y,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes moc_global_after_gate_bf16 needs. */
@@ -369,8 +377,8 @@ int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inter, int64_t 
  * allocation); every call, of any shape, leaves them zero again.  Calls
  * sharing a workspace must not overlap. */
 int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
-                               int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
-                               void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
+                               int64_t hidden, const void* w_up, const void* w_down_t, int64_t ldw_down,
+                               int64_t k, void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
                                void* stream);
 
 /* moc_global_after_gate_bf16 with the layer's residual added in its last
@@ -378,8 +386,8 @@ int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t n
  * (benchmark_decode.py:303) without a separate add.  Same workspace rules. */
 int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
                                         int64_t inter, int64_t hidden, const void* w_up,
-                                        const void* w_down_t, int64_t k, const void* residual,
-                                        void* y, void* idx_out, void* workspace,
+                                        const void* w_down_t, int64_t ldw_down, int64_t k,
+                                        const void* residual, void* y, void* idx_out, void* workspace,
                                         int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes moc_global_decode_bf16 and
@@ -399,8 +407,9 @@ int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, int64_t k, i
  * and y is the same sum in another f32 order.  Same workspace rules (64 KB
  * of counters at its start, zero before the first call, left zero). */
 int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
-                           const void* w_up, int64_t inter, const void* w_down_t, int64_t k, void* y,
-                           void* idx_out, void* workspace, int64_t workspace_bytes, void* stream);
+                           const void* w_up, int64_t inter, const void* w_down_t, int64_t ldw_down,
+                           int64_t k, void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
+                           void* stream);
 
 /* The decoder layer's FFN half y = bf16(x + bf16(FFN(RMSNorm(x)))) for nb <= 4
  * tokens (benchmark_decode.py:101-109,303): the norm (rounding as in
@@ -411,8 +420,8 @@ int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void
 int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb, int64_t hidden,
                                             const void* norm_w, float eps, const void* w_gate,
                                             const void* w_up, int64_t inter, const void* w_down_t,
-                                            int64_t k, void* y, void* idx_out, void* workspace,
-                                            int64_t workspace_bytes, void* stream);
+                                            int64_t ldw_down, int64_t k, void* y, void* idx_out,
+                                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Bytes of the library's own device scratch array (one per GPU, held until
  * the process ends) behind moc_global_after_gate_noalloc_bf16. */
@@ -432,8 +441,8 @@ int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb, int64_t h
  * GPU race. */
 int moc_global_after_gate_noalloc_bf16(const void* x, const void* gate_scores, int64_t nb,
                                        int64_t inter, int64_t hidden, const void* w_up,
-                                       const void* w_down_t, int64_t k, const void* residual,
-                                       void* y, void* idx_out, void* stream);
+                                       const void* w_down_t, int64_t ldw_down, int64_t k,
+                                       const void* residual, void* y, void* idx_out, void* stream);
 
 /* ------------------------------------------------------------------- 2:8 */
 /* Fused gate+up projection with top-2-of-8 selection for nb tokens:
@@ -461,15 +470,15 @@ int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t k, int64_t 
  * (moc::selected_grouped_down, triton_grouped_moc_ops.py:96-131; kernel
  * triton_fused_ffn_kernels.py:228-267). */
 int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb, int64_t k,
-                                   const void* w_down_t, int64_t inter, int64_t hidden, void* y,
-                                   void* workspace, int64_t workspace_bytes, void* stream);
+                                   const void* w_down_t, int64_t ldw_down, int64_t inter, int64_t hidden,
+                                   void* y, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* moc_selected_grouped_down_bf16 for nb <= 64 tokens with the layer's
  * residual added in its last step: y = bf16(residual + bf16(FFN)), the
  * decoder's x + ffn(norm(x)) (benchmark_decode.py:303).  Same workspace. */
 int moc_selected_grouped_down_residual_bf16(const void* sz, const void* idx, int64_t nb, int64_t k,
-                                            const void* w_down_t, int64_t inter, int64_t hidden,
-                                            const void* residual, void* y, void* workspace,
+                                            const void* w_down_t, int64_t ldw_down, int64_t inter,
+                                            int64_t hidden, const void* residual, void* y, void* workspace,
                                             int64_t workspace_bytes, void* stream);
 
 /* 2:4-packed form of a 2:8 selection (this library's operand format for the

@@ -92,29 +92,29 @@ SIGNATURES: dict[str, tuple] = {
     "moc_gemv_bf16": (_int, [_vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
     "moc_gemv_rmsnorm_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _i64, _vp, _i64, _i64,
                                      _i64, _vp, _i64, _vp]),
-    "moc_global_after_gate_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
-                                                   _vp, _vp, _vp, _i64, _vp]),
-    "moc_global_after_gate_noalloc_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
-                                                  _vp, _vp, _vp]),
+    "moc_global_after_gate_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                                   _vp, _vp, _vp, _vp, _i64, _vp]),
+    "moc_global_after_gate_noalloc_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                                                  _vp, _vp, _vp, _vp]),
     "moc_selected_up_silu_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _int, _i64, _vp, _i64, _vp, _vp]),
     "moc_selected_down_workspace_size": (_i64, [_i64, _i64, _i64]),
-    "moc_selected_down_bf16": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
+    "moc_selected_down_bf16": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                       _i64, _vp]),
     "moc_global_after_gate_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
     "moc_global_decode_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
-    "moc_global_decode_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
+    "moc_global_decode_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp,
                                       _i64, _vp]),
-    "moc_global_decode_rmsnorm_residual_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp, _i64,
-                                                       _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
-    "moc_global_after_gate_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
-                                          _i64, _vp]),
+    "moc_global_decode_rmsnorm_residual_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp,
+                                                       _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "moc_global_after_gate_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
+                                          _vp, _i64, _vp]),
     "moc_grouped_top2_up_silu_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
     "moc_grouped_top2_up_silu_rmsnorm_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp,
                                                      _i64, _vp, _vp, _vp]),
-    "moc_selected_grouped_down_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp,
-                                                       _vp, _vp, _i64, _vp]),
+    "moc_selected_grouped_down_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                                                       _vp, _vp, _vp, _i64, _vp]),
     "moc_selected_grouped_down_workspace_size": (_i64, [_i64, _i64, _i64, _i64]),
-    "moc_selected_grouped_down_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp,
+    "moc_selected_grouped_down_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                                               _i64, _vp]),
     "moc_pack28_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp]),
     "moc_grouped_top2_up_silu_packed_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp,

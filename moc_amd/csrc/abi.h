@@ -26,8 +26,8 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // moc_selected_down_bf16 with an optional residual added in the last step
 // (y = bf16(res + bf16(sum)); res may be null) (decode.hip).
 int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
-                       const void* w_down_t, int64_t inter, int64_t hidden, const void* res, void* y,
-                       void* workspace, int64_t workspace_bytes, void* stream);
+                       const void* w_down_t, int64_t ldw_down, int64_t inter, int64_t hidden, const void* res,
+                       void* y, void* workspace, int64_t workspace_bytes, void* stream);
 
 // Bytes of arrival counters at the start of an after-gate workspace.
 constexpr int64_t kAfterGateCounterBytes = 64 * 1024;
@@ -36,7 +36,7 @@ constexpr int64_t kAfterGateCounterBytes = 64 * 1024;
 // be null) on a caller workspace (decode.hip).  up_ready: the dense U that
 // the workspace holds from 4 tokens on was already written by the caller.
 int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter,
-                      int64_t hidden, const void* w_up, const void* w_down_t, int64_t k,
+                      int64_t hidden, const void* w_up, const void* w_down_t, int64_t ldw_down, int64_t k,
                       const void* res, void* y, void* idx_out, void* workspace,
                       int64_t workspace_bytes, void* stream, bool up_ready = false);
 

@@ -564,6 +564,7 @@ template <int L, int CW>
 __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
     const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate, int inter,
     int k, int P, int CB, const uint16_t* __restrict__ w_up, int64_t up_ld, const uint16_t* __restrict__ wdt,
+    int64_t ldd,
     float* __restrict__ part, int* __restrict__ cnt, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ res, int* __restrict__ idx_out) {
   constexpr int QN = CW / 8;            // 16-byte chunks per row segment
@@ -623,7 +624,7 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
 #pragma unroll
   for (int j = 0; j < kDownBatch; ++j) {
     const int e = sl + S * j;
-    dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+    dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * ldd + col)
                      : make_uint4(0, 0, 0, 0);
   }
   const int nch = hidden / 8;
@@ -671,7 +672,7 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
 #pragma unroll
       for (int j = 0; j < kDownBatch; ++j) {
         const int e = e0 + sl + S * j;
-        dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+        dv[j] = e < nsel ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * ldd + col)
                          : make_uint4(0, 0, 0, 0);
       }
     }
@@ -776,7 +777,7 @@ constexpr int kSdBatch = 16;
 template <int L, int CW>
 __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ld, int inter, int k,
-    int hidden, int CB, const uint16_t* __restrict__ wdt, uint16_t* __restrict__ y,
+    int hidden, int CB, const uint16_t* __restrict__ wdt, int64_t ldd, uint16_t* __restrict__ y,
     const uint16_t* __restrict__ res, int* __restrict__ idx_out) {
   constexpr int NW = kSdThreads / 64;
   constexpr int CPT = L / 8;          // 16-byte chunks of a row per thread
@@ -846,7 +847,7 @@ __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
 #pragma unroll
   for (int j = 0; j < kSdBatch; ++j) {
     const int e = r + R * j;
-    dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+    dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * ldd + col)
                   : make_uint4(0, 0, 0, 0);
   }
   {
@@ -879,7 +880,7 @@ __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
 #pragma unroll
     for (int j = 0; j < kSdBatch; ++j) {
       const int e = e0 + R * kSdBatch + R * j;
-      dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * hidden + col)
+      dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * ldd + col)
                     : make_uint4(0, 0, 0, 0);
     }
   }
@@ -919,7 +920,7 @@ constexpr int kDownRows = 128;
 template <typename IdxT>
 __global__ __launch_bounds__(256) void selected_down_kernel(
     const uint16_t* __restrict__ z, const void* __restrict__ idx, int k, int hidden,
-    const uint16_t* __restrict__ wdt, int inter, int G, float* __restrict__ part,
+    const uint16_t* __restrict__ wdt, int64_t ldd, int inter, int G, float* __restrict__ part,
     int* __restrict__ cnt, uint16_t* __restrict__ y, const uint16_t* __restrict__ res) {
   __shared__ float red[32][65];
   __shared__ int last;
@@ -943,7 +944,7 @@ __global__ __launch_bounds__(256) void selected_down_kernel(
 #pragma unroll
   for (int ps = 0; ps < 4; ++ps)
     wv[ps] = (ch[ps] >= 0 && ch[ps] < inter)
-                 ? *reinterpret_cast<const uint4*>(wdt + ch[ps] * hidden + col)
+                 ? *reinterpret_cast<const uint4*>(wdt + ch[ps] * ldd + col)
                  : make_uint4(0, 0, 0, 0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1049,7 +1050,7 @@ inline DownWs down_ws(int64_t nb, int64_t k, int64_t hidden) {
 }
 
 int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
-                         const void* wdt, int64_t inter, int64_t hidden, void* y, void* ws,
+                         const void* wdt, int64_t ldd, int64_t inter, int64_t hidden, void* y, void* ws,
                          hipStream_t st, const void* res = nullptr) {
   const DownWs w = down_ws(nb, k, hidden);
   float* part = static_cast<float*>(ws);
@@ -1057,7 +1058,7 @@ int launch_selected_down(const void* z, const void* idx, int idx_dtype, int64_t 
   const dim3 grid(static_cast<unsigned>(hidden / 64), static_cast<unsigned>(nb * w.G)), block(256);
 #define MOC_DOWN(T)                                                                         \
   selected_down_kernel<T><<<grid, block, 0, st>>>((const uint16_t*)z, idx, (int)k, (int)hidden, \
-                                                  (const uint16_t*)wdt, (int)inter, w.G, part, \
+                                                  (const uint16_t*)wdt, ldd, (int)inter, w.G, part, \
                                                   cnt, (uint16_t*)y, (const uint16_t*)res)
   if (idx_dtype == MOC_I16) MOC_DOWN(int16_t);
   else if (idx_dtype == MOC_I32) MOC_DOWN(int32_t);
@@ -1089,15 +1090,15 @@ inline FusedShape fused_shape(int64_t nb, int64_t k, int64_t hidden) {
 
 template <int CW>
 void launch_fused(const void* x, int hidden, const void* gate, int inter, int k, int nb,
-                  const FusedShape& f, const void* w_up, int64_t up_ld, const void* wdt, float* part,
-                  int* cnt, void* y, const void* res, int* idx_out, hipStream_t st) {
+                  const FusedShape& f, const void* w_up, int64_t up_ld, const void* wdt, int64_t ldd,
+                  float* part, int* cnt, void* y, const void* res, int* idx_out, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(nb * f.P * f.CB)), block(kUdThreads);
   const int per = (inter + kUdThreads - 1) / kUdThreads;
 #define MOC_FU(N)                                                                               \
   select_up_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)x, hidden,               \
                                                        (const uint16_t*)gate, inter, k, f.P, f.CB, \
                                                        (const uint16_t*)w_up, up_ld, (const uint16_t*)wdt, \
-                                                       part, cnt, (uint16_t*)y, (const uint16_t*)res, \
+                                                       ldd, part, cnt, (uint16_t*)y, (const uint16_t*)res, \
                                                        idx_out)
   if (per <= 8) MOC_FU(8);
   else if (per <= 16) MOC_FU(16);
@@ -1110,13 +1111,14 @@ void launch_fused(const void* x, int hidden, const void* gate, int inter, int k,
 // workgroup.
 template <int CW>
 void launch_select_down_cw(const void* g, const void* u, int64_t ld, int nb, int inter, int k, int hidden,
-                           const void* wdt, void* y, const void* res, int* idx_out, hipStream_t st) {
+                           const void* wdt, int64_t ldd, void* y, const void* res, int* idx_out,
+                           hipStream_t st) {
   const int CB = hidden / CW;
   const dim3 grid(static_cast<unsigned>(nb * CB)), block(kSdThreads);
   const int per = (inter + kSdThreads - 1) / kSdThreads;
 #define MOC_SD(N)                                                                                  \
   select_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)g, (const uint16_t*)u, ld, inter, k, \
-                                                     hidden, CB, (const uint16_t*)wdt, (uint16_t*)y,      \
+                                                     hidden, CB, (const uint16_t*)wdt, ldd, (uint16_t*)y, \
                                                      (const uint16_t*)res, idx_out)
   if (per <= 8) MOC_SD(8);
   else MOC_SD(16);
@@ -1263,8 +1265,8 @@ extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64
 
 namespace moc {
 int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb, int64_t k,
-                       const void* w_down_t, int64_t inter, int64_t hidden, const void* res, void* y,
-                       void* workspace, int64_t workspace_bytes, void* stream) {
+                       const void* w_down_t, int64_t ldw_down, int64_t inter, int64_t hidden, const void* res,
+                       void* y, void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(idx_ok(idx_dtype), "moc_selected_down_bf16: bad index dtype");
   MOC_REQUIRE(nb >= 0 && k >= 1 && inter >= 1 && hidden >= 1, "moc_selected_down_bf16: bad shape");
   MOC_REQUIRE(hidden % 64 == 0, "moc_selected_down_bf16: hidden must be a multiple of 64");
@@ -1272,22 +1274,24 @@ int selected_down_impl(const void* z, const void* idx, int idx_dtype, int64_t nb
   if (nb == 0) return MOC_OK;
   MOC_REQUIRE(z && idx && w_down_t && y, "moc_selected_down_bf16: null pointer");
   MOC_REQUIRE(aligned16(w_down_t), "moc_selected_down_bf16: w_down_t must be 16-byte aligned");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_selected_down_bf16: ldw_down must be a multiple of 8 and >= hidden");
   const int64_t need = moc_selected_down_workspace_size(nb, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_selected_down_bf16: workspace of %lld bytes required", (long long)need);
   const DownWs w = down_ws(nb, k, hidden);
   int rc = moc_fill_zero(static_cast<char*>(workspace) + w.part_bytes, w.cnt_bytes, stream);
   if (rc != MOC_OK) return rc;
-  return launch_selected_down(z, idx, idx_dtype, nb, k, w_down_t, inter, hidden, y, workspace,
+  return launch_selected_down(z, idx, idx_dtype, nb, k, w_down_t, ldw_down, inter, hidden, y, workspace,
                               as_stream(stream), res);
 }
 }  // namespace moc
 
 extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
-                                      int64_t k, const void* w_down_t, int64_t inter,
+                                      int64_t k, const void* w_down_t, int64_t ldw_down, int64_t inter,
                                       int64_t hidden, void* y, void* workspace,
                                       int64_t workspace_bytes, void* stream) {
-  return selected_down_impl(z, idx, idx_dtype, nb, k, w_down_t, inter, hidden, nullptr, y, workspace,
+  return selected_down_impl(z, idx, idx_dtype, nb, k, w_down_t, ldw_down, inter, hidden, nullptr, y, workspace,
                             workspace_bytes, stream);
 }
 
@@ -1318,8 +1322,8 @@ extern "C" int64_t moc_global_after_gate_workspace_size(int64_t nb, int64_t inte
 
 namespace moc {
 int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_t inter, int64_t hidden,
-                      const void* w_up, const void* w_down_t, int64_t k, const void* res, void* y,
-                      void* idx_out, void* workspace, int64_t workspace_bytes, void* stream,
+                      const void* w_up, const void* w_down_t, int64_t ldw_down, int64_t k, const void* res,
+                      void* y, void* idx_out, void* workspace, int64_t workspace_bytes, void* stream,
                       bool up_ready) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64, "moc_global_after_gate_bf16: bad shape");
@@ -1329,6 +1333,8 @@ int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_
   MOC_REQUIRE(x && gate_scores && w_up && w_down_t && y, "moc_global_after_gate_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(w_up) && aligned16(w_down_t),
               "moc_global_after_gate_bf16: x and weights must be 16-byte aligned");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_global_after_gate_bf16: ldw_down must be a multiple of 8 and >= hidden");
   const int64_t need = moc_global_after_gate_workspace_size(nb, inter, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_global_after_gate_bf16: workspace of %lld bytes required", (long long)need);
@@ -1353,19 +1359,20 @@ int global_after_gate(const void* x, const void* gate_scores, int64_t nb, int64_
   int* io = static_cast<int*>(idx_out);
   if (f.CW == 256)
     launch_fused<256>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, up, up_ld, w_down_t,
-                      part, cnt, y, res, io, st);
+                      ldw_down, part, cnt, y, res, io, st);
   else
     launch_fused<64>(x, (int)hidden, gate_scores, (int)inter, (int)k, (int)nb, f, up, up_ld, w_down_t,
-                     part, cnt, y, res, io, st);
+                     ldw_down, part, cnt, y, res, io, st);
   return check_launch("select_up_down_kernel");
 }
 }  // namespace moc
 
 extern "C" int moc_global_after_gate_bf16(const void* x, const void* gate_scores, int64_t nb,
                                           int64_t inter, int64_t hidden, const void* w_up,
-                                          const void* w_down_t, int64_t k, void* y, void* idx_out,
-                                          void* workspace, int64_t workspace_bytes, void* stream) {
-  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out,
+                                          const void* w_down_t, int64_t ldw_down, int64_t k, void* y,
+                                          void* idx_out, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, ldw_down, k, nullptr, y, idx_out,
                            workspace, workspace_bytes, stream);
 }
 
@@ -1390,8 +1397,8 @@ namespace {
 // residual added when res != nullptr).  Workspace after the counters: U, G
 // (pitch sd_pitch(inter)), then xn [nb, hidden].
 int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm_w, float eps,
-                     const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t, int64_t k,
-                     const void* res, void* y, void* idx_out, char* ws, hipStream_t st) {
+                     const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t, int64_t ldw_down,
+                     int64_t k, const void* res, void* y, void* idx_out, char* ws, hipStream_t st) {
   const int64_t pitch = sd_pitch(inter);
   void* u = ws + kFusedCounterBytes;
   void* gs = ws + kFusedCounterBytes + align256(nb * pitch * 2);
@@ -1421,9 +1428,11 @@ int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm
   // 64 columns per workgroup up to 8 tokens (<= 256 workgroups at hidden
   // 2048), 128 beyond (12-16 tokens: 32.0-32.5 -> 26.5-26.9 us per layer)
   if (nb <= 8)
-    launch_select_down_cw<64>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, y, res, static_cast<int*>(idx_out), st);
+    launch_select_down_cw<64>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res,
+                              static_cast<int*>(idx_out), st);
   else
-    launch_select_down_cw<128>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, y, res, static_cast<int*>(idx_out), st);
+    launch_select_down_cw<128>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res,
+                               static_cast<int*>(idx_out), st);
   return check_launch("select_down_kernel");
 }
 }  // namespace
@@ -1437,9 +1446,9 @@ extern "C" int64_t moc_global_decode_workspace_size(int64_t nb, int64_t inter, i
 }
 
 extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* w_gate,
-                                      const void* w_up, int64_t inter, const void* w_down_t, int64_t k,
-                                      void* y, void* idx_out, void* workspace, int64_t workspace_bytes,
-                                      void* stream) {
+                                      const void* w_up, int64_t inter, const void* w_down_t, int64_t ldw_down,
+                                      int64_t k, void* y, void* idx_out, void* workspace,
+                                      int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_decode_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64 && hidden % 64 == 0 && hidden < (1LL << 30),
               "moc_global_decode_bf16: bad shape");
@@ -1448,6 +1457,8 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
   MOC_REQUIRE(x && w_gate && w_up && w_down_t && y, "moc_global_decode_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down_t),
               "moc_global_decode_bf16: x and weights must be 16-byte aligned");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_global_decode_bf16: ldw_down must be a multiple of 8 and >= hidden");
   const int64_t need = moc_global_decode_workspace_size(nb, inter, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_global_decode_bf16: workspace of %lld bytes required", (long long)need);
@@ -1456,8 +1467,8 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
   hipStream_t st = as_stream(stream);
   int rc;
   if (sd_fits(nb, inter, k, hidden))
-    return global_decode_sd(x, nb, hidden, nullptr, 0.f, w_gate, w_up, inter, w_down_t, k, nullptr, y, idx_out, ws,
-                            st);
+    return global_decode_sd(x, nb, hidden, nullptr, 0.f, w_gate, w_up, inter, w_down_t, ldw_down, k, nullptr, y,
+                            idx_out, ws, st);
   void* g = ws + abytes;
   const bool pair = dense_up_bytes(nb, inter) > 0;
   if (pair) {
@@ -1468,8 +1479,8 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
     rc = gemv_launch(x, hidden, nb, w_gate, hidden, inter, hidden, g, inter, nullptr, 0, 0, nullptr, 0, st);
   }
   if (rc != MOC_OK) return rc;
-  return global_after_gate(x, g, nb, inter, hidden, w_up, w_down_t, k, nullptr, y, idx_out, workspace, abytes,
-                           stream, pair);
+  return global_after_gate(x, g, nb, inter, hidden, w_up, w_down_t, ldw_down, k, nullptr, y, idx_out, workspace,
+                           abytes, stream, pair);
 }
 
 // The decoder layer's FFN half x + FFN(RMSNorm(x)) for <= 4 tokens in two
@@ -1478,8 +1489,8 @@ extern "C" int moc_global_decode_bf16(const void* x, int64_t nb, int64_t hidden,
 extern "C" int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb, int64_t hidden,
                                                        const void* norm_w, float eps, const void* w_gate,
                                                        const void* w_up, int64_t inter, const void* w_down_t,
-                                                       int64_t k, void* y, void* idx_out, void* workspace,
-                                                       int64_t workspace_bytes, void* stream) {
+                                                       int64_t ldw_down, int64_t k, void* y, void* idx_out,
+                                                       void* workspace, int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 4, "moc_global_decode_rmsnorm_residual_bf16: 0 <= nb <= 4 tokens");
   MOC_REQUIRE(inter >= 1 && hidden >= 8 && hidden <= 4096,
               "moc_global_decode_rmsnorm_residual_bf16: bad shape");
@@ -1493,21 +1504,23 @@ extern "C" int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb
               "moc_global_decode_rmsnorm_residual_bf16: null pointer");
   MOC_REQUIRE(aligned16(x) && aligned16(norm_w) && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down_t),
               "moc_global_decode_rmsnorm_residual_bf16: x, norm_w and weights must be 16-byte aligned");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_global_decode_rmsnorm_residual_bf16: ldw_down must be a multiple of 8 and >= hidden");
   MOC_REQUIRE(y != x, "moc_global_decode_rmsnorm_residual_bf16: y must not alias x");
   const int64_t need = moc_global_decode_workspace_size(nb, inter, k, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_global_decode_rmsnorm_residual_bf16: workspace of %lld bytes required", (long long)need);
-  return global_decode_sd(x, nb, hidden, norm_w, eps, w_gate, w_up, inter, w_down_t, k, x, y, idx_out,
+  return global_decode_sd(x, nb, hidden, norm_w, eps, w_gate, w_up, inter, w_down_t, ldw_down, k, x, y, idx_out,
                           static_cast<char*>(workspace), as_stream(stream));
 }
 
 extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,
                                                    int64_t inter, int64_t hidden, const void* w_up,
-                                                   const void* w_down_t, int64_t k, const void* residual,
-                                                   void* y, void* idx_out, void* workspace,
+                                                   const void* w_down_t, int64_t ldw_down, int64_t k,
+                                                   const void* residual, void* y, void* idx_out, void* workspace,
                                                    int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb == 0 || residual != nullptr, "moc_global_after_gate_residual_bf16: null residual");
-  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, residual, y, idx_out,
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, ldw_down, k, residual, y, idx_out,
                            workspace, workspace_bytes, stream);
 }
 

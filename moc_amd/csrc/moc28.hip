@@ -25,7 +25,7 @@
 #include "gemm_tile.h"
 
 extern "C" int moc_selected_down_bf16(const void* z, const void* idx, int idx_dtype, int64_t nb,
-                                      int64_t k, const void* w_down_t, int64_t inter,
+                                      int64_t k, const void* w_down_t, int64_t ldw_down, int64_t inter,
                                       int64_t hidden, void* y, void* workspace,
                                       int64_t workspace_bytes, void* stream);
 extern "C" int64_t moc_selected_down_workspace_size(int64_t nb, int64_t k, int64_t hidden);
@@ -563,17 +563,19 @@ extern "C" int64_t moc_selected_grouped_down_workspace_size(int64_t nb, int64_t 
 }
 
 extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, int64_t nb,
-                                              int64_t k, const void* w_down_t, int64_t inter,
-                                              int64_t hidden, void* y, void* workspace,
+                                              int64_t k, const void* w_down_t, int64_t ldw_down,
+                                              int64_t inter, int64_t hidden, void* y, void* workspace,
                                               int64_t workspace_bytes, void* stream) {
   MOC_REQUIRE(nb >= 0 && k >= 1 && inter >= k && hidden >= 1, "moc_selected_grouped_down_bf16: bad shape");
   MOC_REQUIRE(hidden % 8 == 0, "moc_selected_grouped_down_bf16: hidden must be a multiple of 8");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_selected_grouped_down_bf16: ldw_down must be a multiple of 8 and >= hidden");
   if (nb == 0) return MOC_OK;
   const int64_t need = moc_selected_grouped_down_workspace_size(nb, k, inter, hidden);
   MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
               "moc_selected_grouped_down_bf16: workspace of %lld bytes required", (long long)need);
   if (nb <= 64)
-    return moc_selected_down_bf16(sz, idx, MOC_I64, nb, k, w_down_t, inter, hidden, y, workspace,
+    return moc_selected_down_bf16(sz, idx, MOC_I64, nb, k, w_down_t, ldw_down, inter, hidden, y, workspace,
                                   workspace_bytes, stream);
   MOC_REQUIRE(inter % 8 == 0, "moc_selected_grouped_down_bf16: intermediate must be a multiple of 8");
   if (sparse28_applies(nb, k, inter)) {
@@ -587,7 +589,7 @@ extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, i
     int rc = moc_pack28_bf16(sz, idx, nb, inter, base, p.ld_ap, meta, p.meta_rows,
                              gbytes > 0 ? gws : nullptr, stream);
     if (rc != MOC_OK) return rc;
-    return moc_sparse28_down_bf16(base, p.ld_ap, meta, p.meta_rows, nb, inter, w_down_t, hidden, 0, hidden,
+    return moc_sparse28_down_bf16(base, p.ld_ap, meta, p.meta_rows, nb, inter, w_down_t, ldw_down, 0, hidden,
                                   y, hidden, gbytes > 0 ? gws : nullptr, gbytes, stream);
   }
   int rc = moc_scatter_sparse_to_dense(MOC_BF16, sz, idx, MOC_I64, nb, k, inter, workspace, inter,
@@ -603,7 +605,7 @@ extern "C" int moc_selected_grouped_down_bf16(const void* sz, const void* idx, i
     if (rc != MOC_OK) return rc;
   }
   // y[nb, hidden] = z[nb, inter] (K-contiguous) x W_down^T[inter, hidden] (N-contiguous)
-  return moc_gemm_ws(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, hidden, 1, 0,
+  return moc_gemm_ws(MOC_BF16, nb, hidden, inter, workspace, inter, 1, w_down_t, ldw_down, 1, 0,
                      nullptr, 0, 0, nullptr, 0, 0, y, hidden, MOC_BF16, gbytes > 0 ? gws : nullptr,
                      gbytes, stream);
 }
@@ -628,8 +630,8 @@ extern "C" int moc_grouped_top2_up_silu_rmsnorm_bf16(const void* x, int64_t nb, 
 }
 
 extern "C" int moc_selected_grouped_down_residual_bf16(const void* sz, const void* idx, int64_t nb,
-                                                       int64_t k, const void* w_down_t, int64_t inter,
-                                                       int64_t hidden, const void* residual, void* y,
+                                                       int64_t k, const void* w_down_t, int64_t ldw_down,
+                                                       int64_t inter, int64_t hidden, const void* residual, void* y,
                                                        void* workspace, int64_t workspace_bytes,
                                                        void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 64, "moc_selected_grouped_down_residual_bf16: 0 <= nb <= 64 tokens");
@@ -637,6 +639,6 @@ extern "C" int moc_selected_grouped_down_residual_bf16(const void* sz, const voi
               "moc_selected_grouped_down_residual_bf16: bad shape");
   if (nb == 0) return MOC_OK;
   MOC_REQUIRE(residual != nullptr, "moc_selected_grouped_down_residual_bf16: null residual");
-  return selected_down_impl(sz, idx, MOC_I64, nb, k, w_down_t, inter, hidden, residual, y, workspace,
+  return selected_down_impl(sz, idx, MOC_I64, nb, k, w_down_t, ldw_down, inter, hidden, residual, y, workspace,
                             workspace_bytes, stream);
 }

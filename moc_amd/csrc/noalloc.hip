@@ -87,8 +87,8 @@ using namespace moc;
 
 extern "C" int moc_global_after_gate_noalloc_bf16(const void* x, const void* gate_scores, int64_t nb,
                                                   int64_t inter, int64_t hidden, const void* w_up,
-                                                  const void* w_down_t, int64_t k, const void* residual,
-                                                  void* y, void* idx_out, void* stream) {
+                                                  const void* w_down_t, int64_t ldw_down, int64_t k,
+                                                  const void* residual, void* y, void* idx_out, void* stream) {
   MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_global_after_gate_noalloc_bf16: 0 <= nb <= 16 tokens");
   MOC_REQUIRE(inter >= 1 && inter <= 16384 && hidden >= 64 && hidden % 64 == 0,
               "moc_global_after_gate_noalloc_bf16: bad shape");
@@ -102,6 +102,6 @@ extern "C" int moc_global_after_gate_noalloc_bf16(const void* x, const void* gat
   void* ws = nullptr;
   const int rc = scratch_of_current_device(&ws, stream);
   if (rc != MOC_OK) return rc;
-  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, k, residual, y, idx_out, ws,
+  return global_after_gate(x, gate_scores, nb, inter, hidden, w_up, w_down_t, ldw_down, k, residual, y, idx_out, ws,
                            MOC_NOALLOC_SCRATCH_BYTES, stream);
 }

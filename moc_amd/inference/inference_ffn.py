@@ -97,7 +97,11 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         w = self.down_proj.weight
         key = (w.data_ptr(), w._version, w.device, w.dtype)
         if self._down_weight_t_key != key:
-            self._down_weight_t = w.detach().transpose(0, 1).contiguous()
+            # [inter, hidden] at a row pitch of hidden + 64 (128 bytes): the
+            # decode kernels read one column block of it per workgroup down
+            # the selected rows, and a 4 KB pitch puts every row's block on
+            # the same memory channels
+            self._down_weight_t = K.down_weight_t_for_decode(w)
             self._down_weight_t_key = key
 
     def _group_offset(self, device: torch.device) -> torch.Tensor:

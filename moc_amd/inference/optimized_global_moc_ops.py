@@ -30,6 +30,12 @@ class OptimizedGlobalMoCExtension:
         self.lib = lib
 
     @staticmethod
+    def _rows_contiguous(w: torch.Tensor) -> bool:
+        """W_down^T may come with padded rows (the module's decode layout,
+        InferenceMoCSwiGLUFFN._down_weight_t): unit column stride suffices."""
+        return w.dim() == 2 and w.stride(1) == 1 and w.stride(0) >= w.shape[1]
+
+    @staticmethod
     def _require(cond: bool, msg: str) -> None:
         if not cond:
             raise RuntimeError(msg)
@@ -61,7 +67,7 @@ class OptimizedGlobalMoCExtension:
         r(sparse_z.dtype == torch.bfloat16, "sparse_z must be BF16")
         r(w_down_t.dtype == torch.bfloat16, "w_down_t must be BF16")
         r(idx.dtype == torch.int64, "idx must be int64")
-        r(sparse_z.is_contiguous() and idx.is_contiguous() and w_down_t.is_contiguous(),
+        r(sparse_z.is_contiguous() and idx.is_contiguous() and self._rows_contiguous(w_down_t),
           "inputs must be contiguous")
         return K.selected_down(sparse_z, idx, w_down_t)
 
@@ -73,7 +79,7 @@ class OptimizedGlobalMoCExtension:
                      (down_weight_t, "down_weight_t")):
             r(t.dtype == torch.bfloat16, f"{n} must be BF16")
         r(x.is_contiguous() and gate_scores.is_contiguous() and up_weight.is_contiguous()
-          and down_weight_t.is_contiguous(), "inputs must be contiguous")
+          and self._rows_contiguous(down_weight_t), "inputs must be contiguous")
         r(0 < k <= gate_scores.shape[1], "invalid k")
         return K.global_after_gate(x, gate_scores, up_weight, down_weight_t, int(k))
 
@@ -112,7 +118,7 @@ def make_optimized_global_moc_graph_runner(module, batch_size: int = 1):
     gate_buf = torch.empty(batch_size, inter, device=device, dtype=dtype)
     y_buf = torch.empty(batch_size, hidden, device=device, dtype=dtype)
     up_w = module.up_proj.weight.contiguous()
-    down_t = module._down_weight_t.contiguous()
+    down_t = module._down_weight_t  # [inter, hidden] rows at the module's padded pitch
     gate_w = module.gate_proj.weight.contiguous()
     if batch_size <= 16 and dtype == torch.bfloat16:
         # gate GEMV (+ dense U from 4 tokens on, same launch) and the

@@ -570,6 +570,37 @@ def _bf16_contig(*ts):
     return [t.contiguous() for t in ts]
 
 
+# Extra elements per row of the decode kernels' W_down^T (MOC_DOWN_T_PITCH_PAD
+# of include/moc_amd.h): 128 bytes, so that the rows' column blocks do not all
+# fall on the same memory channels.
+DOWN_T_PITCH_PAD = 64
+
+
+def down_weight_t_for_decode(down_weight: torch.Tensor) -> torch.Tensor:
+    """W_down [hidden, inter] -> W_down^T [inter, hidden] as the decode
+    kernels read it best: a view of rows at a pitch of round8(hidden) +
+    DOWN_T_PITCH_PAD elements (the pad is never read)."""
+    hidden, inter = down_weight.shape
+    pitch = round_up(hidden, 8) + DOWN_T_PITCH_PAD
+    buf = torch.empty((inter, pitch), dtype=down_weight.dtype, device=down_weight.device)
+    view = buf[:, :hidden]
+    view.copy_(down_weight.detach().t())
+    return view
+
+
+def _down_t_rows(wdt: torch.Tensor):
+    """(tensor, row pitch) of a bf16 W_down^T [inter, hidden]: a view with
+    unit column stride, 16-byte aligned rows and a pitch of a multiple of 8
+    is passed as it is; anything else is made contiguous."""
+    if wdt.dtype != torch.bfloat16:
+        raise ValueError(f"expected bfloat16, got {wdt.dtype}")
+    if (wdt.dim() == 2 and wdt.stride(1) == 1 and wdt.stride(0) >= wdt.shape[1]
+            and wdt.stride(0) % 8 == 0 and wdt.data_ptr() % 16 == 0):
+        return wdt, wdt.stride(0)
+    c = wdt.contiguous()
+    return c, c.shape[1] if c.dim() == 2 else 0
+
+
 def selected_up_silu(x, topk_vals, topk_idx, up_weight) -> torch.Tensor:
     N.require_device(x, topk_vals, topk_idx, up_weight)
     x, vals, w = _bf16_contig(x, topk_vals, up_weight)
@@ -584,7 +615,8 @@ def selected_up_silu(x, topk_vals, topk_idx, up_weight) -> torch.Tensor:
 
 def selected_down(sparse_z, topk_idx, down_weight_t) -> torch.Tensor:
     N.require_device(sparse_z, topk_idx, down_weight_t)
-    z, wdt = _bf16_contig(sparse_z, down_weight_t)
+    (z,) = _bf16_contig(sparse_z)
+    wdt, ldw = _down_t_rows(down_weight_t)
     idx = topk_idx.contiguous()
     nb, k = z.shape
     inter, hidden = wdt.shape
@@ -592,7 +624,7 @@ def selected_down(sparse_z, topk_idx, down_weight_t) -> torch.Tensor:
     ws_bytes = N.query("moc_selected_down_workspace_size", nb, k, hidden)
     ws = _empty((max(ws_bytes, 1),), torch.uint8, z.device)
     N.call("moc_selected_down_bf16", z.data_ptr(), idx.data_ptr(), N.idx_code(idx.dtype), nb, k,
-           wdt.data_ptr(), inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(z))
+           wdt.data_ptr(), ldw, inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(z))
     return y
 
 
@@ -620,7 +652,8 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
     `idx_out` (int32 [nb, k]) receives the selected channels in ascending
     order.  Without `workspace`, the stream's shared workspace is used."""
     N.require_device(x, gate_scores, up_weight, down_weight_t, idx_out)
-    x, g, wu, wdt = _bf16_contig(x, gate_scores, up_weight, down_weight_t)
+    x, g, wu = _bf16_contig(x, gate_scores, up_weight)
+    wdt, ldw = _down_t_rows(down_weight_t)
     nb, hidden = x.shape
     inter = g.shape[1]
     if wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
@@ -651,14 +684,14 @@ def global_after_gate(x, gate_scores, up_weight, down_weight_t, k: int, *, works
         raise ValueError(f"global_after_gate: workspace of {ws_bytes} bytes required")
     if residual is None:
         N.call("moc_global_after_gate_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
-               wu.data_ptr(), wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out),
+               wu.data_ptr(), wdt.data_ptr(), ldw, int(k), y.data_ptr(), N.ptr(idx_out),
                workspace.data_ptr(), ws_bytes, N.stream_of(x))
         return y
     r = residual.reshape(nb, hidden)
     if r.dtype != torch.bfloat16 or not r.is_contiguous():
         raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
     N.call("moc_global_after_gate_residual_bf16", x.data_ptr(), g.data_ptr(), nb, inter, hidden,
-           wu.data_ptr(), wdt.data_ptr(), int(k), r.data_ptr(), y.data_ptr(), N.ptr(idx_out),
+           wu.data_ptr(), wdt.data_ptr(), ldw, int(k), r.data_ptr(), y.data_ptr(), N.ptr(idx_out),
            workspace.data_ptr(), ws_bytes, N.stream_of(x))
     return y
 
@@ -675,7 +708,8 @@ def global_decode(x, gate_weight, up_weight, down_weight_t, k: int, *, workspace
     then Top-K + selected Up * SiLU + selected Down; the result of
     global_after_gate(x, gemv(x, gate_weight), ...)."""
     N.require_device(x, gate_weight, up_weight, down_weight_t, idx_out)
-    x, wg, wu, wdt = _bf16_contig(x, gate_weight, up_weight, down_weight_t)
+    x, wg, wu = _bf16_contig(x, gate_weight, up_weight)
+    wdt, ldw = _down_t_rows(down_weight_t)
     nb, hidden = x.shape
     inter = wg.shape[0]
     if nb > 16:
@@ -692,7 +726,7 @@ def global_decode(x, gate_weight, up_weight, down_weight_t, k: int, *, workspace
     elif workspace.numel() < ws_bytes:
         raise ValueError(f"global_decode: workspace of {ws_bytes} bytes required")
     N.call("moc_global_decode_bf16", x.data_ptr(), nb, hidden, wg.data_ptr(), wu.data_ptr(), inter,
-           wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out), workspace.data_ptr(), ws_bytes,
+           wdt.data_ptr(), ldw, int(k), y.data_ptr(), N.ptr(idx_out), workspace.data_ptr(), ws_bytes,
            N.stream_of(x))
     return y
 
@@ -704,7 +738,8 @@ def global_decode_rmsnorm_residual(x, norm_weight, eps: float, gate_weight, up_w
     norm inside the gate/up GEMV, the residual added by the after-gate
     kernel (moc_global_decode_rmsnorm_residual_bf16)."""
     N.require_device(x, norm_weight, gate_weight, up_weight, down_weight_t, idx_out)
-    x, nw, wg, wu, wdt = _bf16_contig(x, norm_weight, gate_weight, up_weight, down_weight_t)
+    x, nw, wg, wu = _bf16_contig(x, norm_weight, gate_weight, up_weight)
+    wdt, ldw = _down_t_rows(down_weight_t)
     nb, hidden = x.shape
     inter = wg.shape[0]
     if nb > 4:
@@ -722,7 +757,7 @@ def global_decode_rmsnorm_residual(x, norm_weight, eps: float, gate_weight, up_w
     elif workspace.numel() < ws_bytes:
         raise ValueError(f"global_decode_rmsnorm_residual: workspace of {ws_bytes} bytes required")
     N.call("moc_global_decode_rmsnorm_residual_bf16", x.data_ptr(), nb, hidden, nw.data_ptr(), float(eps),
-           wg.data_ptr(), wu.data_ptr(), inter, wdt.data_ptr(), int(k), y.data_ptr(), N.ptr(idx_out),
+           wg.data_ptr(), wu.data_ptr(), inter, wdt.data_ptr(), ldw, int(k), y.data_ptr(), N.ptr(idx_out),
            workspace.data_ptr(), ws_bytes, N.stream_of(x))
     return y
 
@@ -819,8 +854,10 @@ def sparse28_down(ap, meta, inter: int, down_weight_t, *, workspace, out=None) -
     given transposed [inter, hidden]."""
     N.require_device(ap, meta, down_weight_t, workspace, out)
     nb = ap.shape[0]
-    wdt = down_weight_t if down_weight_t.is_contiguous() else down_weight_t.contiguous()
-    if wdt.shape[0] != inter or wdt.dtype != torch.bfloat16:
+    if down_weight_t.dtype != torch.bfloat16:
+        raise ValueError("down_weight_t must be a bf16 [inter, hidden] tensor")
+    wdt, _ = _down_t_rows(down_weight_t)
+    if wdt.shape[0] != inter:
         raise ValueError("down_weight_t must be a bf16 [inter, hidden] tensor")
     hidden = wdt.shape[1]
     nt, ld_ap, meta_rows = packed28_layout(nb, inter)
@@ -846,7 +883,8 @@ def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=N
     """y = sparse_z * W_down^T[idx]; with `residual` (<= 64 tokens),
     residual + y (bf16 add) from the same launches."""
     N.require_device(sparse_z, idx, down_weight_t, residual)
-    sz, wdt = _bf16_contig(sparse_z, down_weight_t)
+    (sz,) = _bf16_contig(sparse_z)
+    wdt, ldw = _down_t_rows(down_weight_t)
     ii = idx.contiguous()
     if ii.dtype != torch.int64:
         raise ValueError("idx must be int64")
@@ -859,18 +897,18 @@ def selected_grouped_down(sparse_z, idx, down_weight_t, *, out=None, workspace=N
     ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else \
         _empty((max(ws_bytes, 1),), torch.uint8, sz.device)
     if residual is None:
-        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
+        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(), ldw,
                inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
         return y
     r = residual.reshape(nb, hidden)
     if r.dtype != torch.bfloat16 or not r.is_contiguous():
         raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
     if nb > 64:
-        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(),
+        N.call("moc_selected_grouped_down_bf16", sz.data_ptr(), ii.data_ptr(), nb, k, wdt.data_ptr(), ldw,
                inter, hidden, y.data_ptr(), ws.data_ptr(), ws_bytes, N.stream_of(sz))
         y.copy_(r + y)
         return y
     N.call("moc_selected_grouped_down_residual_bf16", sz.data_ptr(), ii.data_ptr(), nb, k,
-           wdt.data_ptr(), inter, hidden, r.data_ptr(), y.data_ptr(), ws.data_ptr(), ws_bytes,
+           wdt.data_ptr(), ldw, inter, hidden, r.data_ptr(), y.data_ptr(), ws.data_ptr(), ws_bytes,
            N.stream_of(sz))
     return y

@@ -277,7 +277,9 @@ def test_extension_object_runner_shape(nb):
             p.copy_((torch.randn(p.shape, generator=g) * 0.02).to(torch.bfloat16))
     m._ensure_down_weight_t()
     x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
-    up_w, down_t = m.up_proj.weight.contiguous(), m._down_weight_t.contiguous()
+    # the module's own W_down^T (rows at its padded decode pitch), as the
+    # reference's runner passes it
+    up_w, down_t = m.up_proj.weight.contiguous(), m._down_weight_t
     with torch.no_grad():
         gate = m.gate_proj(x).contiguous()
     vals, idx = ext.cub_topk_bf16_512x11(gate, k)

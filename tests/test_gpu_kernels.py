@@ -664,6 +664,46 @@ def test_global_decode_layer_entry(nb, inter, d):
     close(y_one, y_ref)
 
 
+@pytest.mark.parametrize("nb", [1, 4, 16])
+def test_down_t_padded_pitch_same_bits(nb):
+    """W_down^T at the module's decode layout (rows padded by 128 bytes,
+    down_weight_t_for_decode) gives the same bits as the contiguous matrix
+    on every decode entry that reads it: the layer entries, the after-gate
+    kernel (plain and residual), the selected Down, the 2:8 selected Down."""
+    d, inter, k = 2048, 5461, 1024
+    g = gen(390 + nb)
+    x = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    res = torch.randn(nb, d, generator=g).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wd = (torch.randn(d, inter, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = wd.t().contiguous()
+    wdp = K().down_weight_t_for_decode(wd)
+    assert wdp.shape == wdt.shape and wdp.stride(0) == d + 64 and torch.equal(wdp, wdt)
+    ws = K().global_decode_workspace(nb, inter, k, d, DEV)
+    assert torch.equal(K().global_decode(x, wg, wu, wdp, k, workspace=ws),
+                       K().global_decode(x, wg, wu, wdt, k, workspace=ws))
+    if nb <= 4:
+        assert torch.equal(K().global_decode_rmsnorm_residual(x, nw, 1e-6, wg, wu, wdp, k, workspace=ws),
+                           K().global_decode_rmsnorm_residual(x, nw, 1e-6, wg, wu, wdt, k, workspace=ws))
+    G = K().gemv(x, wg)
+    for r in (None, res):
+        assert torch.equal(K().global_after_gate(x, G, wu, wdp, k, residual=r),
+                           K().global_after_gate(x, G, wu, wdt, k, residual=r))
+    vals, idx, _ = K().topk_rows(G, k)
+    z = K().selected_up_silu(x, vals, idx, wu)
+    assert torch.equal(K().selected_down(z, idx, wdp), K().selected_down(z, idx, wdt))
+    wd8 = (torch.randn(d, 5464, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wg8 = (torch.randn(5464, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu8 = (torch.randn(5464, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    idx8, sz8 = K().grouped_top2_up_silu(x, wg8, wu8)
+    wd8p, wd8t = K().down_weight_t_for_decode(wd8), wd8.t().contiguous()
+    assert torch.equal(K().selected_grouped_down(sz8, idx8, wd8p), K().selected_grouped_down(sz8, idx8, wd8t))
+    assert torch.equal(K().selected_grouped_down(sz8, idx8, wd8p, residual=res),
+                       K().selected_grouped_down(sz8, idx8, wd8t, residual=res))
+
+
 @pytest.mark.parametrize("nb", [1, 2, 3, 4])
 def test_global_decode_rmsnorm_residual(nb):
     """moc_global_decode_rmsnorm_residual_bf16: the decoder layer's FFN half

@@ -39,7 +39,7 @@ def test_library_exports_every_header_symbol(lib):
     assert set(names) == set(N.SIGNATURES), set(names) ^ set(N.SIGNATURES)
     for name in names:
         assert getattr(lib, name) is not None
-    assert lib.moc_abi_version() == 2
+    assert lib.moc_abi_version() == 3
 
 
 def test_validation_errors_without_device_work(lib):

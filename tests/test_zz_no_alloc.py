@@ -20,10 +20,10 @@ DEV = "cuda"
 def test_noalloc_rejects_oversized_shapes_before_device_work():
     lib = N.load()
     # 16 tokens of hidden 8192 and k 16384 need ~32 MB of partial sums
-    rc = lib.moc_global_after_gate_noalloc_bf16(None, None, 16, 16384, 8192, None, None, 16384, None,
-                                                None, None, None)
+    rc = lib.moc_global_after_gate_noalloc_bf16(None, None, 16, 16384, 8192, None, None, 8192, 16384,
+                                                None, None, None, None)
     assert rc == N.MOC_ERR_INVALID and "scratch" in N.last_error()
-    assert lib.moc_global_after_gate_noalloc_bf16(None, None, 0, 5461, 2048, None, None, 1024, None,
+    assert lib.moc_global_after_gate_noalloc_bf16(None, None, 0, 5461, 2048, None, None, 2048, 1024, None,
                                                   None, None, None) == N.MOC_OK
 
 
@@ -46,10 +46,10 @@ def _with_workspace(x, gate, wu, wdt, k, res):
     io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
     if res is None:
         N.call("moc_global_after_gate_bf16", x.data_ptr(), gate.data_ptr(), nb, inter, d, wu.data_ptr(),
-               wdt.data_ptr(), k, y.data_ptr(), io.data_ptr(), ws.data_ptr(), nbytes, N.stream_of(x))
+               wdt.data_ptr(), wdt.stride(0), k, y.data_ptr(), io.data_ptr(), ws.data_ptr(), nbytes, N.stream_of(x))
     else:
         N.call("moc_global_after_gate_residual_bf16", x.data_ptr(), gate.data_ptr(), nb, inter, d,
-               wu.data_ptr(), wdt.data_ptr(), k, res.data_ptr(), y.data_ptr(), io.data_ptr(),
+               wu.data_ptr(), wdt.data_ptr(), wdt.stride(0), k, res.data_ptr(), y.data_ptr(), io.data_ptr(),
                ws.data_ptr(), nbytes, N.stream_of(x))
     return y, io
 
@@ -60,7 +60,7 @@ def _no_alloc(x, gate, wu, wdt, k, res):
     y = torch.empty(nb, d, dtype=torch.bfloat16, device=DEV)
     io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
     N.call("moc_global_after_gate_noalloc_bf16", x.data_ptr(), gate.data_ptr(), nb, inter, d,
-           wu.data_ptr(), wdt.data_ptr(), k, None if res is None else res.data_ptr(), y.data_ptr(),
+           wu.data_ptr(), wdt.data_ptr(), wdt.stride(0), k, None if res is None else res.data_ptr(), y.data_ptr(),
            io.data_ptr(), N.stream_of(x))
     return y, io
 
@@ -105,7 +105,7 @@ def test_noalloc_captured_in_graph_matches_workspace_entry_point():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):  # captures on torch's own capture stream
         N.call("moc_global_after_gate_noalloc_bf16", xs.data_ptr(), gs.data_ptr(), nb, inter, d,
-               wu.data_ptr(), wdt.data_ptr(), k, rs.data_ptr(), y.data_ptr(), io.data_ptr(),
+               wu.data_ptr(), wdt.data_ptr(), wdt.stride(0), k, rs.data_ptr(), y.data_ptr(), io.data_ptr(),
                N.stream_of(xs))
     for rep in range(3):
         xn, gn, _, _, rn = _inputs(nb, d, inter, 960 + rep)
