@@ -386,7 +386,7 @@ def time_train_layer(m, x, go, steps, warmup, probe: list | None = None,
 GEMM_GU_TRAFFIC_BYTES = 1120.2e6 + 358.6e6
 # the same for the B=1 decode layer (the gate + dense-U GEMV pair, then the
 # column-owning select/down kernel), profiles/decode_B1_traffic.md
-DECODE_B1_TRAFFIC_BYTES = 44.79e6 + 0.09e6 + 4.58e6
+DECODE_B1_TRAFFIC_BYTES = 44.80e6 + 0.09e6 + 4.59e6
 
 
 def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
