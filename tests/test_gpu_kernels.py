@@ -820,6 +820,46 @@ def exact_projection_inputs(nb, d, inter, seed):
     return x, wg, wu, wd
 
 
+@pytest.mark.parametrize("nb", [1, 3, 4, 9, 16])
+def test_global_decode_exact_inputs_bitexact(nb):
+    """The layer entry (gate + dense-U GEMV, then the column-owning
+    after-gate kernel) on exact projections: G and U are the same bits on
+    the device and in the oracle whatever the accumulation order, and G holds
+    few distinct values (ties at the threshold in every row), so the
+    kernel's own selection (idx_out) is compared with the oracle's Top-K of
+    the exact G bit for bit without handing it the device's G; y within 2e-2
+    of the oracle (W_down^T at the module's padded row pitch)."""
+    d, inter, k = 2048, 5461, 1024
+    x, wg, wu, wd = exact_projection_inputs(nb, d, inter, 600 + nb)
+    xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    wdp = K().down_weight_t_for_decode(wd.to(DEV))
+    io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
+    y = K().global_decode(xd, wgd, wud, wdp, k, idx_out=io)
+    y_ref, idx_ref, _ = O.masked_reference(x, wg, wu, wd, k)
+    assert np.array_equal(io.cpu().numpy(), idx_ref)
+    close(y, y_ref)
+
+
+@pytest.mark.parametrize("hidden,inter,k", [(1024, 2736, 512), (2048, 5461, 1), (2048, 5461, 5461),
+                                            (2048, 5461, 4000), (256, 100, 7), (768, 8192, 2048)])
+def test_global_decode_layer_entry_shapes(hidden, inter, k):
+    """The column-owning layer at other shapes, on exact projections so
+    the selection is compared with the oracle's directly: k of 1 and of
+    every channel, k = 4000 of 5461 (the k-th largest gate value is
+    negative, below the selection's 32-binade window under the row maximum:
+    the byte-digit passes run), a 100-channel row, I = 8192 (16 channels per
+    thread); idx_out bit-exact, y within 2e-2 of the oracle, at 1 and 2
+    tokens."""
+    for nb in (1, 2):
+        x, wg, wu, wd = exact_projection_inputs(nb, hidden, inter, hidden + inter + k + nb)
+        io = torch.full((nb, k), -1, dtype=torch.int32, device=DEV)
+        y = K().global_decode(x.to(DEV), wg.to(DEV), wu.to(DEV), K().down_weight_t_for_decode(wd.to(DEV)), k,
+                              idx_out=io)
+        y_ref, idx_ref, _ = O.masked_reference(x, wg, wu, wd, k)
+        assert np.array_equal(io.cpu().numpy(), idx_ref), (nb, hidden, inter, k)
+        close(y, y_ref)
+
+
 @pytest.mark.parametrize("nb", [1, 4, 16, 64, 300, 4096])
 def test_grouped_2of8_1b_exact_inputs(nb):
     """MoC 2:8 at the 1b shape (config 4 at nb = 4096): with exact
