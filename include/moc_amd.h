@@ -454,6 +454,28 @@ int moc_grouped_top2_up_silu_bf16(const void* x, int64_t nb, int64_t hidden, con
                                   const void* w_up, int64_t inter, void* idx, void* sz,
                                   void* stream);
 
+/* Workspace bytes of moc_moc28_decode_bf16 (no zeroing needed). */
+int64_t moc_moc28_decode_workspace_size(int64_t nb, int64_t inter, int64_t hidden);
+
+/* The MoC 2:8 decode layer, nb <= 16 tokens: moc::fused_grouped_top2_up_silu
+ * followed by moc::selected_grouped_down (moc/inference/
+ * triton_grouped_moc_ops.py:26-131; inference_ffn.py:281-297) in two
+ * launches: G and U of every token in one GEMV launch, then one launch in
+ * which each workgroup picks the top 2 of every 8 channels of a token's G
+ * row (the selection, tie rule and z rounding of
+ * moc_grouped_top2_up_silu_bf16) and sums the token's selected Down rows
+ * for a block of output columns.  norm_w (optional, nb <= 4, hidden <= 4096):
+ * of RMSNorm(x) (rounding as in moc_gemv_rmsnorm_bf16).  residual
+ * (optional): y = bf16(residual + bf16(FFN)), the decoder's x + ffn(norm(x))
+ * when residual = x (benchmark_decode.py:303).  idx_out (optional): the
+ * selection, int64 [nb, inter / 4] as moc_grouped_top2_up_silu_bf16 writes
+ * it.  inter % 8 == 0 and <= 8192, hidden % 256 == 0; y must not alias x or
+ * the residual. */
+int moc_moc28_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* norm_w, float eps,
+                          const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t,
+                          int64_t ldw_down, const void* residual, void* y, void* idx_out, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+
 /* moc_grouped_top2_up_silu_bf16 of the RMSNorm'd tokens (rounding as in
  * moc_gemv_rmsnorm_bf16: the FFN's pre-norm fused into the gate/up
  * projection, benchmark_decode.py:101-109,303), nb <= 4, hidden <= 4096. */

@@ -109,6 +109,9 @@ SIGNATURES: dict[str, tuple] = {
     "moc_global_after_gate_bf16": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp,
                                           _vp, _i64, _vp]),
     "moc_grouped_top2_up_silu_bf16": (_int, [_vp, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]),
+    "moc_moc28_decode_workspace_size": (_i64, [_i64, _i64, _i64]),
+    "moc_moc28_decode_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp, _i64, _vp, _i64, _vp,
+                                     _vp, _vp, _vp, _i64, _vp]),
     "moc_grouped_top2_up_silu_rmsnorm_bf16": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp,
                                                      _i64, _vp, _vp, _vp]),
     "moc_selected_grouped_down_residual_bf16": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64,

@@ -774,11 +774,18 @@ constexpr int kSdMaxInter = 8192;
 constexpr int kSdMaxK = 4096;
 constexpr int kSdBatch = 16;
 
-template <int L, int CW>
+//
+// G28 (MoC 2:8): the selection is the top 2 of every group of 8 channels
+// (select_group_top2_bits, the rule and rounding of moc_grouped_top2_up_silu_bf16):
+// thread t's L channels are whole groups, so group g's two channels are
+// list entries 2g, 2g + 1 (top-1, then top-2: the reference's order) with
+// their z, and no threshold, ranks or scan are needed; k = inter / 4;
+// idx_out (optional) int64.  Otherwise idx_out (optional) int32.
+template <int L, int CW, bool G28>
 __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ld, int inter, int k,
     int hidden, int CB, const uint16_t* __restrict__ wdt, int64_t ldd, uint16_t* __restrict__ y,
-    const uint16_t* __restrict__ res, int* __restrict__ idx_out) {
+    const uint16_t* __restrict__ res, void* __restrict__ idx_out) {
   constexpr int NW = kSdThreads / 64;
   constexpr int CPT = L / 8;          // 16-byte chunks of a row per thread
   constexpr int Q = CW / 8;           // 16-byte chunks per row segment
@@ -822,7 +829,31 @@ __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
     }
   }
   __syncthreads();
-  {
+  if constexpr (G28) {
+    const int c0 = tid * L;
+    int64_t* io = (idx_out != nullptr && cb == 0) ? static_cast<int64_t*>(idx_out) + static_cast<int64_t>(b) * k
+                                                   : nullptr;
+#pragma unroll
+    for (int q8 = 0; q8 < L / 8; ++q8) {
+      const int c = c0 + 8 * q8;
+      if (c < inter) {  // inter is a multiple of 8: whole groups
+        const uint4 ga = g_st[c / 8], ua = u_st[c / 8];
+        const uint32_t gw[4] = {ga.x, ga.y, ga.z, ga.w}, uw[4] = {ua.x, ua.y, ua.z, ua.w};
+        int b1, b2;
+        uint16_t s1, s2;
+        select_group_top2_bits(gw, uw, b1, b2, s1, s2);
+        const int e = c / 4;
+        sch[e] = static_cast<uint16_t>(c + b1);
+        sch[e + 1] = static_cast<uint16_t>(c + b2);
+        zs[e] = bf16_to_f32(s1);
+        zs[e + 1] = bf16_to_f32(s2);
+        if (io != nullptr) {
+          io[e] = c + b1;
+          io[e + 1] = c + b2;
+        }
+      }
+    }
+  } else {
     const int c0 = tid * L;
     uint32_t w[sel_words<true, L>()];
 #pragma unroll
@@ -850,17 +881,17 @@ __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
     dv[j] = e < k ? *reinterpret_cast<const uint4*>(wdt + static_cast<int64_t>(sch[e]) * ldd + col)
                   : make_uint4(0, 0, 0, 0);
   }
-  {
+  if constexpr (!G28) {
     const uint16_t* graw = reinterpret_cast<const uint16_t*>(g_st);
     const uint16_t* uraw = reinterpret_cast<const uint16_t*>(u_st);
-    const bool write_idx = idx_out != nullptr && cb == 0;
+    int* io = (idx_out != nullptr && cb == 0) ? static_cast<int*>(idx_out) + static_cast<int64_t>(b) * k : nullptr;
     for (int e = tid; e < k; e += kSdThreads) {
       const int c = sch[e];
       zs[e] = round_bf16(round_bf16(silu_f32(bf16_to_f32(graw[c]))) * bf16_to_f32(uraw[c]));
-      if (write_idx) idx_out[static_cast<int64_t>(b) * k + e] = c;
+      if (io != nullptr) io[e] = c;
     }
+    __syncthreads();
   }
-  __syncthreads();
 
   // 2. column sums over the ranks
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -1109,15 +1140,15 @@ void launch_fused(const void* x, int hidden, const void* gate, int inter, int k,
 
 // Column-owning after-gate launch (select_down_kernel), CW columns per
 // workgroup.
-template <int CW>
+template <int CW, bool G28 = false>
 void launch_select_down_cw(const void* g, const void* u, int64_t ld, int nb, int inter, int k, int hidden,
-                           const void* wdt, int64_t ldd, void* y, const void* res, int* idx_out,
+                           const void* wdt, int64_t ldd, void* y, const void* res, void* idx_out,
                            hipStream_t st) {
   const int CB = hidden / CW;
   const dim3 grid(static_cast<unsigned>(nb * CB)), block(kSdThreads);
   const int per = (inter + kSdThreads - 1) / kSdThreads;
 #define MOC_SD(N)                                                                                  \
-  select_down_kernel<N, CW><<<grid, block, 0, st>>>((const uint16_t*)g, (const uint16_t*)u, ld, inter, k, \
+  select_down_kernel<N, CW, G28><<<grid, block, 0, st>>>((const uint16_t*)g, (const uint16_t*)u, ld, inter, k, \
                                                      hidden, CB, (const uint16_t*)wdt, ldd, (uint16_t*)y, \
                                                      (const uint16_t*)res, idx_out)
   if (per <= 8) MOC_SD(8);
@@ -1395,10 +1426,13 @@ namespace {
 // The column-owning layer: G and U of every token (of RMSNorm(x) when
 // norm_w != nullptr) in one GEMV launch, then select_down_kernel (with the
 // residual added when res != nullptr).  Workspace after the counters: U, G
-// (pitch sd_pitch(inter)), then xn [nb, hidden].
+// (pitch sd_pitch(inter)), then xn [nb, hidden].  g28: the MoC 2:8
+// selection (top 2 of every 8 channels, k = inter / 4, idx_out int64) in
+// place of the global Top-K (idx_out int32).
 int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm_w, float eps,
                      const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t, int64_t ldw_down,
-                     int64_t k, const void* res, void* y, void* idx_out, char* ws, hipStream_t st) {
+                     int64_t k, const void* res, void* y, void* idx_out, char* ws, hipStream_t st,
+                     bool g28 = false) {
   const int64_t pitch = sd_pitch(inter);
   void* u = ws + kFusedCounterBytes;
   void* gs = ws + kFusedCounterBytes + align256(nb * pitch * 2);
@@ -1427,12 +1461,14 @@ int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm
   if (rc != MOC_OK) return rc;
   // 64 columns per workgroup up to 8 tokens (<= 256 workgroups at hidden
   // 2048), 128 beyond (12-16 tokens: 32.0-32.5 -> 26.5-26.9 us per layer)
-  if (nb <= 8)
-    launch_select_down_cw<64>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res,
-                              static_cast<int*>(idx_out), st);
+  if (g28 && nb <= 8)
+    launch_select_down_cw<64, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+  else if (g28)
+    launch_select_down_cw<128, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+  else if (nb <= 8)
+    launch_select_down_cw<64>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else
-    launch_select_down_cw<128>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res,
-                               static_cast<int*>(idx_out), st);
+    launch_select_down_cw<128>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   return check_launch("select_down_kernel");
 }
 }  // namespace
@@ -1512,6 +1548,43 @@ extern "C" int moc_global_decode_rmsnorm_residual_bf16(const void* x, int64_t nb
               "moc_global_decode_rmsnorm_residual_bf16: workspace of %lld bytes required", (long long)need);
   return global_decode_sd(x, nb, hidden, norm_w, eps, w_gate, w_up, inter, w_down_t, ldw_down, k, x, y, idx_out,
                           static_cast<char*>(workspace), as_stream(stream));
+}
+
+extern "C" int64_t moc_moc28_decode_workspace_size(int64_t nb, int64_t inter, int64_t hidden) {
+  if (nb < 0 || inter < 8 || hidden < 1) return 0;
+  return kFusedCounterBytes + 2 * align256(nb * sd_pitch(inter) * 2) + align256(nb * hidden * 2);
+}
+
+// The MoC 2:8 decode layer (moc::fused_grouped_top2_up_silu followed by
+// moc::selected_grouped_down, moc/inference/triton_grouped_moc_ops.py:26-131)
+// in two launches: G and U of every token (of RMSNorm(x) when norm_w is
+// given) in one GEMV launch, then select_down_kernel with the top 2 of every
+// 8 channels, the residual added in its last step when given.
+extern "C" int moc_moc28_decode_bf16(const void* x, int64_t nb, int64_t hidden, const void* norm_w, float eps,
+                                     const void* w_gate, const void* w_up, int64_t inter, const void* w_down_t,
+                                     int64_t ldw_down, const void* residual, void* y, void* idx_out,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  MOC_REQUIRE(nb >= 0 && nb <= 16, "moc_moc28_decode_bf16: 0 <= nb <= 16 tokens");
+  MOC_REQUIRE(norm_w == nullptr || nb <= 4, "moc_moc28_decode_bf16: the fused RMSNorm takes nb <= 4 tokens");
+  MOC_REQUIRE(inter >= 8 && inter % 8 == 0 && inter <= kSdMaxInter,
+              "moc_moc28_decode_bf16: inter must be a multiple of 8 and <= %d", kSdMaxInter);
+  MOC_REQUIRE(hidden >= 256 && hidden % 256 == 0 && hidden < (1LL << 30) && (norm_w == nullptr || hidden <= 4096),
+              "moc_moc28_decode_bf16: hidden must be a multiple of 256 (<= 4096 with the fused RMSNorm)");
+  MOC_REQUIRE(eps >= 0.f, "moc_moc28_decode_bf16: eps must be >= 0");
+  if (nb == 0) return MOC_OK;
+  MOC_REQUIRE(x && w_gate && w_up && w_down_t && y, "moc_moc28_decode_bf16: null pointer");
+  MOC_REQUIRE(aligned16(x) && aligned16(w_gate) && aligned16(w_up) && aligned16(w_down_t) &&
+                  (norm_w == nullptr || aligned16(norm_w)),
+              "moc_moc28_decode_bf16: x, norm_w and weights must be 16-byte aligned");
+  MOC_REQUIRE(ldw_down >= hidden && ldw_down % 8 == 0,
+              "moc_moc28_decode_bf16: ldw_down must be a multiple of 8 and >= hidden");
+  MOC_REQUIRE(y != x && (residual == nullptr || residual != y),
+              "moc_moc28_decode_bf16: y must not alias x or the residual");
+  const int64_t need = moc_moc28_decode_workspace_size(nb, inter, hidden);
+  MOC_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "moc_moc28_decode_bf16: workspace of %lld bytes required", (long long)need);
+  return global_decode_sd(x, nb, hidden, norm_w, eps, w_gate, w_up, inter, w_down_t, ldw_down, inter / 4, residual,
+                          y, idx_out, static_cast<char*>(workspace), as_stream(stream), true);
 }
 
 extern "C" int moc_global_after_gate_residual_bf16(const void* x, const void* gate_scores, int64_t nb,

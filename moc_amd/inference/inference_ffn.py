@@ -134,6 +134,17 @@ class InferenceMoCSwiGLUFFN(nn.Module):
             self._decode_ws[(device, nb)] = ws
         return ws
 
+    def _moc28_decode_workspace(self, nb: int, device: torch.device) -> torch.Tensor:
+        """This module's workspace of the 2:8 decode layer entry for nb <= 16
+        tokens (G and U rows, the normalised tokens; no zeroing needed)."""
+        ws = self._decode_ws.get(("2:8", device, nb))
+        if ws is None:
+            c = self.config
+            nbytes = K.moc28_decode_workspace_bytes(nb, c.intermediate_size, c.hidden_size)
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            self._decode_ws[("2:8", device, nb)] = ws
+        return ws
+
     def _packed28_state(self, nb: int, device: torch.device):
         """Row views for nb tokens of this module's 2:4-packed operand
         buffers and zeroed sparse-Down workspace (MoC 2:8 prefill).  One set
@@ -248,6 +259,12 @@ class InferenceMoCSwiGLUFFN(nn.Module):
             ensure_native_ops_ready()
             self._ensure_down_weight_t()
             x_2d = x_2d.contiguous()
+            c = self.config
+            if K.moc28_decode_fits(x_2d.shape[0], c.intermediate_size, c.hidden_size, norm=True):
+                y = K.moc28_decode(x_2d, self.gate_proj.weight, self.up_proj.weight, self._down_weight_t,
+                                   norm_weight=norm_weight, eps=eps, residual=x_2d,
+                                   workspace=self._moc28_decode_workspace(x_2d.shape[0], x_2d.device))
+                return self._restore_output_shape(y, shp)
             idx, sz = K.grouped_top2_up_silu(x_2d, self.gate_proj.weight, self.up_proj.weight,
                                              norm_weight=norm_weight, eps=eps)
             y = K.selected_grouped_down(sz, idx, self._down_weight_t, residual=x_2d)
@@ -291,7 +308,15 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         y_buf = torch.empty(batch_size, h, device=device, dtype=dtype)
         wg = self.gate_proj.weight.contiguous()
         wu = self.up_proj.weight.contiguous()
-        if batch_size > 64 and dtype == torch.bfloat16:
+        if dtype == torch.bfloat16 and K.moc28_decode_fits(batch_size, inter, h):
+            # decode batches: the gate/up GEMV pair, then the top-2-of-8 and
+            # the selected Down in one launch
+            ws = self._moc28_decode_workspace(batch_size, device)
+            buffers = (x_buf, y_buf, ws)
+
+            def _run():
+                K.moc28_decode(x_buf, wg, wu, self._down_weight_t, workspace=ws, out=y_buf)
+        elif batch_size > 64 and dtype == torch.bfloat16:
             # prefill batches: the selection travels 2:4-packed from the
             # gate/up epilogue to the structured-sparse Down
             ap, meta = K.packed28_buffers(batch_size, inter, device)
@@ -352,6 +377,15 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         ensure_native_ops_ready()
         self._ensure_down_weight_t()
         x_2d, shp = self._flatten_decode_input(x)
+        c = self.config
+        if x_2d.dtype == torch.bfloat16 and K.moc28_decode_fits(x_2d.shape[0], c.intermediate_size,
+                                                                 c.hidden_size):
+            # decode: the gate/up GEMV pair, then one launch that selects the
+            # top 2 of every 8 channels and sums the selected Down rows
+            x_2d = x_2d.contiguous()
+            y = K.moc28_decode(x_2d, self.gate_proj.weight, self.up_proj.weight, self._down_weight_t,
+                               workspace=self._moc28_decode_workspace(x_2d.shape[0], x_2d.device))
+            return self._restore_output_shape(y, shp)
         if x_2d.shape[0] > 64 and x_2d.dtype == torch.bfloat16:
             # prefill: the gate/up epilogue writes the selection 2:4-packed and
             # the Down runs on the structured-sparse MFMA (no int64 indices)

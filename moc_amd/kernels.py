@@ -798,6 +798,60 @@ def grouped_top2_up_silu(x, gate_weight, up_weight, *, idx_out=None, sz_out=None
     return idx, sz
 
 
+def moc28_decode_fits(nb: int, inter: int, hidden: int, norm: bool = False) -> bool:
+    """Shapes moc_moc28_decode_bf16 takes (norm: with the fused RMSNorm)."""
+    return (1 <= nb <= (4 if norm else 16) and inter % 8 == 0 and 8 <= inter <= 8192
+            and hidden % 256 == 0 and (not norm or hidden <= 4096))
+
+
+def moc28_decode_workspace_bytes(nb: int, inter: int, hidden: int) -> int:
+    """Workspace bytes of moc28_decode (no zeroing needed)."""
+    return N.query("moc_moc28_decode_workspace_size", nb, inter, hidden)
+
+
+def moc28_decode(x, gate_weight, up_weight, down_weight_t, *, norm_weight: torch.Tensor | None = None,
+                 eps: float = 1e-6, residual: torch.Tensor | None = None, workspace=None, out=None,
+                 idx_out: torch.Tensor | None = None) -> torch.Tensor:
+    """The MoC 2:8 decode layer (<= 16 tokens) in two launches
+    (moc_moc28_decode_bf16): the gate/up GEMV pair of x (of RMSNorm(x) with
+    norm_weight, <= 4 tokens), then the top 2 of every 8 channels and the
+    selected Down, + residual when given.  Same selection (idx_out int64
+    [nb, inter/4]) and z as grouped_top2_up_silu, y as selected_grouped_down
+    in another f32 order."""
+    N.require_device(x, gate_weight, up_weight, down_weight_t, norm_weight, residual, idx_out)
+    x, wg, wu = _bf16_contig(x, gate_weight, up_weight)
+    wdt, ldw = _down_t_rows(down_weight_t)
+    nb, hidden = x.shape
+    inter = wg.shape[0]
+    if not moc28_decode_fits(nb, inter, hidden, norm_weight is not None):
+        raise ValueError(f"moc28_decode: unsupported shape nb={nb}, inter={inter}, hidden={hidden}")
+    if wg.shape != (inter, hidden) or wu.shape != (inter, hidden) or wdt.shape != (inter, hidden):
+        raise ValueError("gate_weight, up_weight and down_weight_t must be [intermediate, hidden]")
+    nw = None
+    if norm_weight is not None:
+        nw = norm_weight.contiguous()
+        if nw.dtype != torch.bfloat16 or nw.shape != (hidden,):
+            raise ValueError("norm_weight must be a bf16 [hidden] tensor")
+    r = None
+    if residual is not None:
+        r = residual.reshape(nb, hidden)
+        if r.dtype != torch.bfloat16 or not r.is_contiguous():
+            raise ValueError("residual must be a contiguous bf16 [nb, hidden] tensor")
+    if idx_out is not None and (idx_out.dtype != torch.int64 or idx_out.shape != (nb, inter // 4)
+                                or not idx_out.is_contiguous()):
+        raise ValueError(f"idx_out must be a contiguous int64 [{nb}, {inter // 4}] tensor")
+    y = _empty((nb, hidden), torch.bfloat16, x.device) if out is None else out
+    ws_bytes = moc28_decode_workspace_bytes(nb, inter, hidden)
+    if workspace is None:
+        workspace = _decode_workspace(x.device, ws_bytes)
+    elif workspace.numel() < ws_bytes:
+        raise ValueError(f"moc28_decode: workspace of {ws_bytes} bytes required")
+    N.call("moc_moc28_decode_bf16", x.data_ptr(), nb, hidden, N.ptr(nw), float(eps), wg.data_ptr(),
+           wu.data_ptr(), inter, wdt.data_ptr(), ldw, N.ptr(r), y.data_ptr(), N.ptr(idx_out),
+           workspace.data_ptr(), ws_bytes, N.stream_of(x))
+    return y
+
+
 def packed28_layout(nb: int, inter: int) -> tuple[int, int, int]:
     """(channel tiles, ld_ap, meta_rows) of the 2:4-packed 2:8 operand."""
     nt = (inter + 63) // 64

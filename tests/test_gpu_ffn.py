@@ -306,10 +306,11 @@ def test_extension_object_runner_shape(nb):
     close(y1, y_ref, 2e-2, 2e-2, "after_gate y")
 
 
-@pytest.mark.parametrize("nb", [1, 64, 4096])
+@pytest.mark.parametrize("nb", [1, 16, 17, 64, 4096])
 def test_inference_moc28_modes(nb):
     """InferenceMoCSwiGLUFFN in MoC 2:8 mode (config 4 at nb = 4096) against
-    the oracle's masked_reference on every row.  The gate/up weights have
+    the oracle's masked_reference on every row: the one-entry decode layer
+    (up to 16 tokens), the two-kernel path (17-64), the packed prefill path.  The gate/up weights have
     integer multiples of 2^-7 and the tokens integer entries in [-1, 1], so
     G and U are exact in any accumulation order and the selection is
     compared on identical values (bit-exact indices checked through

@@ -878,6 +878,82 @@ def test_grouped_2of8_1b_exact_inputs(nb):
     close(y, O.selected_down(sz_ref, idx_ref, wdt))
 
 
+@pytest.mark.parametrize("nb", [1, 3, 4, 9, 16])
+def test_moc28_decode_exact_inputs(nb):
+    """The 2:8 decode layer entry (gate/up GEMV pair, then one launch that
+    picks the top 2 of every 8 channels and sums the selected Down rows per
+    column block) on exact projections: its selection (idx_out) equals the
+    oracle's bit for bit on every group, ties included, without handing it
+    the device's G; y within 2e-2 of the oracle's Down of the oracle's sz;
+    the residual form equals residual + y bit for bit (one rounding of the
+    FFN, then of the sum); W_down^T at the module's padded pitch."""
+    d, inter = 2048, 5464
+    x, wg, wu, wd = exact_projection_inputs(nb, d, inter, 640 + nb)
+    idx_ref, sz_ref, _ = O.grouped_top2_up_silu(x, wg, wu)
+    xd, wgd, wud = x.to(DEV), wg.to(DEV), wu.to(DEV)
+    wdp = K().down_weight_t_for_decode(wd.to(DEV))
+    io = torch.full((nb, inter // 4), -1, dtype=torch.int64, device=DEV)
+    y = K().moc28_decode(xd, wgd, wud, wdp, idx_out=io)
+    assert np.array_equal(io.cpu().numpy(), idx_ref)
+    wdt = wd.t().contiguous()
+    close(y, O.selected_down(sz_ref, idx_ref, wdt))
+    y_two = K().selected_grouped_down(*reversed(K().grouped_top2_up_silu(xd, wgd, wud)), wdp)
+    close(y, y_two)
+    res = torch.randn(nb, d, generator=gen(650 + nb)).to(torch.bfloat16).to(DEV)
+    assert torch.equal(K().moc28_decode(xd, wgd, wud, wdp, residual=res), res + y)
+
+
+@pytest.mark.parametrize("nb", [1, 2, 3, 4])
+def test_moc28_decode_rmsnorm_residual(nb):
+    """The 2:8 decode layer as the decoder's FFN half x + FFN(RMSNorm(x)):
+    its norm and gate rows are the gemv_rmsnorm kernel's (same bits), so the
+    selection equals the oracle's top-2-of-8 of gemv_rmsnorm's G bit for bit;
+    y within 2e-2 of bf16(x + bf16(oracle FFN of gemv_rmsnorm's xn)); the
+    same as the two-kernel 2:8 path (norm inside the gate/up kernel, the
+    residual inside the selected Down) within 2e-2; a second call on the
+    same workspace gives the same bits."""
+    d, inter, eps = 2048, 5464, 1e-6
+    g = gen(660 + nb)
+    x = (torch.randn(nb, d, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(DEV)
+    wg = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(inter, d, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    wdt = K().down_weight_t_for_decode((torch.randn(d, inter, generator=g) * 0.02).to(torch.bfloat16).to(DEV))
+    G, xn = K().gemv_rmsnorm(x, nw, eps, wg)
+    U = K().gemv(xn, wu)
+    io = torch.full((nb, inter // 4), -1, dtype=torch.int64, device=DEV)
+    ws = torch.zeros(N().query("moc_moc28_decode_workspace_size", nb, inter, d), dtype=torch.uint8, device=DEV)
+    y = K().moc28_decode(x, wg, wu, wdt, norm_weight=nw, eps=eps, residual=x, workspace=ws, idx_out=io)
+    assert torch.equal(y, K().moc28_decode(x, wg, wu, wdt, norm_weight=nw, eps=eps, residual=x, workspace=ws))
+    wd_cpu = wdt[:, :d].cpu().t().contiguous()
+    ffn_ref, idx_ref, _ = O.masked_reference(xn.cpu(), wg.cpu(), wu.cpu(), wd_cpu, inter // 4, grouped=True,
+                                             g_override=G.cpu(), u_override=U.cpu())
+    assert np.array_equal(io.cpu().numpy(), idx_ref)
+    close(y, (x.cpu().float() + ffn_ref.float()).to(torch.bfloat16))
+    idx2, sz2 = K().grouped_top2_up_silu(x, wg, wu, norm_weight=nw, eps=eps)
+    assert torch.equal(idx2, io)
+    close(y, K().selected_grouped_down(sz2, idx2, wdt, residual=x))
+
+
+@pytest.mark.parametrize("nb,hidden,inter", [(1, 256, 8), (16, 256, 8), (2, 768, 8192), (12, 768, 8192),
+                                             (5, 1024, 2736), (1, 2048, 4096), (16, 2048, 4104),
+                                             (8, 4096, 1024)])
+def test_moc28_decode_shapes(nb, hidden, inter):
+    """The 2:8 decode layer at other shapes on exact projections: one group
+    (inter 8, k 2), the largest inter (8192, two groups per thread), inter
+    either side of the one-group-per-thread limit (4096 / 4104), 64- and
+    128-column workgroups (up to 8 tokens / beyond), column-block counts
+    that are and are not a multiple of the 8 XCDs; selection bit-exact
+    against the oracle, y within 2e-2."""
+    x, wg, wu, wd = exact_projection_inputs(nb, hidden, inter, 670 + nb + inter)
+    idx_ref, sz_ref, _ = O.grouped_top2_up_silu(x, wg, wu)
+    io = torch.full((nb, inter // 4), -1, dtype=torch.int64, device=DEV)
+    y = K().moc28_decode(x.to(DEV), wg.to(DEV), wu.to(DEV), K().down_weight_t_for_decode(wd.to(DEV)),
+                         idx_out=io)
+    assert np.array_equal(io.cpu().numpy(), idx_ref), (nb, hidden, inter)
+    close(y, O.selected_down(sz_ref, idx_ref, wd.t().contiguous()))
+
+
 def plain_linear(x, w):
     """x @ w.T on the MFMA GEMM without a K split (moc_gemm with no
     workspace): the accumulation order of the 2:8 selecting GEMM."""

@@ -62,6 +62,16 @@ def test_validation_errors_without_device_work(lib):
     # rows == 0 is a no-op
     assert lib.moc_topk_rows(N.MOC_F32, None, 0, 10, 10, 3, 0, None, None, N.MOC_I32, None, 0, None) == N.MOC_OK
     assert lib.moc_moc28_effective_k(5461) == 1366
+    # the 2:8 decode layer: whole groups of 8, the fused norm up to 4 tokens
+    rc = lib.moc_moc28_decode_bf16(None, 1, 2048, None, 1e-6, None, None, 5461, None, 2048, None, None, None,
+                                   None, 0, None)
+    assert rc == N.MOC_ERR_INVALID and "multiple of 8" in N.last_error()
+    rc = lib.moc_moc28_decode_bf16(None, 5, 2048, ctypes.c_void_p(16), 1e-6, None, None, 5464, None, 2048, None,
+                                   None, None, None, 0, None)
+    assert rc == N.MOC_ERR_INVALID and "nb <= 4" in N.last_error()
+    assert lib.moc_moc28_decode_bf16(None, 0, 2048, None, 1e-6, None, None, 5464, None, 2048, None, None, None,
+                                     None, 0, None) == N.MOC_OK
+    assert lib.moc_moc28_decode_workspace_size(16, 5464, 2048) > 0
     assert lib.moc_selected_down_workspace_size(1, 1024, 2048) > 0
 
 
