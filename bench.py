@@ -457,13 +457,15 @@ def gemm_roofline(t, d, inter, k, ws, x, go, reps=10):
     }
 
 
-def decode_bench(nb, sets=8, groups=40, iters=50):
+def decode_bench(nb, sets=8, groups=40, iters=50, moc28=False):
     """Global-MoC decode layer (config 3): gate GEMV + Top-K + selected Up*SiLU
     + selected Down, captured in one HIP graph that walks `sets` distinct
-    weight sets (cold MALL), replayed groups x iters times."""
+    weight sets (cold MALL), replayed groups x iters times.  moc28: the MoC
+    2:8 decode layer instead (d_ffn 5464, top 2 of every 8 channels; the
+    reference's single-layer B=1 row, results/inference_ffn.md:19)."""
     import torch
     from moc_amd import kernels as K
-    d, inter, k = D1B, I1B, K1B
+    d, inter, k = (D1B, 5464, 5464 // 4) if moc28 else (D1B, I1B, K1B)
     gen = torch.Generator(device="cuda").manual_seed(1234)
     layers = []
     for _ in range(sets):
@@ -476,11 +478,17 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
     x = torch.randn(nb, d, device="cuda", generator=gen).to(torch.bfloat16)
     gate = [torch.empty(nb, inter, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
     ys = [torch.empty(nb, d, device="cuda", dtype=torch.bfloat16) for _ in range(sets)]
-    ws = K.global_decode_workspace(nb, inter, k, d, "cuda")
+    if moc28:
+        ws = torch.empty(K.moc28_decode_workspace_bytes(nb, inter, d), dtype=torch.uint8, device="cuda")
+    else:
+        ws = K.global_decode_workspace(nb, inter, k, d, "cuda")
 
     def run_all():
         for (wg, wu, wdt), y in zip(layers, ys):
-            K.global_decode(x, wg, wu, wdt, k, workspace=ws, out=y)
+            if moc28:
+                K.moc28_decode(x, wg, wu, wdt, workspace=ws, out=y)
+            else:
+                K.global_decode(x, wg, wu, wdt, k, workspace=ws, out=y)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -507,15 +515,26 @@ def decode_bench(nb, sets=8, groups=40, iters=50):
     # algorithmic bytes: all of W_gate + the union of selected rows of W_up and
     # W_down^T + activations (x in, G out+in, y out), counted from the masks
     union = []
-    for (wg, _, _), g in zip(layers, gate):
-        K.gemv(x, wg, out=g)
-        _, idx, _ = K.topk_rows(g, k, want_vals=False)
+    for (wg, wu, wdt), g in zip(layers, gate):
+        if moc28:
+            idx = torch.empty(nb, k, dtype=torch.int64, device="cuda")
+            K.moc28_decode(x, wg, wu, wdt, workspace=ws, idx_out=idx)
+        else:
+            K.gemv(x, wg, out=g)
+            _, idx, _ = K.topk_rows(g, k, want_vals=False)
         union.append(int(torch.unique(idx).numel()))
     u_avg = sum(union) / len(union)
     act = 2 * nb * d * 2 + 2 * nb * inter * 2
     bytes_layer = 2 * d * inter + 2 * 2 * d * u_avg + act
     st = summarize(samples)
     achieved = bytes_layer / (st["median"] * 1e-6) / 1e9
+    if moc28:
+        del layers, graph
+        torch.cuda.empty_cache()
+        return {"nb": nb, "us_median": round(st["median"], 3), "us_mean": round(st["mean"], 3),
+                "us_p10": round(st["p10"], 3), "us_p90": round(st["p90"], 3),
+                "union_rows": round(u_avg, 1), "bytes": int(bytes_layer),
+                "achieved_GBs": round(achieved, 1), "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)}
     # the gate GEMV alone, to report the dominant decode kernel separately
     g2 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g2):
@@ -1157,6 +1176,13 @@ def main():
             dec[nb] = decode_bench(nb, groups=args.decode_groups, iters=args.decode_iters)
         configs["3_decode_1b"] = {f"B{nb}": {**r, "tokens_per_s": round(nb / (r["us_median"] * 1e-6), 1)}
                                   for nb, r in dec.items()}
+        log("MoC 2:8 decode B=1/4/16")
+        configs["3b_moc28_decode_1b"] = {
+            "workload": "MoC 2:8 decode layer, d=2048, d_ffn=5464, top 2 of every 8 channels, bf16 "
+                        "(the reference's single-layer row: 56.011 us at B=1 on A800, "
+                        "results/inference_ffn.md:19)",
+            **{f"B{nb}": decode_bench(nb, groups=args.decode_groups, iters=args.decode_iters, moc28=True)
+               for nb in (1, 4, 16)}}
         log("config 4: 2:8 prefill")
         configs["4_moc28_prefill_4096"] = moc28_prefill_bench()
         log("config 5: 350m training step")
