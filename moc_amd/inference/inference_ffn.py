@@ -310,8 +310,10 @@ class InferenceMoCSwiGLUFFN(nn.Module):
         wu = self.up_proj.weight.contiguous()
         if dtype == torch.bfloat16 and K.moc28_decode_fits(batch_size, inter, h):
             # decode batches: the gate/up GEMV pair, then the top-2-of-8 and
-            # the selected Down in one launch
-            ws = self._moc28_decode_workspace(batch_size, device)
+            # the selected Down in one launch (a workspace of the runner's own:
+            # eager calls of the module never share it with the replays)
+            ws = torch.empty(max(K.moc28_decode_workspace_bytes(batch_size, inter, h), 256),
+                             dtype=torch.uint8, device=device)
             buffers = (x_buf, y_buf, ws)
 
             def _run():
