@@ -767,20 +767,20 @@ __global__ __launch_bounds__(kUdThreads) void select_up_down_kernel(
 // the tokens' workgroups of a block, which read the same W_down^T rows where
 // their selections meet, and blocks sharing 128-byte lines use one L2.
 // Rows of G and U: pitch ld (a multiple of 8), 16-byte aligned; inter <=
-// kSdMaxInter, k <= kSdMaxK.
+// kSdMaxInter, k <= kSdMaxK; idx_out (optional) int32.
+// G28 (MoC 2:8): the selection in (0) is the top 2 of every group of 8
+// channels instead (select_group_top2_bits: the tie rule and the single
+// rounding z = bf16(SiLU(g) u) of moc_grouped_top2_up_silu_bf16): thread t's
+// L channels are whole groups, so group g's two channels become list
+// entries 2g, 2g + 1 (top-1, then top-2: the reference's order) with their
+// z, and no threshold, ranks, scan or step-(1) z pass are needed; k =
+// inter / 4; idx_out (optional) int64.
 // ---------------------------------------------------------------------------
 constexpr int kSdThreads = 512;
 constexpr int kSdMaxInter = 8192;
 constexpr int kSdMaxK = 4096;
 constexpr int kSdBatch = 16;
 
-//
-// G28 (MoC 2:8): the selection is the top 2 of every group of 8 channels
-// (select_group_top2_bits, the rule and rounding of moc_grouped_top2_up_silu_bf16):
-// thread t's L channels are whole groups, so group g's two channels are
-// list entries 2g, 2g + 1 (top-1, then top-2: the reference's order) with
-// their z, and no threshold, ranks or scan are needed; k = inter / 4;
-// idx_out (optional) int64.  Otherwise idx_out (optional) int32.
 template <int L, int CW, bool G28>
 __global__ __launch_bounds__(kSdThreads) void select_down_kernel(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ld, int inter, int k,
