@@ -937,14 +937,15 @@ def test_moc28_decode_rmsnorm_residual(nb):
 
 @pytest.mark.parametrize("nb,hidden,inter", [(1, 256, 8), (16, 256, 8), (2, 768, 8192), (12, 768, 8192),
                                              (5, 1024, 2736), (1, 2048, 4096), (16, 2048, 4104),
-                                             (8, 4096, 1024)])
+                                             (8, 4096, 1024), (2, 8192, 1024), (12, 6144, 2048)])
 def test_moc28_decode_shapes(nb, hidden, inter):
     """The 2:8 decode layer at other shapes on exact projections: one group
     (inter 8, k 2), the largest inter (8192, two groups per thread), inter
     either side of the one-group-per-thread limit (4096 / 4104), 64- and
     128-column workgroups (up to 8 tokens / beyond), column-block counts
-    that are and are not a multiple of the 8 XCDs; selection bit-exact
-    against the oracle, y within 2e-2."""
+    that are and are not a multiple of the 8 XCDs, hidden sizes past the
+    row-per-wave GEMV's 4096 (the streaming and pipelined GEMV forms);
+    selection bit-exact against the oracle, y within 2e-2."""
     x, wg, wu, wd = exact_projection_inputs(nb, hidden, inter, 670 + nb + inter)
     idx_ref, sz_ref, _ = O.grouped_top2_up_silu(x, wg, wu)
     io = torch.full((nb, inter // 4), -1, dtype=torch.int64, device=DEV)
