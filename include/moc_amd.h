@@ -256,7 +256,8 @@ int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, 
 /* The MoC FFN backward for rows tokens, bf16 operands, as one call
  * (_MoCFunction.backward, moc/ffn.py:175-259; _MoCGCPFunction.backward
  * :423-497): with s_s NULL (GCP) S and Z are recomputed from g_s, u_s and Z
- * scattered dense (s into s_tmp), else Z is scattered from z_s; dWd =
+ * scattered dense (S also into s_tmp when it is not NULL; the gradient step
+ * recomputes S from g_s, the same bits), else Z is scattered from z_s; dWd =
  * go^T Z, gZ = go W_down (into zbuf after Z), gG and gU dense from gZ, dWg =
  * gG^T x, dWu = gU^T x (stacked: one GEMM over [gG | gU], gu = gg + ld_ggu/2
  * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Weight gradients in

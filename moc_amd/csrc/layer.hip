@@ -151,7 +151,6 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
               "moc_ffn_backward_bf16: operands need 16-byte aligned rows (leading dimensions multiples of 8)");
   MOC_REQUIRE(idx && g_s && u_s && dwg && dwu && dwd && ld_dw >= d && lddwd >= inter,
               "moc_ffn_backward_bf16: null operand or bad leading dimension");
-  MOC_REQUIRE(s_s != nullptr || s_tmp != nullptr, "moc_ffn_backward_bf16: GCP needs s_tmp");
   MOC_REQUIRE(s_s == nullptr || z_s != nullptr, "moc_ffn_backward_bf16: saved S needs saved Z");
   const int64_t esz = grad_dtype == MOC_BF16 ? 2 : 4;
   const int64_t pitch = ld_ggu / 2;
@@ -169,7 +168,7 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
   if (s_s == nullptr) {
     // GCP: S = SiLU(G M), Z = S U M recomputed, Z scattered dense (:435-442)
     rc = moc_gcp_recompute_scatter(MOC_BF16, g_s, u_s, idx, idx_dtype, rows, k, inter, s_tmp, zbuf, ldz, stream);
-    s_use = s_tmp;
+    s_use = nullptr;  // the aux kernel recomputes S from g_s (the same bits) instead of reading it back
   } else {
     rc = moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
   }

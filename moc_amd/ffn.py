@@ -300,7 +300,8 @@ def _backward_common(grad_out, x, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w,
         return _layer_backward(x, x2, go, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gcp,
                                grad_dtype or down_w.dtype)
     if gcp and x.dtype == torch.bfloat16 and K.row_pitch(inter, torch.bfloat16) <= 8192:
-        s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter)
+        # S is not kept: the aux kernel recomputes it from g_s (the same bits)
+        s_s, z_full = K.gcp_recompute_scatter(g_s, u_s, idx, inter, want_s=False)
     else:
         if gcp:
             s_s, z_s = K.gcp_recompute(g_s, u_s)
@@ -350,7 +351,7 @@ def _layer_backward(x, x2, go, idx, g_s, u_s, s_s, z_s, gate_w, up_w, down_w, gc
     stacked = _stack_weight_grads(dev, inter, d, pitch, bf16)
     zbuf = torch.empty((rows, pitch), dtype=bf16, device=dev)
     ggu = torch.empty((rows, 2 * pitch), dtype=bf16, device=dev)
-    s_tmp = torch.empty((rows, kk), dtype=bf16, device=dev) if gcp else None
+    s_tmp = None  # GCP: the aux kernel recomputes S from g_s
     dx = torch.empty((rows, d), dtype=bf16, device=dev)
     if stacked:
         dw = torch.empty((2 * pitch, d), dtype=grad_dtype, device=dev)
@@ -690,7 +691,7 @@ def _block_backward_native(ctx, go, h2, rstd, norm_w, idx, g_s, u_s, s_s, z_s, g
     xn = torch.empty((rows, d), dtype=bf16, device=dev)
     zbuf = torch.empty((rows, pitch), dtype=bf16, device=dev)
     ggu = torch.empty((rows, 2 * pitch), dtype=bf16, device=dev)
-    s_tmp = torch.empty((rows, kk), dtype=bf16, device=dev) if ctx.gcp else None
+    s_tmp = None  # GCP: the aux kernel recomputes S from g_s
     dh = torch.empty((rows, d), dtype=bf16, device=dev)
     if stacked:
         dw = torch.empty((2 * pitch, d), dtype=grad_dtype, device=dev)

@@ -1192,3 +1192,27 @@ def test_after_gate_one_token_shapes(hidden, inter, k):
     close(y, O.selected_down(z_ref, idx_ref, wdt))
     yr = K().global_after_gate(xd, Gd, wud, wdtd, k, residual=res)
     assert torch.equal(yr, res + y)
+
+
+@pytest.mark.parametrize("rows,inter,k", [(4096, 5461, 1024), (300, 132, 100)])
+def test_backward_aux_recomputed_s_matches_gcp_recompute(rows, inter, k):
+    """The GCP backward keeps no S: the aux kernel recomputes it from g_s.
+    Its dL/dG and dL/dU equal, bit for bit, the ones computed from the GCP
+    recompute's own S (moc_gcp_recompute_scatter), on gate values spanning
+    zeros, negatives and large magnitudes."""
+    g = gen(950 + rows)
+    scores = torch.randn(rows, inter, generator=g).to(torch.bfloat16).to(DEV)
+    _, idx, _ = K().topk_rows(scores, k, idx_dtype=torch.int16, want_vals=False)
+    gs = (torch.randn(rows, k, generator=g) * 4).to(torch.bfloat16)
+    gs[:, :3] = torch.tensor([0.0, -0.0, 30.0])
+    gs, us = gs.to(DEV), torch.randn(rows, k, generator=g).to(torch.bfloat16).to(DEV)
+    gz = K().padded_empty(rows, inter, torch.bfloat16, DEV)
+    gz.copy_(torch.randn(rows, inter, generator=g).to(torch.bfloat16))
+    s_rec, _ = K().gcp_recompute_scatter(gs, us, idx, inter)
+    a = K().sparse_backward_aux(idx, gs, us, s_rec, gz, inter)
+    b = K().sparse_backward_aux(idx, gs, us, None, gz, inter)
+    w = (inter + 7) // 8 * 8
+    for p, q in zip(a, b):
+        pv = p.as_strided((rows, w), p.stride()).view(torch.int16)
+        qv = q.as_strided((rows, w), q.stride()).view(torch.int16)
+        assert torch.equal(pv, qv)
