@@ -148,7 +148,9 @@ int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const void* u_spa
  * grad_u = s*gz, grad_g = u*gz*SiLU'(g) (moc/training/triton_sparse_aux.py:
  * 363-423; bf16 follows the materialised-bf16 chain at :376-400, f32 the fused
  * kernel :139-182).  s_sparse may be NULL: s is then recomputed from g
- * (GCP, moc/ffn.py:435). */
+ * (GCP, moc/ffn.py:435).  gz_full may be grad_u itself (gz_ld == out_ld,
+ * bf16 with 16-byte aligned rows, pitch a multiple of 8 and <= 8192): each
+ * row's gZ is read whole before that row is written. */
 int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype, const void* g_sparse,
                             const void* u_sparse, const void* s_sparse, const void* gz_full,
                             int64_t gz_ld, int64_t rows, int64_t k, int64_t inter, void* grad_g,
@@ -260,8 +262,11 @@ int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, 
  * recomputes S from g_s, the same bits), else Z is scattered from z_s; dWd =
  * go^T Z, gZ = go W_down (into zbuf after Z), gG and gU dense from gZ, dWg =
  * gG^T x, dWu = gU^T x (stacked: one GEMM over [gG | gU], gu = gg + ld_ggu/2
- * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Weight gradients in
- * grad_dtype (MOC_BF16 or MOC_F32), dX in bf16. */
+ * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Where the stacked
+ * weight gradients and dWd both split K, they run as one grouped launch
+ * after the other steps (fewer K splits each, one reduction): gZ then goes
+ * into gu's rows and zbuf keeps Z.  Weight gradients in grad_dtype
+ * (MOC_BF16 or MOC_F32), dX in bf16. */
 int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* go, int64_t ldgo,
                           const void* x, int64_t ldx, const void* idx, int idx_dtype, const void* g_s,
                           const void* u_s, const void* s_s, const void* z_s, const void* wg, int64_t ldwg,

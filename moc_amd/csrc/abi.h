@@ -51,6 +51,19 @@ int launch_gate_up_2of8(const void* x, int64_t nb, int64_t hidden, const void* w
 int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* W1,
                   const float* W2, int64_t ldw, float* C1, float* C2, int64_t ldc, hipStream_t st);
 
+// Two bf16 GEMMs of split-K size (C1 [M1, N1] = A1 B1, C2 [M2, N2] = A2 B2,
+// strides as in moc_gemm_ws, output dtype c_dtype for both) as one grouped
+// split-K launch plus one reduction launch (gemm.hip).  Returns 1 without
+// launching when the grouped plan does not beat the two products apart or
+// the operands do not suit it; the caller then issues two GEMMs.
+// gemm_split_pair_workspace: its workspace bytes, 0 where it does not apply.
+int64_t gemm_split_pair_workspace(int64_t M1, int64_t N1, int64_t K1, int64_t M2, int64_t N2, int64_t K2);
+int gemm_split_pair(int64_t M1, int64_t N1, int64_t K1, const void* A1, int64_t a1_sm, int64_t a1_sk,
+                    const void* B1, int64_t b1_sk, int64_t b1_sn, void* C1, int64_t ldc1, int64_t M2, int64_t N2,
+                    int64_t K2, const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk,
+                    int64_t b2_sn, void* C2, int64_t ldc2, int c_dtype, void* workspace, int64_t workspace_bytes,
+                    hipStream_t st);
+
 }  // namespace moc
 
 #define MOC_REQUIRE(cond, ...)        \

@@ -157,6 +157,15 @@ struct GemmArgs {
   // decoder block's x + ffn(...) in the Down GEMM's epilogue.
   const uint16_t* res;
   int64_t ldres;
+  // Grouped split-K launch (gemm_pp_kernel<..., DUAL = false, SPLIT = true>,
+  // grp_wgs > 0): workgroups [0, grp_wgs) run the product above, the ones
+  // after them a second product of the same operand layouts with operands
+  // a[1], b[1] (nk[1] stays 0) and its own K tiles, extents, tiles, split
+  // and partial slices (grp_C, rows grp_ldc apart, grp_ws_stride apart).
+  int grp_wgs;
+  int grp_nk, grp_M, grp_N, grp_tiles_m, grp_tiles_n, grp_ksplit, grp_kper;
+  void* grp_C;
+  int64_t grp_ldc, grp_ws_stride;
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const Operand& o) {
@@ -922,10 +931,28 @@ void gemm_pp_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = wave >> 2;
   const int sw = wave & 3;
+  int bid = static_cast<int>(blockIdx.x);
+  if constexpr (SPLIT && !DUAL) {
+    if (g.grp_wgs > 0 && bid >= g.grp_wgs) {  // the grouped launch's second product
+      bid -= g.grp_wgs;
+      g.a[0] = g.a[1];
+      g.b[0] = g.b[1];
+      g.nk[0] = g.grp_nk;
+      g.M = g.grp_M;
+      g.N = g.grp_N;
+      g.tiles_m = g.grp_tiles_m;
+      g.tiles_n = g.grp_tiles_n;
+      g.ksplit = g.grp_ksplit;
+      g.kper = g.grp_kper;
+      g.C = g.grp_C;
+      g.ldc = g.grp_ldc;
+      g.ws_stride = g.grp_ws_stride;
+    }
+  }
   // split-K: workgroup bid runs K tiles [split * kper, +kper) of its tile
   // and writes an f32 partial tile into slice `split` of the workspace
-  const int split = SPLIT ? static_cast<int>(blockIdx.x % g.ksplit) : 0;
-  int tbid = SPLIT ? static_cast<int>(blockIdx.x / g.ksplit) : static_cast<int>(blockIdx.x);
+  const int split = SPLIT ? bid % g.ksplit : 0;
+  int tbid = SPLIT ? bid / g.ksplit : bid;
   // tail fix-up: workgroup fix_full + part * fix_tail + slot runs part
   // `part` of the K range of tile fix_full + slot
   int part = -1, slot = 0;
@@ -1226,13 +1253,11 @@ void gemm_pp_kernel(GemmArgs g) {
 // result does not depend on timing), converted to the output type.  One
 // thread per four consecutive columns of a row.
 template <bool OUT_F32>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t stride,
-                                                            int ksplit, int M, int N, int64_t ldw,
-                                                            void* __restrict__ C, int64_t ldc, int vec,
-                                                            const uint16_t* __restrict__ res = nullptr,
-                                                            int64_t ldres = 0) {
+__device__ __forceinline__ void splitk_reduce_quad(int64_t q, const float* __restrict__ ws, int64_t stride,
+                                                   int ksplit, int M, int N, int64_t ldw, void* __restrict__ C,
+                                                   int64_t ldc, int vec, const uint16_t* __restrict__ res,
+                                                   int64_t ldres) {
   const int qpr = (N + 3) / 4;
-  const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (q >= static_cast<int64_t>(M) * qpr) return;
   const int row = static_cast<int>(q / qpr), c = static_cast<int>(q % qpr) * 4;
   const float* p = ws + row * ldw + c;
@@ -1268,6 +1293,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
         dst[e] = static_cast<uint16_t>(pack_bf16x2(r[e], 0.0f) & 0xFFFF);
     }
   }
+}
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t stride,
+                                                            int ksplit, int M, int N, int64_t ldw,
+                                                            void* __restrict__ C, int64_t ldc, int vec,
+                                                            const uint16_t* __restrict__ res = nullptr,
+                                                            int64_t ldres = 0) {
+  splitk_reduce_quad<OUT_F32>(static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x, ws, stride, ksplit, M, N,
+                              ldw, C, ldc, vec, res, ldres);
+}
+
+// The sums of a grouped split-K launch's two products in one launch:
+// workgroups [0, blocks0) reduce the first, the rest the second.
+struct ReduceJob {
+  const float* ws;
+  int64_t stride;
+  int ksplit, M, N;
+  int64_t ldw;
+  void* C;
+  int64_t ldc;
+  int vec;
+};
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void splitk_reduce_pair_kernel(ReduceJob j0, ReduceJob j1, int blocks0) {
+  const bool second = static_cast<int>(blockIdx.x) >= blocks0;
+  const ReduceJob& j = second ? j1 : j0;
+  const int64_t q = static_cast<int64_t>(static_cast<int>(blockIdx.x) - (second ? blocks0 : 0)) * 256 + threadIdx.x;
+  splitk_reduce_quad<OUT_F32>(q, j.ws, j.stride, j.ksplit, j.M, j.N, j.ldw, j.C, j.ldc, j.vec, nullptr, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1698,6 +1753,60 @@ FixPlan plan_fix_short(int64_t M, int64_t N, int nk) {
   const int64_t tiles256 = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   if (3 * tiles256 > cu_count() || nk > kShortFixMaxKTiles) return FixPlan();
   return plan_fix_tiles(((M + 127) / 128) * ((N + kBN - 1) / kBN), nk);
+}
+
+// Two split-K products in one launch (the layer backward's weight gradients
+// at the 130m shape: dW_gu 48 tiles and dWd 24 tiles over K = 8192).  Apart,
+// each splits K until its tiles alone fill the CUs (5 and 10 ways: 63 MB of
+// f32 partials each, two GEMM and two reduction launches); together they
+// share the CUs with fewer splits (3 and 3: 57 MB of partials, one launch
+// of each kind).  Costs in K-tile times: kRound per launch (prologue,
+// epilogue, turnover), kReduce per reduction launch, and the partials'
+// bytes written and read back at kTileBytes per K-tile time.  Kept when it
+// beats the two products apart; bytes = 0 otherwise.
+struct PairSplitPlan {
+  SplitPlan p[2];
+  int64_t bytes = 0;  // arrival counters + both products' partials
+};
+
+PairSplitPlan plan_split_pair(int64_t M1, int64_t N1, int nk1, int64_t M2, int64_t N2, int nk2) {
+  constexpr double kRound = 5.0, kReduce = 1.0, kTileBytes = 8.7e6;
+  PairSplitPlan r;
+  const SplitPlan sep[2] = {plan_split(M1, N1, nk1), plan_split(M2, N2, nk2)};
+  if (sep[0].ksplit < 2 || sep[1].ksplit < 2) return r;
+  const int64_t cus = cu_count();
+  const int64_t M[2] = {M1, M2};
+  const int64_t ldw[2] = {(N1 + 3) & ~3LL, (N2 + 3) & ~3LL};
+  const int64_t t[2] = {((M1 + kBM - 1) / kBM) * ((N1 + kBN - 1) / kBN), ((M2 + kBM - 1) / kBM) * ((N2 + kBN - 1) / kBN)};
+  const int nk[2] = {nk1, nk2};
+  auto part_bytes = [&](int i, int ks) { return static_cast<double>(ks) * M[i] * ldw[i] * 4; };
+  double best = 0;
+  for (int i = 0; i < 2; ++i) best += kRound + sep[i].kper + kReduce + 2 * part_bytes(i, sep[i].ksplit) / kTileBytes;
+  int pick[2] = {0, 0}, per[2] = {0, 0};
+  for (int a = 2; a <= std::max(2, nk1 / 4); ++a) {
+    for (int b = 2; b <= std::max(2, nk2 / 4); ++b) {
+      const int kp[2] = {(nk1 + a - 1) / a, (nk2 + b - 1) / b};
+      const int ks[2] = {(nk1 + kp[0] - 1) / kp[0], (nk2 + kp[1] - 1) / kp[1]};
+      if (t[0] * ks[0] + t[1] * ks[1] > cus) continue;
+      const double cost =
+          kRound + std::max(kp[0], kp[1]) + kReduce + 2 * (part_bytes(0, ks[0]) + part_bytes(1, ks[1])) / kTileBytes;
+      if (cost < best) {
+        best = cost;
+        pick[0] = ks[0], pick[1] = ks[1];
+        per[0] = kp[0], per[1] = kp[1];
+      }
+    }
+  }
+  if (pick[0] == 0) return r;
+  r.bytes = kFixCounterBytes;
+  for (int i = 0; i < 2; ++i) {
+    r.p[i].ksplit = pick[i];
+    r.p[i].kper = per[i];
+    r.p[i].ldw = ldw[i];
+    r.p[i].bytes = static_cast<int64_t>(pick[i]) * M[i] * ldw[i] * 4;
+    r.bytes += r.p[i].bytes;
+  }
+  return r;
 }
 
 }  // namespace
@@ -2182,6 +2291,99 @@ int f32_gemm_pair(int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, 
   gemm_f32_tiled_kernel<true, true><<<grid, 512, 0, st>>>(a, static_cast<int>((K + kF32BK - 1) / kF32BK * kF32BK),
                                                           nullptr, 0, 0);
   return check_launch("gemm_f32_tiled_kernel (pair)");
+}
+
+namespace {
+
+// One bf16 product of a grouped launch: C [M, N] = A B over K, strides as
+// in moc_gemm_ws.  False when the 512-thread split kernel cannot take it.
+bool pair_product(int64_t M, int64_t N, int64_t K, const void* A, int64_t a_sm, int64_t a_sk, const void* B,
+                  int64_t b_sk, int64_t b_sn, int& la, int& lb, Operand& oa, Operand& ob) {
+  if (M <= 0 || N <= 0 || K <= 0 || M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31)) return false;
+  la = layout_of(a_sm, a_sk, M, K);
+  lb = layout_of(b_sn, b_sk, N, K);
+  if (la < 0 || lb < 0 || !aligned16(A) || !aligned16(B)) return false;
+  const int64_t lda = la ? a_sm : a_sk, ldb = lb ? b_sn : b_sk;
+  if (lda % 8 != 0 || ldb % 8 != 0 || lda < (la ? K : ((M + 7) & ~7LL)) || ldb < (lb ? K : ((N + 7) & ~7LL)))
+    return false;
+  if (!make_operand(A, lda, la == 1, M, K, oa) || !make_operand(B, ldb, lb == 1, N, K, ob)) return false;
+  auto no_wrap = [](const Operand& o) {
+    return static_cast<int64_t>(o.bytes) + 512 * o.ld + 4096 < (1LL << 32) && 512 * o.ld < (1LL << 31);
+  };
+  return no_wrap(oa) && no_wrap(ob);
+}
+
+}  // namespace
+
+int64_t gemm_split_pair_workspace(int64_t M1, int64_t N1, int64_t K1, int64_t M2, int64_t N2, int64_t K2) {
+  if (M1 <= 0 || N1 <= 0 || K1 <= 0 || M2 <= 0 || N2 <= 0 || K2 <= 0) return 0;
+  return plan_split_pair(M1, N1, static_cast<int>((K1 + kBK - 1) / kBK), M2, N2,
+                         static_cast<int>((K2 + kBK - 1) / kBK))
+      .bytes;
+}
+
+int gemm_split_pair(int64_t M1, int64_t N1, int64_t K1, const void* A1, int64_t a1_sm, int64_t a1_sk,
+                    const void* B1, int64_t b1_sk, int64_t b1_sn, void* C1, int64_t ldc1, int64_t M2, int64_t N2,
+                    int64_t K2, const void* A2, int64_t a2_sm, int64_t a2_sk, const void* B2, int64_t b2_sk,
+                    int64_t b2_sn, void* C2, int64_t ldc2, int c_dtype, void* workspace, int64_t workspace_bytes,
+                    hipStream_t st) {
+  if (c_dtype != MOC_BF16 && c_dtype != MOC_F32) return 1;
+  if (C1 == nullptr || C2 == nullptr || ldc1 < N1 || ldc2 < N2) return 1;
+  const int nk1 = static_cast<int>((K1 + kBK - 1) / kBK), nk2 = static_cast<int>((K2 + kBK - 1) / kBK);
+  const PairSplitPlan plan = K1 > 0 && K2 > 0 ? plan_split_pair(M1, N1, nk1, M2, N2, nk2) : PairSplitPlan();
+  if (plan.bytes == 0 || workspace == nullptr || workspace_bytes < plan.bytes || !aligned16(workspace)) return 1;
+  GemmArgs a{};
+  int la1, lb1, la2, lb2;
+  if (!pair_product(M1, N1, K1, A1, a1_sm, a1_sk, B1, b1_sk, b1_sn, la1, lb1, a.a[0], a.b[0]) ||
+      !pair_product(M2, N2, K2, A2, a2_sm, a2_sk, B2, b2_sk, b2_sn, la2, lb2, a.a[1], a.b[1]) || la1 != la2 ||
+      lb1 != lb2)
+    return 1;
+  const SplitPlan& p1 = plan.p[0];
+  const SplitPlan& p2 = plan.p[1];
+  float* ws1 = reinterpret_cast<float*>(static_cast<char*>(workspace) + kFixCounterBytes);
+  float* ws2 = reinterpret_cast<float*>(reinterpret_cast<char*>(ws1) + p1.bytes);
+  a.nk[0] = nk1;
+  a.nk[1] = 0;
+  a.M = static_cast<int>(M1);
+  a.N = static_cast<int>(N1);
+  a.C = ws1;
+  a.ldc = p1.ldw;
+  a.tiles_m = static_cast<int>((M1 + kBM - 1) / kBM);
+  a.tiles_n = static_cast<int>((N1 + kBN - 1) / kBN);
+  a.vec_store = 1;
+  a.pp = 1;
+  a.ksplit = p1.ksplit;
+  a.kper = p1.kper;
+  a.ws_stride = M1 * p1.ldw;
+  a.grp_wgs = a.tiles_m * a.tiles_n * p1.ksplit;
+  a.grp_nk = nk2;
+  a.grp_M = static_cast<int>(M2);
+  a.grp_N = static_cast<int>(N2);
+  a.grp_tiles_m = static_cast<int>((M2 + kBM - 1) / kBM);
+  a.grp_tiles_n = static_cast<int>((N2 + kBN - 1) / kBN);
+  a.grp_ksplit = p2.ksplit;
+  a.grp_kper = p2.kper;
+  a.grp_C = ws2;
+  a.grp_ldc = p2.ldw;
+  a.grp_ws_stride = M2 * p2.ldw;
+  const dim3 grid(static_cast<unsigned>(a.grp_wgs + a.grp_tiles_m * a.grp_tiles_n * p2.ksplit)), block(kPpThreads);
+  if (la1 && lb1) gemm_pp_kernel<true, true, true, false, true><<<grid, block, 0, st>>>(a);
+  else if (la1) gemm_pp_kernel<true, false, true, false, true><<<grid, block, 0, st>>>(a);
+  else if (lb1) gemm_pp_kernel<false, true, true, false, true><<<grid, block, 0, st>>>(a);
+  else gemm_pp_kernel<false, false, true, false, true><<<grid, block, 0, st>>>(a);
+  int rc = check_launch("gemm_pp_kernel (grouped split-K)");
+  if (rc != MOC_OK) return rc;
+  const int64_t esz = c_dtype == MOC_F32 ? 4 : 2;
+  auto vec = [&](const void* c, int64_t ldc) { return aligned16(c) && (ldc * esz) % 16 == 0 ? 1 : 0; };
+  const ReduceJob j1{ws1, M1 * p1.ldw, p1.ksplit, static_cast<int>(M1), static_cast<int>(N1), p1.ldw, C1, ldc1,
+                     vec(C1, ldc1)};
+  const ReduceJob j2{ws2, M2 * p2.ldw, p2.ksplit, static_cast<int>(M2), static_cast<int>(N2), p2.ldw, C2, ldc2,
+                     vec(C2, ldc2)};
+  const int64_t b1 = (M1 * ((N1 + 3) / 4) + 255) / 256, b2 = (M2 * ((N2 + 3) / 4) + 255) / 256;
+  const dim3 rgrid(static_cast<unsigned>(b1 + b2));
+  if (c_dtype == MOC_F32) splitk_reduce_pair_kernel<true><<<rgrid, 256, 0, st>>>(j1, j2, static_cast<int>(b1));
+  else splitk_reduce_pair_kernel<false><<<rgrid, 256, 0, st>>>(j1, j2, static_cast<int>(b1));
+  return check_launch("splitk_reduce_pair_kernel");
 }
 
 }  // namespace moc

@@ -132,6 +132,7 @@ extern "C" int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int6
   if (rows <= 0 || d <= 0 || inter <= 0) return 0;
   int64_t w = std::max(gemm_ws(d, inter, rows, 0), gemm_ws(rows, inter, d, 0));
   w = std::max(w, stacked ? gemm_ws(ld_ggu, d, rows, 0) : gemm_ws(inter, d, rows, 0));
+  if (stacked) w = std::max(w, moc::gemm_split_pair_workspace(ld_ggu, d, rows, d, inter, rows));
   return std::max(w, gemm_ws(rows, d, inter, inter));
 }
 
@@ -163,6 +164,12 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
   const int64_t need = moc_ffn_backward_workspace_size(rows, d, inter, ld_ggu, stacked);
   MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
               "moc_ffn_backward_bf16: workspace of %lld bytes required", (long long)need);
+  // Stacked weight gradients of split-K size run beside dWd as one grouped
+  // launch (one reduction), so Z must outlive gZ: gZ then goes into gU's
+  // rows and the aux kernel turns them into gG | gU in place.
+  const int64_t pair_ws = stacked ? moc::gemm_split_pair_workspace(2 * pitch, d, rows, d, inter, rows) : 0;
+  const bool grouped = pair_ws > 0 && workspace_bytes >= pair_ws && moc::aligned16(workspace) &&
+                       ld_ggu <= 8192 && moc::aligned16(gu);
   int rc;
   const void* s_use = s_s;
   if (s_s == nullptr) {
@@ -173,6 +180,30 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
     rc = moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
   }
   if (rc != MOC_OK) return rc;
+  if (grouped) {
+    // gZ = go W_down into gU's rows; gG, gU dense from it (:455-480)
+    rc = moc_gemm_ws(MOC_BF16, rows, inter, d, go, ldgo, 1, wd, ldwd, 1, 0, nullptr, 0, 0, nullptr, 0, 0, gu,
+                     ld_ggu, MOC_BF16, workspace, workspace_bytes, stream);
+    if (rc != MOC_OK) return rc;
+    rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_use, gu, ld_ggu, rows, k, inter, gg, gu,
+                                 ld_ggu, stream);
+    if (rc != MOC_OK) return rc;
+    // [dWg | dWu] = [gG | gU]^T x and dWd = go^T Z (:483-490, :447) in one launch
+    rc = moc::gemm_split_pair(2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, dwg, ld_dw, d, inter, rows, go, 1,
+                              ldgo, zbuf, ldz, 1, dwd, lddwd, grad_dtype, workspace, workspace_bytes,
+                              moc::as_stream(stream));
+    if (rc == 1) {  // not taken after all: the two products apart
+      rc = moc_gemm_ws(MOC_BF16, 2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, 0, nullptr, 0, 0, nullptr, 0, 0,
+                       dwg, ld_dw, grad_dtype, workspace, workspace_bytes, stream);
+      if (rc == MOC_OK)
+        rc = moc_gemm_ws(MOC_BF16, d, inter, rows, go, 1, ldgo, zbuf, ldz, 1, 0, nullptr, 0, 0, nullptr, 0, 0,
+                         dwd, lddwd, grad_dtype, workspace, workspace_bytes, stream);
+    }
+    if (rc != MOC_OK) return rc;
+    // dX = gG Wg + gU Wu (:491-497)
+    return moc_gemm_ws(MOC_BF16, rows, d, inter, gg, ld_ggu, 1, wg, ldwg, 1, inter, gu, ld_ggu, 1, wu, ldwu, 1,
+                       dx, lddx, MOC_BF16, workspace, workspace_bytes, stream);
+  }
   // dWd = go^T Z
   rc = moc_gemm_ws(MOC_BF16, d, inter, rows, go, 1, ldgo, zbuf, ldz, 1, 0, nullptr, 0, 0, nullptr, 0, 0, dwd,
                    lddwd, grad_dtype, workspace, workspace_bytes, stream);

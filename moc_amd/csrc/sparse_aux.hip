@@ -460,19 +460,22 @@ template <typename IdxT, bool VEC>
 __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     const IdxT* __restrict__ idx, const uint16_t* __restrict__ g_s,
     const uint16_t* __restrict__ u_s, const uint16_t* __restrict__ s_s,
-    const uint16_t* __restrict__ gz_full, int64_t gz_ld, int k, int64_t inter,
-    uint16_t* __restrict__ grad_g, uint16_t* __restrict__ grad_u, int64_t out_ld) {
+    const uint16_t* gz_full, int64_t gz_ld, int k, int64_t inter,
+    uint16_t* __restrict__ grad_g, uint16_t* grad_u, int64_t out_ld) {
   extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
   // an output row is inter values plus zeros up to a multiple of 8; rows
-  // are out_ld apart (out_ld may leave room for another tensor's rows)
+  // are out_ld apart (out_ld may leave room for another tensor's rows).
+  // gz_full may be grad_u itself (gz_ld == out_ld): the row's gZ values are
+  // staged whole before the barrier that precedes the row's stores.
   const int64_t width = out_row_width(inter, out_ld);
-  uint16_t* gzrow = rbuf;                  // [gz_ld]
-  uint16_t* ggrow = rbuf + gz_ld;          // [width]
-  uint16_t* gurow = rbuf + gz_ld + width;  // [width]
+  const int64_t gz_w = out_row_width(inter, gz_ld);
+  uint16_t* gzrow = rbuf;                 // [gz_w]
+  uint16_t* ggrow = rbuf + gz_w;          // [width]
+  uint16_t* gurow = rbuf + gz_w + width;  // [width]
   const int64_t row = blockIdx.x;
   RowEntries<IdxT, kRowThreadsBwd, VEC> r;
   r.load(idx, g_s, u_s, s_s, row, k, 0);
-  row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_ld);
+  row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_w);
   row_zero<kRowThreadsBwd>(ggrow, width);
   row_zero<kRowThreadsBwd>(gurow, width);
   __syncthreads();
@@ -699,10 +702,13 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
   if (rows == 0) return MOC_OK;
   MOC_REQUIRE(idx && g_sparse && u_sparse && gz_full && grad_g && grad_u,
               "moc_sparse_backward_aux: null pointer");
+  const bool in_place = gz_full == grad_u;
+  MOC_REQUIRE(gz_full != grad_g && (!in_place || gz_ld == out_ld),
+              "moc_sparse_backward_aux: gz_full may only be grad_u itself, with gz_ld == out_ld");
   if (dtype == MOC_BF16 && rows < (1LL << 31) && row_form_ok(gz_full, gz_ld) &&
       row_form_ok(grad_g, out_ld) && row_form_ok(grad_u, out_ld)) {
     hipStream_t st = as_stream(stream);
-    const size_t lds = static_cast<size_t>(gz_ld + 2 * out_row_width(inter, out_ld)) * 2;
+    const size_t lds = static_cast<size_t>(out_row_width(inter, gz_ld) + 2 * out_row_width(inter, out_ld)) * 2;
     const bool vec = entries_vec_ok(k, idx_dtype, idx, g_sparse, u_sparse, s_sparse);
 #define MOC_BWDR(T)                                                                                 \
   if (vec)                                                                                          \
@@ -719,6 +725,8 @@ extern "C" int moc_sparse_backward_aux(int dtype, const void* idx, int idx_dtype
 #undef MOC_BWDR
     return check_launch("backward_aux_rows_kernel");
   }
+  MOC_REQUIRE(!in_place, "moc_sparse_backward_aux: gZ in grad_u's rows needs the bf16 row form (16-byte aligned "
+                         "rows, pitch a multiple of 8 and <= %lld)", (long long)kRowMaxLd);
   const int64_t esz = dtype == MOC_BF16 ? 2 : 4;
   MOC_REQUIRE(rows <= 65535 || out_row_width(inter, out_ld) == out_ld,
               "moc_sparse_backward_aux: more than 65535 rows need out_ld = inter rounded to 8");

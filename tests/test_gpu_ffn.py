@@ -378,6 +378,36 @@ def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
         assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
 
 
+@pytest.mark.parametrize("mode", ["moc", "moc_gcp"])
+@pytest.mark.parametrize("shape", [(8192, 768, 2048, 384), (4096, 512, 1024, 256)])
+def test_native_layer_grouped_weight_grads(mode, shape, monkeypatch):
+    """Where the stacked [dWg | dWu] and dWd both split K (the 130m layer),
+    the one-call backward runs them as one grouped launch with fewer K splits
+    each and gZ in gU's rows: out and dX equal the per-kernel path's bit for
+    bit (same gZ, same gG | gU), the weight gradients differ only by the
+    order of their f32 partial sums (at most a bf16 rounding step), and all
+    match the oracle."""
+    from moc_amd import ffn
+    rows, d, inter, k = shape
+    x, wg, wu, wd, go = make_inputs(rows, d, inter, torch.bfloat16, seed=rows + inter)
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", True)
+    a = run_module(mode, x, wg, wu, wd, go, k)
+    monkeypatch.setattr(ffn, "USE_NATIVE_LAYER", False)
+    b = run_module(mode, x, wg, wu, wd, go, k)
+    for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, b):
+        if name in ("out", "dx"):
+            assert torch.equal(p, q), f"{mode} {shape}: {name} differs"
+        else:
+            # one bf16 step of the value, or a sliver of the tensor's scale
+            # where partial sums cancel
+            pf, qf = p.float(), q.float()
+            step = qf.abs() * 2.0 ** -7 + 1e-5 * qf.abs().max()
+            assert bool(((pf - qf).abs() <= step).all()), f"{mode} {shape}: {name} beyond one bf16 step"
+    ref = oracle_pass(x, wg, wu, wd, go, k, "moc_gcp", mode == "moc_gcp")
+    for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, ref):
+        close(p, q, 2e-2, 2e-2, name)
+
+
 @pytest.mark.parametrize("mode", ["moc", "moc_gcp", "moc_2_8", "moc_post_silu_abs"])
 @pytest.mark.parametrize("shape", [(512, 512, 1376, 256), (300, 132, 404, 100), (2, 64, 100, 1),
                                    (3, 128, 132, 132)])

@@ -1194,6 +1194,39 @@ def test_after_gate_one_token_shapes(hidden, inter, k):
     assert torch.equal(yr, res + y)
 
 
+@pytest.mark.parametrize("rows,inter,k,gcp", [(1024, 2048, 384, True), (300, 132, 100, False)])
+def test_backward_aux_in_place_matches(rows, inter, k, gcp):
+    """gZ in dL/dU's own rows (the layer backward's grouped weight-gradient
+    order, [gG | gU] stacked at one pitch): the aux kernel reads each row
+    whole before writing it, so dL/dG and dL/dU equal, bit for bit, the
+    ones computed from a separate gZ buffer."""
+    from moc_amd import _native as N
+    g = gen(960 + rows)
+    scores = torch.randn(rows, inter, generator=g).to(torch.bfloat16).to(DEV)
+    _, idx, _ = K().topk_rows(scores, k, idx_dtype=torch.int16, want_vals=False)
+    gs = (torch.randn(rows, k, generator=g) * 4).to(torch.bfloat16).to(DEV)
+    us = torch.randn(rows, k, generator=g).to(torch.bfloat16).to(DEV)
+    ss = None if gcp else torch.randn(rows, k, generator=g).to(torch.bfloat16).to(DEV)
+    gz = K().padded_empty(rows, inter, torch.bfloat16, DEV)
+    gz.copy_(torch.randn(rows, inter, generator=g).to(torch.bfloat16))
+    ref_g, ref_u, _ = K().sparse_backward_aux(idx, gs, us, ss, gz, inter, stacked=True)
+    pitch = K().row_pitch(inter, torch.bfloat16)
+    buf = torch.full((rows, 2 * pitch), float("nan"), dtype=torch.bfloat16, device=DEV)
+    buf[:, pitch:pitch + inter].copy_(gz)
+    gg, gu = buf[:, :inter], buf[:, pitch:pitch + inter]
+    N.call("moc_sparse_backward_aux", N.dtype_code(torch.bfloat16), idx.data_ptr(), N.idx_code(idx.dtype),
+           gs.data_ptr(), us.data_ptr(), N.ptr(ss), gu.data_ptr(), 2 * pitch, rows, k, inter,
+           gg.data_ptr(), gu.data_ptr(), 2 * pitch, N.stream_of(gs))
+    torch.cuda.synchronize()
+    assert torch.equal(gg.view(torch.int16), ref_g.view(torch.int16))
+    assert torch.equal(gu.view(torch.int16), ref_u.view(torch.int16))
+    # another pitch for gZ than for the outputs is refused
+    with pytest.raises(ValueError, match="gz_full may only be grad_u"):
+        N.call("moc_sparse_backward_aux", N.dtype_code(torch.bfloat16), idx.data_ptr(), N.idx_code(idx.dtype),
+               gs.data_ptr(), us.data_ptr(), N.ptr(ss), gu.data_ptr(), pitch, rows, k, inter,
+               gg.data_ptr(), gu.data_ptr(), 2 * pitch, N.stream_of(gs))
+
+
 @pytest.mark.parametrize("rows,inter,k", [(4096, 5461, 1024), (300, 132, 100)])
 def test_backward_aux_recomputed_s_matches_gcp_recompute(rows, inter, k):
     """The GCP backward keeps no S: the aux kernel recomputes it from g_s.
