@@ -262,11 +262,13 @@ int64_t moc_ffn_backward_workspace_size(int64_t rows, int64_t d, int64_t inter, 
  * recomputes S from g_s, the same bits), else Z is scattered from z_s; dWd =
  * go^T Z, gZ = go W_down (into zbuf after Z), gG and gU dense from gZ, dWg =
  * gG^T x, dWu = gU^T x (stacked: one GEMM over [gG | gU], gu = gg + ld_ggu/2
- * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Where the stacked
- * weight gradients and dWd both split K, they run as one grouped launch
- * after the other steps (fewer K splits each, one reduction): gZ then goes
- * into gu's rows and zbuf keeps Z.  Weight gradients in grad_dtype
- * (MOC_BF16 or MOC_F32), dX in bf16. */
+ * and dwu = dwg + ld_ggu/2 rows), dX = gG Wg + gU Wu.  Stacked with ld_ggu
+ * and ldz at most 8192: gZ goes into gu's rows, one pass turns them into
+ * gG | gU in place and writes Z into zbuf (no scatter launch; with s_tmp
+ * set in GCP mode the scatter runs to fill it), and the weight gradients
+ * run after it, dWd beside [dWg | dWu] as one grouped launch where both
+ * split K (fewer K splits each, one reduction).  Weight gradients in
+ * grad_dtype (MOC_BF16 or MOC_F32), dX in bf16. */
 int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int64_t k, const void* go, int64_t ldgo,
                           const void* x, int64_t ldx, const void* idx, int idx_dtype, const void* g_s,
                           const void* u_s, const void* s_s, const void* z_s, const void* wg, int64_t ldwg,

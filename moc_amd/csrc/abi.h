@@ -64,6 +64,15 @@ int gemm_split_pair(int64_t M1, int64_t N1, int64_t K1, const void* A1, int64_t 
                     int64_t b2_sn, void* C2, int64_t ldc2, int c_dtype, void* workspace, int64_t workspace_bytes,
                     hipStream_t st);
 
+// moc_sparse_backward_aux in its bf16 row form that also writes the dense Z
+// rows (z_full, pitch z_ld): z = bf16(S u) from the recomputed S when
+// z_sparse is NULL (GCP), else the saved z_sparse scattered (sparse_aux.hip).
+// Returns 1 without launching where the row form does not apply.
+int sparse_backward_aux_z(const void* idx, int idx_dtype, const void* g_sparse, const void* u_sparse,
+                          const void* s_sparse, const void* z_sparse, const void* gz_full, int64_t gz_ld,
+                          int64_t rows, int64_t k, int64_t inter, void* grad_g, void* grad_u, int64_t out_ld,
+                          void* z_full, int64_t z_ld, hipStream_t st);
+
 }  // namespace moc
 
 #define MOC_REQUIRE(cond, ...)        \

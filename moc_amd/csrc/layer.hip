@@ -164,35 +164,44 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
   const int64_t need = moc_ffn_backward_workspace_size(rows, d, inter, ld_ggu, stacked);
   MOC_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr),
               "moc_ffn_backward_bf16: workspace of %lld bytes required", (long long)need);
-  // Stacked weight gradients of split-K size run beside dWd as one grouped
-  // launch (one reduction), so Z must outlive gZ: gZ then goes into gU's
-  // rows and the aux kernel turns them into gG | gU in place.
-  const int64_t pair_ws = stacked ? moc::gemm_split_pair_workspace(2 * pitch, d, rows, d, inter, rows) : 0;
-  const bool grouped = pair_ws > 0 && workspace_bytes >= pair_ws && moc::aligned16(workspace) &&
-                       ld_ggu <= 8192 && moc::aligned16(gu);
+  // Stacked layout within the row kernels' limits: gZ goes into gU's rows,
+  // the gradient pass turns them into gG | gU in place and writes the dense
+  // Z as well (no scatter launch), so Z outlives gZ and the weight gradients
+  // run last, dWd beside [dWg | dWu] as one grouped split-K launch where
+  // both split K.
+  const bool late = stacked && ld_ggu <= 8192 && ldz <= 8192 && moc::aligned16(gu);
+  hipStream_t st = moc::as_stream(stream);
   int rc;
-  const void* s_use = s_s;
-  if (s_s == nullptr) {
-    // GCP: S = SiLU(G M), Z = S U M recomputed, Z scattered dense (:435-442)
-    rc = moc_gcp_recompute_scatter(MOC_BF16, g_s, u_s, idx, idx_dtype, rows, k, inter, s_tmp, zbuf, ldz, stream);
-    s_use = nullptr;  // the aux kernel recomputes S from g_s (the same bits) instead of reading it back
-  } else {
-    rc = moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
-  }
-  if (rc != MOC_OK) return rc;
-  if (grouped) {
-    // gZ = go W_down into gU's rows; gG, gU dense from it (:455-480)
+  if (late) {
+    // gZ = go W_down into gU's rows
     rc = moc_gemm_ws(MOC_BF16, rows, inter, d, go, ldgo, 1, wd, ldwd, 1, 0, nullptr, 0, 0, nullptr, 0, 0, gu,
                      ld_ggu, MOC_BF16, workspace, workspace_bytes, stream);
     if (rc != MOC_OK) return rc;
-    rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_use, gu, ld_ggu, rows, k, inter, gg, gu,
-                                 ld_ggu, stream);
+    // gG, gU dense (:455-480) and Z (GCP: S, Z recomputed, :435-437)
+    rc = 1;
+    if (s_s != nullptr || s_tmp == nullptr) {
+      rc = moc::sparse_backward_aux_z(idx, idx_dtype, g_s, u_s, s_s, s_s != nullptr ? z_s : nullptr, gu, ld_ggu,
+                                      rows, k, inter, gg, gu, ld_ggu, zbuf, ldz, st);
+      if (rc < 0) return rc;
+    }
+    if (rc == 1) {  // S wanted in s_tmp, or no fused form: the scatter, then gG | gU in place
+      rc = s_s == nullptr
+               ? moc_gcp_recompute_scatter(MOC_BF16, g_s, u_s, idx, idx_dtype, rows, k, inter, s_tmp, zbuf, ldz,
+                                           stream)
+               : moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
+      if (rc != MOC_OK) return rc;
+      rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_s, gu, ld_ggu, rows, k, inter, gg, gu,
+                                   ld_ggu, stream);
+    }
     if (rc != MOC_OK) return rc;
-    // [dWg | dWu] = [gG | gU]^T x and dWd = go^T Z (:483-490, :447) in one launch
-    rc = moc::gemm_split_pair(2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, dwg, ld_dw, d, inter, rows, go, 1,
-                              ldgo, zbuf, ldz, 1, dwd, lddwd, grad_dtype, workspace, workspace_bytes,
-                              moc::as_stream(stream));
-    if (rc == 1) {  // not taken after all: the two products apart
+    // [dWg | dWu] = [gG | gU]^T x (:483-490) and dWd = go^T Z (:447): one
+    // grouped launch where the plan takes them, else two
+    const int64_t pair_ws = moc::gemm_split_pair_workspace(2 * pitch, d, rows, d, inter, rows);
+    rc = 1;
+    if (pair_ws > 0 && workspace_bytes >= pair_ws)
+      rc = moc::gemm_split_pair(2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, dwg, ld_dw, d, inter, rows, go, 1,
+                                ldgo, zbuf, ldz, 1, dwd, lddwd, grad_dtype, workspace, workspace_bytes, st);
+    if (rc == 1) {
       rc = moc_gemm_ws(MOC_BF16, 2 * pitch, d, rows, gg, 1, ld_ggu, x, ldx, 1, 0, nullptr, 0, 0, nullptr, 0, 0,
                        dwg, ld_dw, grad_dtype, workspace, workspace_bytes, stream);
       if (rc == MOC_OK)
@@ -204,6 +213,13 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
     return moc_gemm_ws(MOC_BF16, rows, d, inter, gg, ld_ggu, 1, wg, ldwg, 1, inter, gu, ld_ggu, 1, wu, ldwu, 1,
                        dx, lddx, MOC_BF16, workspace, workspace_bytes, stream);
   }
+  if (s_s == nullptr) {
+    // GCP: S = SiLU(G M), Z = S U M recomputed, Z scattered dense (:435-442)
+    rc = moc_gcp_recompute_scatter(MOC_BF16, g_s, u_s, idx, idx_dtype, rows, k, inter, s_tmp, zbuf, ldz, stream);
+  } else {
+    rc = moc_scatter_sparse_to_dense(MOC_BF16, z_s, idx, idx_dtype, rows, k, inter, zbuf, ldz, stream);
+  }
+  if (rc != MOC_OK) return rc;
   // dWd = go^T Z
   rc = moc_gemm_ws(MOC_BF16, d, inter, rows, go, 1, ldgo, zbuf, ldz, 1, 0, nullptr, 0, 0, nullptr, 0, 0, dwd,
                    lddwd, grad_dtype, workspace, workspace_bytes, stream);
@@ -212,8 +228,9 @@ extern "C" int moc_ffn_backward_bf16(int64_t rows, int64_t d, int64_t inter, int
   rc = moc_gemm_ws(MOC_BF16, rows, inter, d, go, ldgo, 1, wd, ldwd, 1, 0, nullptr, 0, 0, nullptr, 0, 0, zbuf,
                    ldz, MOC_BF16, workspace, workspace_bytes, stream);
   if (rc != MOC_OK) return rc;
-  // gG, gU dense (:455-480)
-  rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_use, zbuf, ldz, rows, k, inter, gg, gu,
+  // gG, gU dense (:455-480); GCP: the kernel recomputes S from g_s (the
+  // same bits as the recompute above)
+  rc = moc_sparse_backward_aux(MOC_BF16, idx, idx_dtype, g_s, u_s, s_s, zbuf, ldz, rows, k, inter, gg, gu,
                                ld_ggu, stream);
   if (rc != MOC_OK) return rc;
   // dWg = gG^T x, dWu = gU^T x (:483-490)

@@ -456,12 +456,18 @@ __global__ __launch_bounds__(kRowThreads) void forward_aux_rows_f32_kernel(
     reinterpret_cast<float4*>(z_full + row * z_ld)[c] = reinterpret_cast<const float4*>(zrow)[c];
 }
 
-template <typename IdxT, bool VEC>
+// ZOUT: the same pass also writes the dense Z rows that the weight gradient
+// dWd = dD^T Z reads (z_full, rows z_ld apart): z = bf16(S u) from the
+// recomputed S (GCP, the bits of gcp_scatter_rows_kernel) or the saved z_s
+// (the bits of the scatter), so no separate scatter launch is needed when
+// dWd runs after this kernel.
+template <typename IdxT, bool VEC, bool ZOUT = false>
 __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
     const IdxT* __restrict__ idx, const uint16_t* __restrict__ g_s,
     const uint16_t* __restrict__ u_s, const uint16_t* __restrict__ s_s,
     const uint16_t* gz_full, int64_t gz_ld, int k, int64_t inter,
-    uint16_t* __restrict__ grad_g, uint16_t* grad_u, int64_t out_ld) {
+    uint16_t* __restrict__ grad_g, uint16_t* grad_u, int64_t out_ld,
+    const uint16_t* __restrict__ z_s = nullptr, uint16_t* __restrict__ z_full = nullptr, int64_t z_ld = 0) {
   extern __shared__ __attribute__((aligned(16))) uint16_t rbuf[];
   // an output row is inter values plus zeros up to a multiple of 8; rows
   // are out_ld apart (out_ld may leave room for another tensor's rows).
@@ -469,29 +475,45 @@ __global__ __launch_bounds__(kRowThreadsBwd) void backward_aux_rows_kernel(
   // staged whole before the barrier that precedes the row's stores.
   const int64_t width = out_row_width(inter, out_ld);
   const int64_t gz_w = out_row_width(inter, gz_ld);
+  const int64_t z_w = ZOUT ? out_row_width(inter, z_ld) : 0;
   uint16_t* gzrow = rbuf;                 // [gz_w]
   uint16_t* ggrow = rbuf + gz_w;          // [width]
   uint16_t* gurow = rbuf + gz_w + width;  // [width]
+  uint16_t* zrow = gurow + width;         // [z_w] (ZOUT)
   const int64_t row = blockIdx.x;
   RowEntries<IdxT, kRowThreadsBwd, VEC> r;
   r.load(idx, g_s, u_s, s_s, row, k, 0);
   row_load<kRowThreadsBwd>(gzrow, gz_full + row * gz_ld, gz_w);
   row_zero<kRowThreadsBwd>(ggrow, width);
   row_zero<kRowThreadsBwd>(gurow, width);
+  if constexpr (ZOUT) row_zero<kRowThreadsBwd>(zrow, z_w);
   __syncthreads();
   for (int e0 = 0; e0 < k; e0 += kRowThreadsBwd * kRowPer) {
     if (e0 > 0) r.load(idx, g_s, u_s, s_s, row, k, e0);
+    uint16_t zv[kRowPer];
+    if constexpr (ZOUT) {
+      if (z_s != nullptr) {
+        if constexpr (VEC) {
+          r.load4(z_s, row * k + r.entry(e0, 0), r.entry(e0, 0) < k, zv);
+        } else {
+#pragma unroll
+          for (int q = 0; q < kRowPer; ++q) zv[q] = r.entry(e0, q) < k ? z_s[row * k + r.entry(e0, q)] : uint16_t(0);
+        }
+      }
+    }
 #pragma unroll
     for (int q = 0; q < kRowPer; ++q) {
       const int64_t ch = r.ch[q];
       if (ch < 0 || ch >= inter) continue;
-      sparse_bwd_entry(bf16_to_f32(r.a[q]), bf16_to_f32(r.b[q]), s_s != nullptr,
-                       bf16_to_f32(r.c[q]), bf16_to_f32(gzrow[ch]), ggrow[ch], gurow[ch]);
+      const float g = bf16_to_f32(r.a[q]), u = bf16_to_f32(r.b[q]);
+      sparse_bwd_entry(g, u, s_s != nullptr, bf16_to_f32(r.c[q]), bf16_to_f32(gzrow[ch]), ggrow[ch], gurow[ch]);
+      if constexpr (ZOUT) zrow[ch] = z_s != nullptr ? zv[q] : to_bf16(rnd(silu_f32(g)) * u);
     }
   }
   __syncthreads();
   row_store<kRowThreadsBwd>(grad_g + row * out_ld, ggrow, width);
   row_store<kRowThreadsBwd>(grad_u + row * out_ld, gurow, width);
+  if constexpr (ZOUT) row_store<kRowThreadsBwd>(z_full + row * z_ld, zrow, z_w);
 }
 
 // Zeros columns [0, width) of rows x ld elements of esz bytes (16-byte
@@ -790,3 +812,45 @@ extern "C" int moc_gcp_recompute_scatter(int dtype, const void* g_sparse, const 
 #undef MOC_GCPS
   return check_launch("gcp_scatter_rows_kernel");
 }
+
+namespace moc {
+
+// moc_sparse_backward_aux (bf16 row form) that also writes the dense Z rows
+// (z_full, pitch z_ld) from the recomputed S (z_sparse NULL: GCP) or from the
+// saved z_sparse: the scatter of Z fused into the gradient pass for a
+// backward that runs dWd after it.  Returns 1 without launching where the
+// row form does not apply.
+int sparse_backward_aux_z(const void* idx, int idx_dtype, const void* g_sparse, const void* u_sparse,
+                          const void* s_sparse, const void* z_sparse, const void* gz_full, int64_t gz_ld,
+                          int64_t rows, int64_t k, int64_t inter, void* grad_g, void* grad_u, int64_t out_ld,
+                          void* z_full, int64_t z_ld, hipStream_t st) {
+  if (!idx_ok(idx_dtype) || rows <= 0 || rows >= (1LL << 31) || k < 1 || inter < k || gz_ld < inter ||
+      out_ld < inter || z_ld < inter)
+    return 1;
+  if (!idx || !g_sparse || !u_sparse || !gz_full || !grad_g || !grad_u || !z_full) return 1;
+  if (gz_full == grad_g || (gz_full == grad_u && gz_ld != out_ld)) return 1;
+  if (!row_form_ok(gz_full, gz_ld) || !row_form_ok(grad_g, out_ld) || !row_form_ok(grad_u, out_ld) ||
+      !row_form_ok(z_full, z_ld))
+    return 1;
+  const size_t lds = static_cast<size_t>(out_row_width(inter, gz_ld) + 2 * out_row_width(inter, out_ld) +
+                                         out_row_width(inter, z_ld)) * 2;
+  if (lds > 64 * 1024) return 1;
+  const bool vec = entries_vec_ok(k, idx_dtype, idx, g_sparse, u_sparse, s_sparse) &&
+                   reinterpret_cast<uintptr_t>(z_sparse) % 8 == 0;
+#define MOC_BWDZ(T)                                                                                        \
+  if (vec)                                                                                                 \
+    backward_aux_rows_kernel<T, true, true><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
+        (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const uint16_t*)s_sparse,    \
+        (const uint16_t*)gz_full, gz_ld, (int)k, inter, (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld,      \
+        (const uint16_t*)z_sparse, (uint16_t*)z_full, z_ld);                                              \
+  else                                                                                                     \
+    backward_aux_rows_kernel<T, false, true><<<dim3(static_cast<unsigned>(rows)), kRowThreadsBwd, lds, st>>>( \
+        (const T*)idx, (const uint16_t*)g_sparse, (const uint16_t*)u_sparse, (const uint16_t*)s_sparse,    \
+        (const uint16_t*)gz_full, gz_ld, (int)k, inter, (uint16_t*)grad_g, (uint16_t*)grad_u, out_ld,      \
+        (const uint16_t*)z_sparse, (uint16_t*)z_full, z_ld)
+  MOC_IDX_DISPATCH(idx_dtype, MOC_BWDZ);
+#undef MOC_BWDZ
+  return check_launch("backward_aux_rows_kernel (with Z)");
+}
+
+}  // namespace moc
