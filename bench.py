@@ -83,6 +83,9 @@ def parse_args():
                         "launches of the headline's timed steps) as markdown")
     p.add_argument("--trace-steps", type=float, default=1.0,
                    help="with --trace-summary: steps the traced run made (per-step columns)")
+    p.add_argument("--trace-by-grid", action="store_true",
+                   help="with --trace-summary: also split every kernel's dispatches by grid size "
+                        "(mean and median duration per kernel and grid, from *kernel_trace.csv)")
     p.add_argument("--trace-headline", action="store_true",
                    help="with --trace-summary: the trace is of `bench.py --skip-extra`; report the "
                         "seven GEMM launches of its timed fwd+bwd steps")
@@ -990,6 +993,24 @@ def gemm_k_sweep() -> dict:
     return res
 
 
+def trace_by_grid(d: str) -> None:
+    """Per (kernel, grid size) of a rocprofv3 kernel trace: dispatches, mean
+    and median duration (one kernel template serving launches of several
+    shapes, told apart by their grids)."""
+    import csv
+    import glob
+    trace = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    runs = {}
+    for r in csv.DictReader(open(trace[0])):
+        grid = int(r.get("Grid_Size_X") or r.get("Grid_Size") or 0)
+        runs.setdefault((r["Kernel_Name"], grid), []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("\n| kernel | grid (threads) | dispatches | mean us | median us |\n|---|---:|---:|---:|---:|")
+    for (name, grid), v in sorted(runs.items(), key=lambda kv: -sum(kv[1])):
+        name = name if len(name) < 100 else name[:97] + "..."
+        print(f"| `{name}` | {grid} | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} |")
+
+
 def trace_summary(d: str, steps: float, headline: bool) -> None:
     """Markdown summary of a rocprofv3 CSV output directory: the kernels by
     total time (from *kernel_stats.csv), and with `headline` the GEMM
@@ -1061,6 +1082,8 @@ def main():
     args = parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary, args.trace_steps, args.trace_headline)
+        if args.trace_by_grid:
+            trace_by_grid(args.trace_summary)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the MoC FFN path has no "
