@@ -379,14 +379,16 @@ def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
 
 
 @pytest.mark.parametrize("mode", ["moc", "moc_gcp"])
-@pytest.mark.parametrize("shape", [(8192, 768, 2048, 384), (4096, 512, 1024, 256)])
-def test_native_layer_grouped_weight_grads(mode, shape, monkeypatch):
+@pytest.mark.parametrize("shape,oracle", [((8192, 768, 2048, 384), True), ((4096, 512, 1024, 256), True),
+                                          ((32768, 512, 1024, 256), False)])
+def test_native_layer_grouped_weight_grads(mode, shape, oracle, monkeypatch):
     """Where the stacked [dWg | dWu] and dWd both split K (the 130m layer),
     the one-call backward runs them as one grouped launch with fewer K splits
-    each and gZ in gU's rows: out and dX equal the per-kernel path's bit for
-    bit (same gZ, same gG | gU), the weight gradients differ only by the
-    order of their f32 partial sums (at most a bf16 rounding step), and all
-    match the oracle."""
+    each and gZ in gU's rows (also at 32768 tokens, where dX's tiles fill
+    the CUs): out and dX equal the per-kernel path's bit for bit (same gZ,
+    same gG | gU), the weight gradients differ only by the order of their
+    f32 partial sums (at most a bf16 rounding step), and all match the
+    oracle where it runs in seconds."""
     from moc_amd import ffn
     rows, d, inter, k = shape
     x, wg, wu, wd, go = make_inputs(rows, d, inter, torch.bfloat16, seed=rows + inter)
@@ -403,6 +405,8 @@ def test_native_layer_grouped_weight_grads(mode, shape, monkeypatch):
             pf, qf = p.float(), q.float()
             step = qf.abs() * 2.0 ** -7 + 1e-5 * qf.abs().max()
             assert bool(((pf - qf).abs() <= step).all()), f"{mode} {shape}: {name} beyond one bf16 step"
+    if not oracle:
+        return
     ref = oracle_pass(x, wg, wu, wd, go, k, "moc_gcp", mode == "moc_gcp")
     for name, p, q in zip(("out", "dx", "dWg", "dWu", "dWd"), a, ref):
         close(p, q, 2e-2, 2e-2, name)
