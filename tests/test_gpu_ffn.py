@@ -380,12 +380,12 @@ def test_native_layer_matches_per_kernel_path(mode, shape, monkeypatch):
 
 @pytest.mark.parametrize("mode", ["moc", "moc_gcp"])
 @pytest.mark.parametrize("shape,oracle", [((8192, 768, 2048, 384), True), ((4096, 512, 1024, 256), True),
-                                          ((32768, 512, 1024, 256), False)])
+                                          ((32768, 512, 1024, 256), False), ((8190, 768, 2048, 384), False)])
 def test_native_layer_grouped_weight_grads(mode, shape, oracle, monkeypatch):
     """Where the stacked [dWg | dWu] and dWd both split K (the 130m layer),
     the one-call backward runs them as one grouped launch with fewer K splits
     each and gZ in gU's rows (also at 32768 tokens, where dX's tiles fill
-    the CUs): out and dX equal the per-kernel path's bit for bit (same gZ,
+    the CUs, and at a token count that ends inside a K tile): out and dX equal the per-kernel path's bit for bit (same gZ,
     same gG | gU), the weight gradients differ only by the order of their
     f32 partial sums (at most a bf16 rounding step), and all match the
     oracle where it runs in seconds."""
