@@ -459,6 +459,36 @@ def test_topk_wide_range_rows_vs_oracle(k):
     assert np.array_equal(idx.cpu().numpy(), O.topk_indices(s, k))
 
 
+@pytest.mark.parametrize("inter,k", [(961, 1), (961, 480), (2048, 384), (2736, 512), (2736, 2736),
+                                     (4096, 100), (4096, 4000)])
+def test_topk_two_wave_bf16_rows_vs_oracle(inter, k):
+    """bf16 rows of 961-4096 channels take two waves per row: the same
+    selection as the oracle on rows spanning ~140 binades (all-negative rows,
+    NaN, inf, a block of equal top keys, signed zeros) and on rows of heavy
+    ties, indices and bit mask."""
+    g = gen(inter + k)
+    rows = 40
+    mag = torch.exp2(torch.rand(rows, inter, generator=g) * 140 - 70)
+    sign = torch.where(torch.rand(rows, inter, generator=g) < 0.3, -1.0, 1.0)
+    s = (sign * mag).to(torch.bfloat16)
+    s[::4] = -s[::4].abs()
+    s[1::6, 17] = float("nan")
+    s[2::6, 33] = float("inf")
+    s[3::6, 40:60] = 2.0 ** 60
+    ties = torch.tensor(np.random.default_rng(inter).choice([0.0, -0.0, 1.0, -2.0, 0.5], size=(8, inter)),
+                        dtype=torch.bfloat16)
+    s = torch.cat([s, ties])
+    vals, idx, mask = K().topk_rows(s.to(DEV), k, want_mask=True)
+    want = O.topk_indices(s, k)
+    assert np.array_equal(idx.cpu().numpy(), want)
+    # the selected entries' raw bits (NaN payloads included)
+    assert np.array_equal(vals.cpu().view(torch.int16).numpy(),
+                          np.take_along_axis(s.view(torch.int16).numpy(), want.astype(np.int64), 1))
+    bits = mask.cpu().numpy().view(np.uint32)
+    m = (bits[:, np.arange(inter) // 32] >> (np.arange(inter) % 32)) & 1
+    assert np.array_equal(m.astype(bool), O.topk_mask(want, inter))
+
+
 def test_topk_heavy_ties_and_index_dtypes():
     vals = torch.tensor(np.random.default_rng(3).choice([0.0, -0.0, 1.0, -2.0, 0.5, float("inf")],
                                                         size=(33, 700)), dtype=torch.float32)
