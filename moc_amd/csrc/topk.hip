@@ -162,10 +162,10 @@ int launch_topk_kernel(const void* scores, int64_t rows, int inter, int64_t ld, 
 
 // One wave per row while a thread's share fits 128 (f32) or 256 (bf16)
 // channels in registers; wider f32 rows, f32 rows of more than 960 channels
-// when there are fewer rows than SIMDs, and bf16 rows of 961-8192 channels
-// use two waves per row (each row's dependent chain halves; the 130m
-// layer's 8192 rows of 2048 also took 1.14 rounds of the wave slots at one
-// wave per row).
+// when there are fewer rows than SIMDs, and bf16 rows of 961-4032 channels
+// use two waves per row, bf16 rows of 4033-8192 channels four (each row's
+// dependent chain shortens; four waves on the 130m and 350m rows of 2048
+// and 2736 measured slower than two).
 template <bool BF16>
 int launch_topk(const void* scores, int64_t rows, int inter, int64_t ld, int k, int transform,
                 void* vals, void* idx, int idx_dtype, uint32_t* mask, int64_t mask_ld,
@@ -193,6 +193,10 @@ int launch_topk(const void* scores, int64_t rows, int inter, int64_t ld, int k, 
     }
   }
   if constexpr (BF16) {
+    if (per1 >= 64 && per1 <= 128) {
+      const int per4 = (inter + 255) / 256;
+      MOC_TOPK_L8(4, per4);
+    }
     if (per1 >= 16 && per1 <= 128) {
       const int per2 = (inter + 127) / 128;
       MOC_TOPK_L8(2, per2);

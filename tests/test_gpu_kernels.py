@@ -462,7 +462,8 @@ def test_topk_wide_range_rows_vs_oracle(k):
 @pytest.mark.parametrize("inter,k", [(961, 1), (961, 480), (2048, 384), (2736, 512), (2736, 2736),
                                      (4096, 100), (4096, 4000), (5461, 1024), (8192, 3000)])
 def test_topk_two_wave_bf16_rows_vs_oracle(inter, k):
-    """bf16 rows of 961-8192 channels take two waves per row: the same
+    """bf16 rows of 961-4032 channels take two waves per row, of 4033-8192
+    four: the same
     selection as the oracle on rows spanning ~140 binades (all-negative rows,
     NaN, inf, a block of equal top keys, signed zeros) and on rows of heavy
     ties, indices and bit mask."""
