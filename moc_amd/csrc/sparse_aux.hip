@@ -162,9 +162,11 @@ __global__ __launch_bounds__(256) void sparse_backward_aux_kernel(
 // tensors are read and written once, coalesced, and need no separate
 // zero-fill launch.  The per-entry arithmetic is the same as above.
 // ---------------------------------------------------------------------------
-// Threads per row: 512 for the backward row (its per-entry bf16 chain is
-// the heaviest), 256 for the others.
-constexpr int kRowThreadsBwd = 512;
+// Threads per row: 256 (the backward row at 512 measured 118.9 against
+// 116-117 us on 16384 rows of 5461 and 33.7 against 26-27 us on 8192 rows of
+// 2048; the other row kernels at 512, 49.6 against 67 us for the GCP
+// recompute + scatter at 16384 x 5461).
+constexpr int kRowThreadsBwd = 256;
 constexpr int kRowThreads = 256;
 constexpr int64_t kRowMaxLd = 8192;  // three staged rows fit the default 64 KB of LDS
 
