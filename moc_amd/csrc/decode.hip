@@ -1459,14 +1459,15 @@ int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm
     rc = gemv_launch(x, hidden, nb, w_gate, hidden, inter, hidden, gs, pitch, w_up, hidden, inter, u, pitch, st);
   }
   if (rc != MOC_OK) return rc;
-  // 32 columns per workgroup for one token (64 workgroups at hidden 2048:
-  // half the W_down^T bytes through each CU, 18.42 -> 18.21 us per layer;
-  // equal at 2 tokens), 64 up to 8 tokens (<= 256 workgroups), 128 beyond
-  // (12-16 tokens: 32.0-32.5 -> 26.5-26.9 us per layer)
+  // 16 columns per workgroup for one token (128 workgroups at hidden 2048:
+  // a quarter of the W_down^T bytes through each CU; 64 columns 18.42, 32
+  // 18.21-18.28, 16 18.11-18.13 us per layer; 32 equal to 64 at 2 tokens),
+  // 64 up to 8 tokens (<= 256 workgroups), 128 beyond (12-16 tokens:
+  // 32.0-32.5 -> 26.5-26.9 us per layer)
   if (g28 && nb == 1)
-    launch_select_down_cw<32, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+    launch_select_down_cw<16, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (!g28 && nb == 1)
-    launch_select_down_cw<32>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+    launch_select_down_cw<16>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (g28 && nb <= 8)
     launch_select_down_cw<64, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (g28)
