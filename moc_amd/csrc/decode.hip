@@ -1461,13 +1461,18 @@ int global_decode_sd(const void* x, int64_t nb, int64_t hidden, const void* norm
   if (rc != MOC_OK) return rc;
   // 16 columns per workgroup for one token (128 workgroups at hidden 2048:
   // a quarter of the W_down^T bytes through each CU; 64 columns 18.42, 32
-  // 18.21-18.28, 16 18.11-18.13 us per layer; 32 equal to 64 at 2 tokens),
-  // 64 up to 8 tokens (<= 256 workgroups), 128 beyond (12-16 tokens:
+  // 18.21-18.28, 16 18.11-18.13 us per layer), 32 for 2-4 tokens (64
+  // against 32: 19.80-19.83 -> 19.65 us at 2, 22.07-22.09 -> 21.98-22.00 at
+  // 4), 64 up to 8 tokens (<= 256 workgroups), 128 beyond (12-16 tokens:
   // 32.0-32.5 -> 26.5-26.9 us per layer)
   if (g28 && nb == 1)
     launch_select_down_cw<16, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (!g28 && nb == 1)
     launch_select_down_cw<16>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+  else if (g28 && nb <= 4)
+    launch_select_down_cw<32, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
+  else if (!g28 && nb <= 4)
+    launch_select_down_cw<32>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (g28 && nb <= 8)
     launch_select_down_cw<64, true>(gs, u, pitch, (int)nb, in, (int)k, hd, w_down_t, ldw_down, y, res, idx_out, st);
   else if (g28)
